@@ -1,0 +1,179 @@
+/*
+ * opendde_amd — C ABI of the MI355X (gfx950) Pairformer pair-stack kernels.
+ *
+ * Plain C: fixed-width integers, raw device pointers, element strides, a HIP
+ * stream handle passed as void*.  No torch types.  The library never
+ * allocates device memory: callers pass a workspace sized by the matching
+ * *_workspace_bytes query.  Every entry point returns 0 on success or a
+ * negative ODDE_E* status, with a message in odde_last_error() (thread
+ * local).  All work is enqueued on the given stream; nothing synchronises.
+ *
+ * Pair tensors are addressed as  p[x][y][c] = base + x*s0 + y*s1 + c
+ * (element strides; the channel stride must be 1).  Every kernel treats its
+ * view as the *starting-node / natural* orientation; the ending-node
+ * (transposed) form is the same call with s0 and s1 swapped for z, the mask
+ * and the output, so no transposed copy of z is ever made.
+ */
+#ifndef OPENDDE_AMD_H
+#define OPENDDE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ODDE_ABI_VERSION 1
+
+/* element types */
+#define ODDE_F32 0
+#define ODDE_BF16 1
+
+/* status codes */
+#define ODDE_OK 0
+#define ODDE_EINVAL -1       /* bad argument (shape, stride, dtype, null) */
+#define ODDE_EUNSUPPORTED -2 /* valid but not implemented (e.g. head_dim != 32) */
+#define ODDE_EWORKSPACE -3   /* workspace too small or misaligned */
+#define ODDE_EHIP -4         /* HIP runtime / launch error */
+
+/* Kernel ids for odde_launch_count / odde_timing_query. */
+#define ODDE_K_TRIATT_PROJ 0
+#define ODDE_K_TRIATT_CORE 1
+#define ODDE_K_TRIATT_OUT 2
+#define ODDE_K_TRIMUL_PROJ 3
+#define ODDE_K_TRIMUL_CONTRACT 4
+#define ODDE_K_TRIMUL_OUT 5
+#define ODDE_K_TRIATT_RELAYOUT 6
+#define ODDE_K_COUNT 7
+
+int odde_abi_version(void);
+const char* odde_last_error(void);
+
+/*
+ * Triangle attention, whole module (starting node over the given view):
+ *   x = LN(z);  tri_bias[h,q,k] = x[q,k] . w_bias[h];  q,k,v,g = x W^T per head
+ *   o[i,q] = softmax_k( q[i,q].k[i,k]/sqrt(D) + inf*(mask[i,k]-1) + tri_bias[q,k] ) v[i,k]
+ *   update[i,q] = W_o( sigmoid(g[i,q]) * o[i,q] )
+ *   out = (add_residual ? z : 0) + update          (out may alias z)
+ * Replaces the reference's TriangleAttention.forward + Attention.forward
+ * (opendde/model/triangular/triangular.py:648-706,
+ *  opendde/model/triangular/layers.py:426-481) on a GPU tensor.
+ * Weights are in compute_dtype, row-major [out][in]; LN params are f32.
+ */
+typedef struct odde_triatt_args {
+  uint32_t struct_size; /* sizeof(odde_triatt_args) */
+  int32_t n;            /* tokens: the view is n x n */
+  int32_t c;            /* channels of z */
+  int32_t heads;        /* H */
+  int32_t head_dim;     /* D (32) */
+  int32_t z_dtype;      /* ODDE_F32 / ODDE_BF16: z, out */
+  int32_t compute_dtype;/* ODDE_F32 / ODDE_BF16: weights, intermediates, MFMA */
+  int32_t add_residual;
+  const void* z;
+  int64_t z_s0, z_s1;
+  const float* mask; /* may be NULL (all ones) */
+  int64_t mask_s0, mask_s1;
+  void* out;
+  int64_t out_s0, out_s1;
+  const float* ln_w;
+  const float* ln_b;
+  const void* w_bias; /* [H][C]  (TriangleAttention.linear)   */
+  const void* w_q;    /* [H*D][C] mha.linear_q                */
+  const void* w_k;
+  const void* w_v;
+  const void* w_g;    /* [H*D][C] mha.linear_g                */
+  const void* w_o;    /* [C][H*D] mha.linear_o                */
+  float inf;          /* 1e9 */
+  float eps;          /* 1e-5 */
+  void* workspace;
+  uint64_t workspace_bytes;
+} odde_triatt_args;
+
+int odde_triatt_workspace_bytes(const odde_triatt_args* args, uint64_t* bytes);
+int odde_triatt_fwd(const odde_triatt_args* args, void* hip_stream);
+
+/*
+ * Triangle attention core only — the slot the reference fills with
+ * cuequivariance_triangular_attn(q, k, v, bias, mask, scale)
+ * (opendde/model/triangular/layers.py:484-494, called at :462-472):
+ *   out[b,i,h,q,:] = softmax_k( scale*q.k + bias[b,h,q,k] + mask_term ) v[b,i,h,k,:]
+ * q, k, v, out: [B][I][H][J][D] with arbitrary element strides (D contiguous);
+ * bias: [B][H][J][J] f32 (the reference passes [B,1,H,J,J]);
+ * mask: [B][I][J] uint8, nonzero = keep; dropped keys get -inf_value
+ * (the reference's torch path uses -1e9, layers.py:472 / triangular.py:677);
+ * mask may be NULL.  dtype is that of q, k, v and out.
+ */
+typedef struct odde_triatt_core_args {
+  uint32_t struct_size;
+  int32_t batch, rows, heads, n, head_dim; /* B, I, H, J, D */
+  int32_t dtype;
+  const void* q; int64_t q_sb, q_si, q_sh, q_sj;
+  const void* k; int64_t k_sb, k_si, k_sh, k_sj;
+  const void* v; int64_t v_sb, v_si, v_sh, v_sj;
+  const float* bias; int64_t b_sb, b_sh, b_sq, b_sk;
+  const uint8_t* mask; int64_t m_sb, m_si, m_sk;
+  void* out; int64_t o_sb, o_si, o_sh, o_sj;
+  float scale;
+  float inf_value; /* 1e9 */
+  void* workspace;
+  uint64_t workspace_bytes;
+} odde_triatt_core_args;
+
+int odde_triatt_core_workspace_bytes(const odde_triatt_core_args* args, uint64_t* bytes);
+int odde_triatt_core_fwd(const odde_triatt_core_args* args, void* hip_stream);
+
+/*
+ * Triangle multiplicative update, whole module:
+ *   x = LN_in(z); a = mask*sigmoid(x Wag^T)*(x Wap^T); b likewise
+ *   outgoing: p[i,j] = sum_k a[i,k]*b[j,k];  incoming: p[i,j] = sum_k a[k,i]*b[k,j]
+ *   update = (LN_out(p) W_z^T) * sigmoid(x W_g^T)
+ *   out = (add_residual ? z : 0) + update          (out may alias z)
+ * Argument list of kernel_triangular_mult
+ * (opendde/model/triangular/triangular.py:17-30, called at :498-515):
+ * p_in_weight = cat(linear_a_p, linear_b_p), g_in_weight = cat(linear_a_g,
+ * linear_b_g), p_out_weight = linear_z, g_out_weight = linear_g.
+ */
+typedef struct odde_trimul_args {
+  uint32_t struct_size;
+  int32_t n;
+  int32_t c;        /* c_z */
+  int32_t c_hidden; /* Ch */
+  int32_t z_dtype;
+  int32_t compute_dtype;
+  int32_t outgoing; /* 1 = outgoing (Alg. 11), 0 = incoming (Alg. 12) */
+  int32_t add_residual;
+  const void* z;
+  int64_t z_s0, z_s1;
+  const float* mask; /* may be NULL */
+  int64_t mask_s0, mask_s1;
+  void* out;
+  int64_t out_s0, out_s1;
+  const float* norm_in_weight;
+  const float* norm_in_bias;
+  const float* norm_out_weight;
+  const float* norm_out_bias;
+  const void* p_in_weight;  /* [2*Ch][C] */
+  const void* g_in_weight;  /* [2*Ch][C] */
+  const void* p_out_weight; /* [C][Ch]   */
+  const void* g_out_weight; /* [C][C]    */
+  float eps;
+  void* workspace;
+  uint64_t workspace_bytes;
+} odde_trimul_args;
+
+int odde_trimul_workspace_bytes(const odde_trimul_args* args, uint64_t* bytes);
+int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
+
+/* Instrumentation (no counterpart in the reference): per-kernel launch
+ * counters (always on), and optional HIP-event timing of every launch on the
+ * stream it runs on.  odde_timing_query synchronises on the recorded events. */
+int64_t odde_launch_count(int kernel_id);
+int odde_timing_enable(int on);
+int odde_timing_reset(void);
+int odde_timing_query(int kernel_id, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OPENDDE_AMD_H */

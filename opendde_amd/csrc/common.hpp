@@ -1,0 +1,196 @@
+// Shared device helpers for the gfx950 (CDNA4) pair-stack kernels.
+//
+// Everything here is built around one MFMA tile: the 16x16 output block with
+// a 32-deep contraction ("K32 fragment").  Lane l of a wave64 holds
+//   * for an A operand: row (l % 16), eight contraction slots of group l / 16;
+//   * for a B operand: column (l % 16), the same eight slots of group l / 16;
+//   * for the f32x4 accumulator: column (l % 16), rows 4 * (l / 16) + r.
+// Only the row/column ownership and the accumulator layout are relied upon:
+// A and B always use the same slot -> contraction-index map, so the order in
+// which the hardware walks the 32 slots does not matter.
+//
+// bf16 fragments feed v_mfma_f32_16x16x32_bf16 (one instruction); f32
+// fragments feed eight v_mfma_f32_16x16x4_f32 (slot e of every group in
+// instruction e), giving true fp32 products for the fp32 tier.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace odde {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ----------------------------------------------------------------------------
+// scalar conversions
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// ----------------------------------------------------------------------------
+// K32 fragments
+// ----------------------------------------------------------------------------
+template <typename CT> struct Frag;
+
+template <> struct Frag<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void zero() {
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)0.0f;
+  }
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void set(int e, float x) { v[e] = (bf16)x; }
+  __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
+};
+
+template <> struct Frag<float> {
+  f32x4 lo, hi;
+  __device__ __forceinline__ void zero() {
+    lo = f32x4{0.f, 0.f, 0.f, 0.f};
+    hi = lo;
+  }
+  __device__ __forceinline__ void load(const float* p) {
+    lo = *reinterpret_cast<const f32x4*>(p);
+    hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ void set(int e, float x) {
+    if (e < 4) lo[e] = x; else hi[e - 4] = x;
+  }
+  __device__ __forceinline__ float get(int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
+};
+
+// acc += A * B over one 32-deep slot set.
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[0], b.lo[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[1], b.lo[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[2], b.lo[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[3], b.lo[3], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[0], b.hi[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[1], b.hi[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[2], b.hi[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[3], b.hi[3], acc, 0, 0, 0);
+}
+
+// ----------------------------------------------------------------------------
+// small vector stores of 4 consecutive elements
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+  bf16x4 v;
+  v[0] = (bf16)a; v[1] = (bf16)b; v[2] = (bf16)c; v[3] = (bf16)d;
+  *reinterpret_cast<bf16x4*>(p) = v;
+}
+__device__ __forceinline__ void load4(const float* p, float* o) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(p);
+  o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
+}
+__device__ __forceinline__ void load4(const bf16* p, float* o) {
+  bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  o[0] = (float)v[0]; o[1] = (float)v[1]; o[2] = (float)v[2]; o[3] = (float)v[3];
+}
+
+// 8 contiguous elements -> float
+__device__ __forceinline__ void load8(const float* p, float* o) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  for (int e = 0; e < 4; ++e) { o[e] = a[e]; o[e + 4] = b[e]; }
+}
+__device__ __forceinline__ void load8(const bf16* p, float* o) {
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+  for (int e = 0; e < 8; ++e) o[e] = (float)v[e];
+}
+
+// ----------------------------------------------------------------------------
+// cross-lane reductions inside a wave64 over the four 16-lane groups
+// (lanes l, l^16, l^32, l^48 hold the same row / column).
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float xor_shfl(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+__device__ __forceinline__ float group_sum(float v) {
+  v += xor_shfl(v, 16);
+  v += xor_shfl(v, 32);
+  return v;
+}
+__device__ __forceinline__ float group_max(float v) {
+  v = fmaxf(v, xor_shfl(v, 16));
+  v = fmaxf(v, xor_shfl(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// ----------------------------------------------------------------------------
+// Row loader with fused LayerNorm: a wave owns 16 rows of C channels and ends
+// with the normalised rows as K32 fragments (kC = C / 32 of them): lane l
+// holds row (l % 16), channels 32 s + 8 (l / 16) + e.  Statistics are fp32,
+// two-pass (mean, then centred second moment), eps as given.  Rows flagged
+// invalid produce zero fragments.
+// ----------------------------------------------------------------------------
+template <typename ZT, typename CT, int C>
+__device__ __forceinline__ void ln_rows_to_frags(const ZT* row_ptr, bool valid,
+                                                 const float* __restrict__ ln_w,
+                                                 const float* __restrict__ ln_b, float eps,
+                                                 Frag<CT> (&frag)[C / 32]) {
+  constexpr int kC = C / 32;
+  const int g = lane_id() >> 4;
+  float x[kC][8];
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    if (valid) {
+      load8(row_ptr + 32 * t + 8 * g, x[t]);
+    } else {
+      for (int e = 0; e < 8; ++e) x[t][e] = 0.f;
+    }
+    for (int e = 0; e < 8; ++e) s += x[t][e];
+  }
+  const float mean = group_sum(s) * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int t = 0; t < kC; ++t)
+    for (int e = 0; e < 8; ++e) {
+      const float d = x[t][e] - mean;
+      q += d * d;
+    }
+  const float rstd = rsqrtf(group_sum(q) * (1.0f / C) + eps);
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    float w[8], b[8];
+    load8(ln_w + 32 * t + 8 * g, w);
+    load8(ln_b + 32 * t + 8 * g, b);
+    for (int e = 0; e < 8; ++e) {
+      const float y = valid ? (x[t][e] - mean) * rstd * w[e] + b[e] : 0.f;
+      frag[t].set(e, y);
+    }
+  }
+}
+
+// Load a K32 fragment of a weight matrix W[out][K] (row-major, K contiguous):
+// lane l takes output row (o0 + l % 16) and contraction slots 32 t + 8 g.
+// Rows at or beyond n_out read as zero.
+template <typename CT>
+__device__ __forceinline__ void load_w_frag(const CT* __restrict__ w, int ld, int o0, int n_out,
+                                            int t, Frag<CT>& f) {
+  const int o = o0 + (lane_id() & 15);
+  const int g = lane_id() >> 4;
+  if (o < n_out) f.load(w + (size_t)o * ld + 32 * t + 8 * g);
+  else f.zero();
+}
+
+}  // namespace odde

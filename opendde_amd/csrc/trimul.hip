@@ -1,0 +1,429 @@
+// Triangle multiplicative update (outgoing / incoming) for gfx950.
+//
+// Three kernels, stream ordered:
+//   1. trimul_proj     — LN_in + the four gated projections per pair row,
+//                        a = mask*sigmoid(x Wag^T)*(x Wap^T) (b likewise),
+//                        written channel-major as A[c][x][k], B[c][y][k] so
+//                        that the contraction is one NT GEMM per channel.
+//                        Incoming reads z through swapped strides, which
+//                        writes a[k,i] at A[c][i][k]: no transposed copy.
+//   2. trimul_contract — P[c][x][y] = sum_k A[c][x][k] B[c][y][k]: a batched
+//                        NT GEMM on MFMA, 128x128 tiles, LDS-staged K blocks,
+//                        XCD-aware tile order (all tiles of one channel on
+//                        one XCD so A_c and B_c stay in that XCD's L2).
+//   3. trimul_out      — per pair row: LN_out over the channel-major P
+//                        (transposed through LDS), W_z, times
+//                        sigmoid(W_g LN_in(z)) recomputed from z (which is
+//                        read for the residual anyway), plus the residual.
+//
+// Workspace (CT = compute type, Np = N rounded up to 128):
+//   A, B, P : [Ch][Np][Np]
+#include "common.hpp"
+#include "runtime.hpp"
+
+namespace odde {
+
+// ---------------------------------------------------------------------------
+// 1. projection
+// ---------------------------------------------------------------------------
+template <typename ZT, typename CT>
+struct TrimulProjArgs {
+  const ZT* z;
+  int64_t z_s0, z_s1;
+  const float* mask;
+  int64_t m_s0, m_s1;
+  const float* ln_w;
+  const float* ln_b;
+  const CT* wp;  // [2Ch][C]  a_p rows then b_p rows
+  const CT* wg;  // [2Ch][C]  a_g rows then b_g rows
+  CT* A;
+  CT* B;
+  int n, np, ch;
+  float eps;
+};
+
+template <typename ZT, typename CT, int kC>
+__global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
+  constexpr int C = kC * 32;
+  const int x_ = blockIdx.y;  // first index of the (strided) view
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int y0 = blockIdx.x * 64 + w * 16;
+  const int yl = y0 + r16;
+  const bool valid = x_ < a.n && yl < a.n;
+  const ZT* rowp = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
+  Frag<CT> xf[kC];
+  ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xf);
+
+  // mask for the four rows y0+4g .. +3 this lane writes
+  const int yb = y0 + 4 * g;
+  float mk[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int y = yb + r;
+    mk[r] = (x_ < a.n && y < a.n)
+                ? (a.mask ? a.mask[(int64_t)x_ * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
+                : 0.f;
+  }
+  const int ch = a.ch, np = a.np;
+  for (int cb = 0; cb < ch / 16; ++cb) {
+    f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap, bp = ap, bg = ap;
+#pragma unroll
+    for (int t = 0; t < kC; ++t) {
+      Frag<CT> f;
+      load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
+      mma(ap, xf[t], f);
+      load_w_frag(a.wg, C, cb * 16, 2 * ch, t, f);
+      mma(ag, xf[t], f);
+      load_w_frag(a.wp, C, ch + cb * 16, 2 * ch, t, f);
+      mma(bp, xf[t], f);
+      load_w_frag(a.wg, C, ch + cb * 16, 2 * ch, t, f);
+      mma(bg, xf[t], f);
+    }
+    const int c = cb * 16 + r16;
+    const size_t off = ((size_t)c * np + x_) * np + yb;
+    float va[4], vb[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      va[r] = mk[r] * sigmoidf_(ag[r]) * ap[r];
+      vb[r] = mk[r] * sigmoidf_(bg[r]) * bp[r];
+    }
+    store4(a.A + off, va[0], va[1], va[2], va[3]);
+    store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. contraction: batched NT GEMM, P_c = A_c B_c^T
+// ---------------------------------------------------------------------------
+template <typename CT>
+struct ContractArgs {
+  const CT* A;
+  const CT* B;
+  CT* P;
+  int np, ch;
+};
+
+template <typename CT> struct ContractCfg;
+template <> struct ContractCfg<bf16> { static constexpr int BK = 64; static constexpr int PAD = 8; };
+template <> struct ContractCfg<float> { static constexpr int BK = 32; static constexpr int PAD = 4; };
+
+template <typename CT>
+__global__ __launch_bounds__(256) void trimul_contract_kernel(ContractArgs<CT> a) {
+  constexpr int BK = ContractCfg<CT>::BK;
+  constexpr int LD = BK + ContractCfg<CT>::PAD;
+  constexpr int VEC = 16 / sizeof(CT);            // elements per 16-byte chunk
+  constexpr int CHUNKS = 128 * BK / VEC;          // chunks per operand tile
+  __shared__ __attribute__((aligned(16))) CT As[128 * LD];
+  __shared__ __attribute__((aligned(16))) CT Bs[128 * LD];
+
+  const int T = a.np / 128;
+  const int tiles = T * T;
+  // XCD-aware order: workgroup ids are dealt round-robin over 8 XCDs; give
+  // every tile of one channel to the same XCD when the channel count allows.
+  int bid = blockIdx.x, c, tile;
+  if ((a.ch & 7) == 0) {
+    const int xcd = bid & 7, local = bid >> 3;
+    c = (local / tiles) * 8 + xcd;
+    tile = local % tiles;
+  } else {
+    c = bid / tiles;
+    tile = bid % tiles;
+  }
+  const int x0 = (tile / T) * 128, y0 = (tile % T) * 128;
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wm = w >> 1, wn = w & 1;
+  const size_t plane = (size_t)a.np * a.np;
+  const CT* Ab = a.A + c * plane + (size_t)x0 * a.np;
+  const CT* Bb = a.B + c * plane + (size_t)y0 * a.np;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < a.np; k0 += BK) {
+#pragma unroll
+    for (int it = 0; it < CHUNKS / 256; ++it) {
+      const int ci = threadIdx.x + it * 256;
+      const int r = ci / (BK / VEC), cc = (ci % (BK / VEC)) * VEC;
+      *reinterpret_cast<f32x4*>(&As[r * LD + cc]) =
+          *reinterpret_cast<const f32x4*>(Ab + (size_t)r * a.np + k0 + cc);
+      *reinterpret_cast<f32x4*>(&Bs[r * LD + cc]) =
+          *reinterpret_cast<const f32x4*>(Bb + (size_t)r * a.np + k0 + cc);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+      Frag<CT> af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        af[i].load(&As[(wm * 64 + i * 16 + r16) * LD + kk + 8 * g]);
+        bfr[i].load(&Bs[(wn * 64 + i * 16 + r16) * LD + kk + 8 * g]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], bfr[j], af[i]);
+    }
+    __syncthreads();
+  }
+  // acc[i][j]: column = row x (x0 + 64wm + 16i + r16), rows y = y0 + 64wn + 16j + 4g + r
+  CT* Pb = a.P + c * plane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int xx = x0 + wm * 64 + i * 16 + r16;
+      const int yy = y0 + wn * 64 + j * 16 + 4 * g;
+      store4(Pb + (size_t)xx * a.np + yy, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 3. LN_out + W_z, gate, residual
+// ---------------------------------------------------------------------------
+template <typename ZT, typename CT>
+struct TrimulOutArgs {
+  const CT* P;  // [Ch][Np][Np]
+  const ZT* z;
+  int64_t z_s0, z_s1;
+  ZT* out;
+  int64_t o_s0, o_s1;
+  const float* ln_in_w;
+  const float* ln_in_b;
+  const float* ln_out_w;
+  const float* ln_out_b;
+  const CT* wz;  // [C][Ch]
+  const CT* wg;  // [C][C]
+  int n, np, c;
+  int add;
+  float eps;
+};
+
+template <typename ZT, typename CT, int kC, int kCh>
+__global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a) {
+  constexpr int C = kC * 32, CH = kCh * 32;
+  constexpr int LD = CH + 16 / sizeof(CT);   // row stride of the transposed tile
+  __shared__ __attribute__((aligned(16))) CT pt[64 * LD];
+
+  const int x_ = blockIdx.y;
+  const int y0 = blockIdx.x * 64;
+  // stage P[:, x_, y0:y0+64] transposed to pt[y][c]
+  {
+    constexpr int VEC = 16 / sizeof(CT);
+    constexpr int PER_C = 64 / VEC;              // 16-byte chunks per channel row
+    const CT* src = a.P + (size_t)x_ * a.np + y0;
+    for (int ci = threadIdx.x; ci < CH * PER_C; ci += 256) {
+      const int c = ci / PER_C, yy = (ci % PER_C) * VEC;
+      CT v[VEC];
+      *reinterpret_cast<f32x4*>(v) =
+          *reinterpret_cast<const f32x4*>(src + (size_t)c * a.np * a.np + yy);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) pt[(yy + e) * LD + c] = v[e];
+    }
+  }
+  __syncthreads();
+
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int yl = y0 + w * 16 + r16;
+  const bool valid = x_ < a.n && yl < a.n;
+  Frag<CT> xp[kCh], xz[kC];
+  ln_rows_to_frags<CT, CT, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b, a.eps, xp);
+  const ZT* zrow = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
+  ln_rows_to_frags<ZT, CT, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, xz);
+
+  for (int cb = 0; cb < C / 16; ++cb) {
+    f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
+#pragma unroll
+    for (int t = 0; t < kCh; ++t) {
+      Frag<CT> f;
+      load_w_frag(a.wz, CH, cb * 16, C, t, f);
+      mma(ay, f, xp[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < kC; ++t) {
+      Frag<CT> f;
+      load_w_frag(a.wg, C, cb * 16, C, t, f);
+      mma(agt, f, xz[t]);
+    }
+    if (!valid) continue;
+    const int c0 = cb * 16 + 4 * g;
+    float base[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.add) load4(zrow + c0, base);
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[e] * sigmoidf_(agt[e]);
+    store4(a.out + (int64_t)x_ * a.o_s0 + (int64_t)yl * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+  }
+}
+
+}  // namespace odde
+
+// ===========================================================================
+// host side
+// ===========================================================================
+using namespace odde;
+
+namespace {
+
+struct TrimulWs { void* A; void* B; void* P; uint64_t bytes; };
+
+TrimulWs carve_trimul(void* base, uint64_t size, int n, int ch, int dt) {
+  const int np = round_up(n, 128);
+  const uint64_t plane = (uint64_t)ch * np * np * dtype_size(dt);
+  Carver c(base, size);
+  TrimulWs w;
+  w.A = c.take<char>(plane);
+  w.B = c.take<char>(plane);
+  w.P = c.take<char>(plane);
+  w.bytes = (c.used + 255) & ~uint64_t(255);
+  return w;
+}
+
+int kdim(int c) {
+  switch (c) {
+    case 64: return 2;
+    case 128: return 4;
+    case 256: return 8;
+    case 384: return 12;
+    default: return 0;
+  }
+}
+
+int check_trimul(const odde_trimul_args* a) {
+  if (!a) return set_error(ODDE_EINVAL, "trimul: null args");
+  if (a->struct_size != sizeof(odde_trimul_args))
+    return set_error(ODDE_EINVAL, "trimul: struct_size mismatch (ABI version skew)");
+  if (a->n <= 0 || a->c <= 0 || a->c_hidden <= 0)
+    return set_error(ODDE_EINVAL, "trimul: n, c and c_hidden must be positive");
+  if (!kdim(a->c) || !kdim(a->c_hidden))
+    return set_error(ODDE_EUNSUPPORTED, "trimul: c and c_hidden must be 64, 128, 256 or 384");
+  if (!valid_dtype(a->z_dtype) || !valid_dtype(a->compute_dtype))
+    return set_error(ODDE_EINVAL, "trimul: bad dtype");
+  if (a->z_dtype == ODDE_BF16 && a->compute_dtype == ODDE_F32)
+    return set_error(ODDE_EUNSUPPORTED, "trimul: bf16 storage with f32 compute");
+  return ODDE_OK;
+}
+
+template <typename ZT, typename CT, int kC>
+void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
+  dim3 grid(p.np / 64, p.np);
+  hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
+}
+
+template <typename ZT, typename CT, int kC, int kCh>
+void launch_to(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
+  dim3 grid(p.np / 64, p.n);
+  hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh>), grid, dim3(256), 0, st, p);
+}
+
+template <typename ZT, typename CT, int kC>
+bool dispatch_to(const TrimulOutArgs<ZT, CT>& p, int ch, hipStream_t st) {
+  switch (ch) {
+    case 64: launch_to<ZT, CT, kC, 2>(p, st); return true;
+    case 128: launch_to<ZT, CT, kC, 4>(p, st); return true;
+    case 256: launch_to<ZT, CT, kC, 8>(p, st); return true;
+    case 384: launch_to<ZT, CT, kC, 12>(p, st); return true;
+    default: return false;
+  }
+}
+
+template <typename ZT, typename CT>
+int run_trimul(const odde_trimul_args* a, hipStream_t st) {
+  const int n = a->n, C = a->c, ch = a->c_hidden;
+  const int np = round_up(n, 128);
+  TrimulWs ws = carve_trimul(a->workspace, a->workspace_bytes, n, ch, a->compute_dtype);
+  const bool out = a->outgoing != 0;
+
+  TrimulProjArgs<ZT, CT> p;
+  p.z = static_cast<const ZT*>(a->z);
+  // incoming: a[k,i] lands at A[c][i][k] by reading the view transposed
+  p.z_s0 = out ? a->z_s0 : a->z_s1;
+  p.z_s1 = out ? a->z_s1 : a->z_s0;
+  p.mask = a->mask;
+  p.m_s0 = out ? a->mask_s0 : a->mask_s1;
+  p.m_s1 = out ? a->mask_s1 : a->mask_s0;
+  p.ln_w = a->norm_in_weight; p.ln_b = a->norm_in_bias;
+  p.wp = static_cast<const CT*>(a->p_in_weight);
+  p.wg = static_cast<const CT*>(a->g_in_weight);
+  p.A = static_cast<CT*>(ws.A); p.B = static_cast<CT*>(ws.B);
+  p.n = n; p.np = np; p.ch = ch; p.eps = a->eps;
+  {
+    LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
+    switch (C) {
+      case 64: launch_tp<ZT, CT, 2>(p, st); break;
+      case 128: launch_tp<ZT, CT, 4>(p, st); break;
+      case 256: launch_tp<ZT, CT, 8>(p, st); break;
+      case 384: launch_tp<ZT, CT, 12>(p, st); break;
+    }
+    int rc = check_launch("trimul_proj");
+    if (rc) return rc;
+  }
+
+  ContractArgs<CT> k;
+  k.A = p.A; k.B = p.B; k.P = static_cast<CT*>(ws.P); k.np = np; k.ch = ch;
+  {
+    const int tiles = (np / 128) * (np / 128);
+    LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
+    hipLaunchKernelGGL((trimul_contract_kernel<CT>), dim3(tiles * ch), dim3(256), 0, st, k);
+    int rc = check_launch("trimul_contract");
+    if (rc) return rc;
+  }
+
+  TrimulOutArgs<ZT, CT> o;
+  o.P = k.P;
+  o.z = static_cast<const ZT*>(a->z); o.z_s0 = a->z_s0; o.z_s1 = a->z_s1;
+  o.out = static_cast<ZT*>(a->out); o.o_s0 = a->out_s0; o.o_s1 = a->out_s1;
+  o.ln_in_w = a->norm_in_weight; o.ln_in_b = a->norm_in_bias;
+  o.ln_out_w = a->norm_out_weight; o.ln_out_b = a->norm_out_bias;
+  o.wz = static_cast<const CT*>(a->p_out_weight);
+  o.wg = static_cast<const CT*>(a->g_out_weight);
+  o.n = n; o.np = np; o.c = C; o.add = a->add_residual; o.eps = a->eps;
+  {
+    LaunchScope ls(ODDE_K_TRIMUL_OUT, st);
+    bool ok = false;
+    switch (C) {
+      case 64: ok = dispatch_to<ZT, CT, 2>(o, ch, st); break;
+      case 128: ok = dispatch_to<ZT, CT, 4>(o, ch, st); break;
+      case 256: ok = dispatch_to<ZT, CT, 8>(o, ch, st); break;
+      case 384: ok = dispatch_to<ZT, CT, 12>(o, ch, st); break;
+    }
+    if (!ok) return set_error(ODDE_EUNSUPPORTED, "trimul: unsupported c/c_hidden");
+    return check_launch("trimul_out");
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int odde_trimul_workspace_bytes(const odde_trimul_args* a, uint64_t* bytes) {
+  int rc = check_trimul(a);
+  if (rc) return rc;
+  if (!bytes) return set_error(ODDE_EINVAL, "trimul: null bytes");
+  *bytes = carve_trimul(nullptr, 0, a->n, a->c_hidden, a->compute_dtype).bytes;
+  return ODDE_OK;
+}
+
+int odde_trimul_fwd(const odde_trimul_args* a, void* stream) {
+  int rc = check_trimul(a);
+  if (rc) return rc;
+  if (!a->z || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->norm_out_weight ||
+      !a->norm_out_bias || !a->p_in_weight || !a->g_in_weight || !a->p_out_weight ||
+      !a->g_out_weight)
+    return set_error(ODDE_EINVAL, "trimul: null tensor pointer");
+  const uint64_t need = carve_trimul(nullptr, 0, a->n, a->c_hidden, a->compute_dtype).bytes;
+  if (!a->workspace || a->workspace_bytes < need ||
+      (reinterpret_cast<uintptr_t>(a->workspace) & 255))
+    return set_error(ODDE_EWORKSPACE, "trimul: workspace missing, too small or not 256-byte aligned");
+  const int zes = dtype_size(a->z_dtype);
+  if ((reinterpret_cast<uintptr_t>(a->z) | reinterpret_cast<uintptr_t>(a->out)) & 15 ||
+      ((a->z_s0 | a->z_s1 | a->out_s0 | a->out_s1) * zes) & 15)
+    return set_error(ODDE_EINVAL, "trimul: z/out rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) return run_trimul<float, float>(a, st);
+  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_BF16) return run_trimul<float, bf16>(a, st);
+  return run_trimul<bf16, bf16>(a, st);
+}
+
+}  // extern "C"

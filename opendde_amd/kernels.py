@@ -1,0 +1,277 @@
+"""Tensor-level entry points of the HIP backend (thin layer over the C ABI).
+
+PyTorch is used here only as plumbing: it owns device memory (outputs and the
+per-call workspace, via the caching allocator) and names the current stream.
+All arithmetic happens in the gfx950 kernels of ``libopendde_amd.so``.
+There is no fallback in this module: unsupported shapes, non-GPU tensors or a
+missing library raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+SUPPORTED_CHANNELS = (64, 128, 256, 384)
+HEAD_DIM = 32
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return _lib.F32
+    if dt == torch.bfloat16:
+        return _lib.BF16
+    raise TypeError(f"HIP backend supports float32 and bfloat16 tensors, got {dt}")
+
+
+def autocast_compute_dtype(t: torch.Tensor) -> torch.dtype:
+    """Compute precision for a call: the tensor's own dtype, or bf16 when a
+    float32 tensor arrives under CUDA autocast with bf16 (the reference's bf16
+    inference mode keeps the residual stream in float32 and runs the module
+    arithmetic in bf16)."""
+    if t.dtype == torch.bfloat16:
+        return torch.bfloat16
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+        return torch.bfloat16
+    return torch.float32
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("HIP backend tensors must be on a GPU device")
+
+
+def _pair_view_ok(t: torch.Tensor, name: str) -> None:
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be [N, N, C], got {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must have a unit channel stride")
+    if t.shape[0] != t.shape[1]:
+        raise ValueError(f"{name} must be square in its pair dims")
+
+
+# Converted weights are cached per (parameter storage, version, dtype) so the
+# per-call cost is a dictionary lookup once weights are in place.
+_wcache: Dict[Tuple, torch.Tensor] = {}
+
+
+def prepared(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    key = (t.data_ptr(), t._version, tuple(t.shape), t.dtype, dtype, t.device)
+    hit = _wcache.get(key)
+    if hit is None:
+        if len(_wcache) > 4096:
+            _wcache.clear()
+        hit = t.detach().to(dtype).contiguous()
+        _wcache[key] = hit
+    return hit
+
+
+def prepared_cat(ts, dtype: torch.dtype) -> torch.Tensor:
+    key = ("cat",) + tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in ts) + (dtype,)
+    hit = _wcache.get(key)
+    if hit is None:
+        hit = torch.cat([t.detach() for t in ts], 0).to(dtype).contiguous()
+        _wcache[key] = hit
+    return hit
+
+
+def _mask_view(mask: Optional[torch.Tensor], n: int, device) -> Tuple[Optional[torch.Tensor], int, int]:
+    if mask is None:
+        return None, 0, 0
+    if mask.dim() != 2 or tuple(mask.shape) != (n, n):
+        raise ValueError(f"mask must be [N, N] = [{n}, {n}], got {tuple(mask.shape)}")
+    if mask.dtype != torch.float32:
+        mask = mask.float()
+    if mask.device != device:
+        raise ValueError("mask must be on the same device as z")
+    return mask, mask.stride(0), mask.stride(1)
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    # torch's caching allocator returns 256-byte aligned blocks.
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, ln_b,
+                       w_bias, w_q, w_k, w_v, w_g, w_o, heads: int, starting: bool = True,
+                       out: Optional[torch.Tensor] = None, add_residual: bool = False,
+                       compute_dtype: Optional[torch.dtype] = None, inf: float = 1e9,
+                       eps: float = 1e-5) -> torch.Tensor:
+    """Fused triangle attention on one pair tensor z [N, N, C].
+
+    starting=False runs the ending-node form by reading z, the mask and the
+    output through transposed strides (no transposed copies).  With
+    ``add_residual`` the result is z + update, written to ``out`` (which may
+    be z itself for an in-place update); otherwise ``out`` receives the
+    update.  Returns ``out``.
+    """
+    _require_gpu(z, mask)
+    _pair_view_ok(z, "z")
+    n, c = z.shape[0], z.shape[2]
+    if c not in SUPPORTED_CHANNELS or heads * HEAD_DIM not in SUPPORTED_CHANNELS:
+        raise NotImplementedError(
+            f"HIP triangle attention supports c, heads*32 in {SUPPORTED_CHANNELS}; got c={c}, "
+            f"heads={heads}")
+    if w_q.shape[0] != heads * HEAD_DIM:
+        raise NotImplementedError("HIP triangle attention requires a per-head dim of 32")
+    ct = compute_dtype or autocast_compute_dtype(z)
+    if z.dtype == torch.bfloat16 and ct == torch.float32:
+        raise NotImplementedError("bf16 storage with fp32 compute is not provided")
+    if out is None:
+        out = torch.empty_like(z, memory_format=torch.contiguous_format)
+    _pair_view_ok(out, "out")
+    if out.dtype != z.dtype or out.shape != z.shape:
+        raise ValueError("out must match z in shape and dtype")
+    m, ms0, ms1 = _mask_view(mask, n, z.device)
+    zs0, zs1 = z.stride(0), z.stride(1)
+    os0, os1 = out.stride(0), out.stride(1)
+    if not starting:
+        zs0, zs1, ms0, ms1, os0, os1 = zs1, zs0, ms1, ms0, os1, os0
+    lnw = prepared(ln_w, torch.float32)
+    lnb = prepared(ln_b, torch.float32)
+    ws = [prepared(w, ct) for w in (w_bias, w_q, w_k, w_v, w_g, w_o)]
+    a = _lib.TriattArgs()
+    a.struct_size = ctypes.sizeof(_lib.TriattArgs)
+    a.n, a.c, a.heads, a.head_dim = n, c, heads, HEAD_DIM
+    a.z_dtype, a.compute_dtype = dtype_code(z.dtype), dtype_code(ct)
+    a.add_residual = 1 if add_residual else 0
+    a.z, a.z_s0, a.z_s1 = _ptr(z), zs0, zs1
+    a.mask, a.mask_s0, a.mask_s1 = _ptr(m), ms0, ms1
+    a.out, a.out_s0, a.out_s1 = _ptr(out), os0, os1
+    a.ln_w, a.ln_b = _ptr(lnw), _ptr(lnb)
+    a.w_bias, a.w_q, a.w_k, a.w_v, a.w_g, a.w_o = (_ptr(w) for w in ws)
+    a.inf, a.eps = float(inf), float(eps)
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    _lib.check(lib.odde_triatt_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)), "triatt workspace")
+    work = _workspace(nb.value, z.device)
+    a.workspace, a.workspace_bytes = _ptr(work), work.numel()
+    _lib.check(lib.odde_triatt_fwd(ctypes.byref(a), _stream(z.device)), "odde_triatt_fwd")
+    return out
+
+
+def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, outgoing: bool,
+                            norm_in_weight, norm_in_bias, p_in_weight, g_in_weight,
+                            norm_out_weight, norm_out_bias, p_out_weight, g_out_weight,
+                            out: Optional[torch.Tensor] = None, add_residual: bool = False,
+                            compute_dtype: Optional[torch.dtype] = None,
+                            eps: float = 1e-5) -> torch.Tensor:
+    """Fused triangle multiplicative update on one pair tensor z [N, N, C];
+    same ``out`` / ``add_residual`` contract as :func:`triangle_attention`.
+    ``p_in_weight``/``g_in_weight`` are [2*Ch, C] (a rows then b rows)."""
+    _require_gpu(z, mask)
+    _pair_view_ok(z, "z")
+    n, c = z.shape[0], z.shape[2]
+    ch = p_in_weight.shape[0] // 2
+    if c not in SUPPORTED_CHANNELS or ch not in SUPPORTED_CHANNELS:
+        raise NotImplementedError(
+            f"HIP triangle multiplication supports c, c_hidden in {SUPPORTED_CHANNELS}; "
+            f"got c={c}, c_hidden={ch}")
+    ct = compute_dtype or autocast_compute_dtype(z)
+    if z.dtype == torch.bfloat16 and ct == torch.float32:
+        raise NotImplementedError("bf16 storage with fp32 compute is not provided")
+    if out is None:
+        out = torch.empty_like(z, memory_format=torch.contiguous_format)
+    _pair_view_ok(out, "out")
+    if out.dtype != z.dtype or out.shape != z.shape:
+        raise ValueError("out must match z in shape and dtype")
+    m, ms0, ms1 = _mask_view(mask, n, z.device)
+    f32 = torch.float32
+    a = _lib.TrimulArgs()
+    a.struct_size = ctypes.sizeof(_lib.TrimulArgs)
+    a.n, a.c, a.c_hidden = n, c, ch
+    a.z_dtype, a.compute_dtype = dtype_code(z.dtype), dtype_code(ct)
+    a.outgoing = 1 if outgoing else 0
+    a.add_residual = 1 if add_residual else 0
+    a.z, a.z_s0, a.z_s1 = _ptr(z), z.stride(0), z.stride(1)
+    a.mask, a.mask_s0, a.mask_s1 = _ptr(m), ms0, ms1
+    a.out, a.out_s0, a.out_s1 = _ptr(out), out.stride(0), out.stride(1)
+    keep = [prepared(norm_in_weight, f32), prepared(norm_in_bias, f32),
+            prepared(norm_out_weight, f32), prepared(norm_out_bias, f32),
+            prepared(p_in_weight, ct), prepared(g_in_weight, ct),
+            prepared(p_out_weight, ct), prepared(g_out_weight, ct)]
+    (a.norm_in_weight, a.norm_in_bias, a.norm_out_weight, a.norm_out_bias,
+     a.p_in_weight, a.g_in_weight, a.p_out_weight, a.g_out_weight) = (_ptr(t) for t in keep)
+    a.eps = float(eps)
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    _lib.check(lib.odde_trimul_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)), "trimul workspace")
+    work = _workspace(nb.value, z.device)
+    a.workspace, a.workspace_bytes = _ptr(work), work.numel()
+    _lib.check(lib.odde_trimul_fwd(ctypes.byref(a), _stream(z.device)), "odde_trimul_fwd")
+    return out
+
+
+def triangle_attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                            bias: torch.Tensor, mask: Optional[torch.Tensor],
+                            scale: float, inf: float = 1e9) -> torch.Tensor:
+    """The accelerated slot of the reference's Attention.forward
+    (``cuequivariance_triangular_attn(q, k, v, bias, mask, scale)``,
+    opendde/model/triangular/layers.py:484-494):
+
+      q, k, v: [B, I, H, J, D] (or [B*I, H, J, D]; any strides, D contiguous);
+      bias: broadcastable to [B, 1, H, J, J] (float);
+      mask: bool, broadcastable to [B, I, 1, 1, J], True = keep (or None).
+    Returns softmax(scale*q k^T + bias + mask_term) v as [B, I, H, J, D] in q's
+    dtype, where dropped keys get -inf (= -1e9, the torch path's value).
+    """
+    _require_gpu(q, k, v, bias, mask)
+    squeeze = False
+    if q.dim() == 4:
+        q, k, v = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
+        squeeze = True
+    if q.dim() != 5 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v must share a [B, I, H, J, D] shape")
+    bsz, rows, heads, n, d = q.shape
+    if d != HEAD_DIM:
+        raise NotImplementedError("HIP triangle attention core requires head_dim == 32")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise ValueError("q, k, v need a unit stride on the head dim")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v dtypes differ")
+    b = bias
+    while b.dim() < 5:
+        b = b.unsqueeze(0)
+    b = b.float().expand(bsz, 1, heads, n, n)[:, 0]
+    if mask is not None:
+        mk = mask
+        while mk.dim() < 5:
+            mk = mk.unsqueeze(0)
+        mk = mk.expand(bsz, rows, 1, 1, n)[:, :, 0, 0, :].to(torch.uint8)
+    else:
+        mk = None
+    out = torch.empty((bsz, rows, heads, n, d), dtype=q.dtype, device=q.device)
+    a = _lib.TriattCoreArgs()
+    a.struct_size = ctypes.sizeof(_lib.TriattCoreArgs)
+    a.batch, a.rows, a.heads, a.n, a.head_dim = bsz, rows, heads, n, d
+    a.dtype = dtype_code(q.dtype)
+    a.q, a.q_sb, a.q_si, a.q_sh, a.q_sj = _ptr(q), *q.stride()[:4]
+    a.k, a.k_sb, a.k_si, a.k_sh, a.k_sj = _ptr(k), *k.stride()[:4]
+    a.v, a.v_sb, a.v_si, a.v_sh, a.v_sj = _ptr(v), *v.stride()[:4]
+    a.bias, a.b_sb, a.b_sh, a.b_sq, a.b_sk = _ptr(b), *b.stride()
+    if mk is not None:
+        a.mask, a.m_sb, a.m_si, a.m_sk = _ptr(mk), *mk.stride()
+    a.out, a.o_sb, a.o_si, a.o_sh, a.o_sj = _ptr(out), *out.stride()[:4]
+    a.scale, a.inf_value = float(scale), float(inf)
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    _lib.check(lib.odde_triatt_core_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)),
+               "triatt core workspace")
+    work = _workspace(nb.value, q.device)
+    a.workspace, a.workspace_bytes = _ptr(work), work.numel()
+    _lib.check(lib.odde_triatt_core_fwd(ctypes.byref(a), _stream(q.device)), "odde_triatt_core_fwd")
+    return out[0] if squeeze else out

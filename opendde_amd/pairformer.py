@@ -1,0 +1,236 @@
+"""PairformerBlock / PairformerStack and their non-triangle members, drop-in
+for opendde/model/modules/pairformer.py:59-451 (blocks part),
+modules/primitives.py:158-279,645-857 and modules/transformer.py:39-671.
+
+With an accelerated triangle kernel value on GPU tensors the block runs the
+fused HIP kernels with the residual add folded in, in place when
+``inplace_safe``; the ending-node attention reads and writes z through
+transposed strides instead of the reference's two full transposed copies of z
+(pairformer.py:218-226).  The pair transition and the single track run as
+PyTorch ops.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import hook
+from .layers import LayerNorm, Linear, LinearNoBias
+from .triangular import (TriangleAttention, TriangleMultiplicationIncoming,
+                         TriangleMultiplicationOutgoing)
+
+_TRANSITION_FLAT_CHUNK_ROWS = 262_144
+
+
+class Transition(nn.Module):
+    """SwiGLU transition (primitives.py:158-217), flat-chunked by rows."""
+
+    def __init__(self, c_in: int, n: int) -> None:
+        super().__init__()
+        self.n = n
+        self.c_in = c_in
+        self.layernorm1 = LayerNorm(c_in)
+        self.linear_no_bias_a = LinearNoBias(in_features=c_in, out_features=n * c_in,
+                                             initializer="relu")
+        self.linear_no_bias_b = LinearNoBias(in_features=c_in, out_features=n * c_in,
+                                             initializer="relu")
+        self.linear_no_bias = LinearNoBias(in_features=n * c_in, out_features=c_in,
+                                           initializer="zeros")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        other = x.shape[:-1]
+        xf = x.reshape(-1, x.shape[-1])
+        if xf.shape[0] > _TRANSITION_FLAT_CHUNK_ROWS:
+            chunks = xf.split(_TRANSITION_FLAT_CHUNK_ROWS, dim=0)
+        elif x.dim() >= 2 and x.shape[-2] >= 3200:
+            chunks = torch.chunk(xf, 8, dim=0)
+        else:
+            chunks = (xf,)
+        outputs = None
+        start = 0
+        for ch in chunks:
+            y = self.layernorm1(ch)
+            a = F.silu(self.linear_no_bias_a(y))
+            b = self.linear_no_bias_b(y)
+            del y
+            b = b * a
+            del a
+            b = self.linear_no_bias(b)
+            if outputs is None:
+                outputs = torch.empty((xf.shape[0], self.c_in), dtype=b.dtype, device=b.device)
+            outputs[start:start + b.shape[0]] = b
+            start += b.shape[0]
+        return outputs.reshape(*other, self.c_in)
+
+
+def _sdpa_fp32(q, k, v, bias):
+    """Attention in fp32 (primitives.py:220-258): SDPA with scale 1 and an
+    additive bias; returns the input dtype."""
+    d = q.dtype
+    o = F.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                       attn_mask=None if bias is None else bias.float(), scale=1.0)
+    return o.to(d)
+
+
+class SingleAttention(nn.Module):
+    """primitives.Attention restricted to what AttentionPairBias uses
+    (primitives.py:645-857): q with bias, k/v/o/g without, gating, q /= sqrt(dh)."""
+
+    def __init__(self, c_q: int, c_k: int, c_v: int, c_hidden: int, num_heads: int,
+                 gating: bool = True, q_linear_bias: bool = True, zero_init: bool = True):
+        super().__init__()
+        self.c_hidden = c_hidden
+        self.num_heads = num_heads
+        hd = c_hidden * num_heads
+        self.linear_q = Linear(c_q, hd) if q_linear_bias else LinearNoBias(c_q, hd)
+        self.linear_k = LinearNoBias(c_k, hd)
+        self.linear_v = LinearNoBias(c_v, hd)
+        self.linear_o = LinearNoBias(hd, c_q)
+        self.linear_g = LinearNoBias(c_q, hd, initializer="zeros") if gating else None
+        self.sigmoid = nn.Sigmoid()
+        if zero_init:
+            nn.init.zeros_(self.linear_o.weight)
+
+    def forward(self, q_x, kv_x, attn_bias=None):
+        def heads(t):
+            return t.view(t.shape[:-1] + (self.num_heads, -1)).transpose(-2, -3)
+        q = heads(self.linear_q(q_x)) / math.sqrt(self.c_hidden)
+        k = heads(self.linear_k(kv_x))
+        v = heads(self.linear_v(kv_x))
+        if attn_bias is not None and attn_bias.dim() != q.dim():
+            attn_bias = attn_bias.unsqueeze(-3)
+        o = _sdpa_fp32(q, k, v, attn_bias).transpose(-2, -3)
+        if self.linear_g is not None:
+            g = self.sigmoid(self.linear_g(q_x))
+            o = o * g.view(g.shape[:-1] + (self.num_heads, -1))
+        o = o.reshape(o.shape[:-2] + (-1,))
+        return self.linear_o(o)
+
+
+class AttentionPairBias(nn.Module):
+    """Algorithm 24 with has_s=False (transformer.py:39-671): single-track
+    attention biased by a per-head projection of LN(z)."""
+
+    def __init__(self, has_s: bool = False, create_offset_ln_z: bool = True, n_heads: int = 16,
+                 c_a: int = 384, c_s: int = 384, c_z: int = 128) -> None:
+        super().__init__()
+        if has_s:
+            raise NotImplementedError("only the Pairformer form (has_s=False) is provided")
+        assert c_a % n_heads == 0
+        self.n_heads = n_heads
+        self.layernorm_a = LayerNorm(c_a)
+        self.attention = SingleAttention(c_a, c_a, c_a, c_a // n_heads, n_heads, gating=True,
+                                         q_linear_bias=True, zero_init=True)
+        self.layernorm_z = LayerNorm(c_z, create_offset=create_offset_ln_z)
+        self.linear_nobias_z = LinearNoBias(in_features=c_z, out_features=n_heads)
+
+    def forward(self, a: torch.Tensor, s: Optional[torch.Tensor], z: torch.Tensor,
+                extra_attn_bias: Optional[torch.Tensor] = None, **_unused) -> torch.Tensor:
+        a = self.layernorm_a(a)
+        bias = self.linear_nobias_z(self.layernorm_z(z)).movedim(-1, -3)
+        if extra_attn_bias is not None:
+            eb = extra_attn_bias
+            while eb.dim() < bias.dim() - 1:
+                eb = eb.unsqueeze(0)
+            if eb.dim() == bias.dim() - 1:
+                eb = eb.unsqueeze(-3)
+            bias = bias + eb.to(dtype=bias.dtype, device=bias.device)
+        return self.attention(q_x=a, kv_x=a, attn_bias=bias)
+
+
+class PairformerBlock(nn.Module):
+    """Algorithm 17 block (pairformer.py:59-273)."""
+
+    def __init__(self, n_heads: int = 16, c_z: int = 128, c_s: int = 384, c_hidden_mul: int = 128,
+                 c_hidden_pair_att: int = 32, no_heads_pair: int = 4,
+                 num_intermediate_factor: int = 4, hidden_scale_up: bool = False) -> None:
+        super().__init__()
+        self.n_heads = n_heads
+        if hidden_scale_up:
+            no_heads_pair = c_z // c_hidden_pair_att
+            c_hidden_mul = c_z
+        self.tri_mul_out = TriangleMultiplicationOutgoing(c_z=c_z, c_hidden=c_hidden_mul)
+        self.tri_mul_in = TriangleMultiplicationIncoming(c_z=c_z, c_hidden=c_hidden_mul)
+        self.tri_att_start = TriangleAttention(c_in=c_z, c_hidden=c_hidden_pair_att,
+                                               no_heads=no_heads_pair)
+        self.tri_att_end = TriangleAttention(c_in=c_z, c_hidden=c_hidden_pair_att,
+                                             no_heads=no_heads_pair)
+        self.pair_transition = Transition(c_in=c_z, n=num_intermediate_factor)
+        self.c_s = c_s
+        if c_s > 0:
+            self.attention_pair_bias = AttentionPairBias(has_s=False, create_offset_ln_z=True,
+                                                         n_heads=n_heads, c_a=c_s, c_z=c_z)
+            self.single_transition = Transition(c_in=c_s, n=4)
+
+    def forward(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: torch.Tensor,
+                triangle_multiplicative: str = "torch", triangle_attention: str = "torch",
+                inplace_safe: bool = False, chunk_size: Optional[int] = None,
+                extra_attn_bias: Optional[torch.Tensor] = None):
+        hook.check_multiplicative_kernel(triangle_multiplicative)
+        hook.check_attention_kernel(triangle_attention)
+        hip_mul = hook.is_accelerated(triangle_multiplicative) and z.is_cuda
+        hip_att = hook.is_accelerated(triangle_attention) and z.is_cuda
+
+        # triangle multiplications: z + update, in place when allowed
+        for mod in (self.tri_mul_out, self.tri_mul_in):
+            if hip_mul:
+                z = mod.hip_apply(z, pair_mask, out=z if inplace_safe else None,
+                                  add_residual=True)
+            elif inplace_safe:
+                z = mod(z, mask=pair_mask, inplace_safe=True, _add_with_inplace=True,
+                        triangle_multiplicative="torch")
+            else:
+                z = z + mod(z, mask=pair_mask, triangle_multiplicative="torch")
+
+        if hip_att:
+            z = self.tri_att_start.hip_apply(z, pair_mask, out=z if inplace_safe else None,
+                                             add_residual=True)
+            z = self.tri_att_end.hip_apply(z, pair_mask, transpose=True,
+                                           out=z if inplace_safe else None, add_residual=True)
+        else:
+            upd = self.tri_att_start(z, mask=pair_mask, triangle_attention="torch",
+                                     chunk_size=chunk_size)
+            z = z.add_(upd) if inplace_safe else z + upd
+            zt = z.transpose(-2, -3).contiguous()
+            upd = self.tri_att_end(zt, mask=pair_mask.transpose(-1, -2) if pair_mask is not None
+                                   else None, triangle_attention="torch", chunk_size=chunk_size)
+            zt = zt.add_(upd) if inplace_safe else zt + upd
+            z = zt.transpose(-2, -3).contiguous()
+
+        upd = self.pair_transition(z)
+        z = z.add_(upd) if inplace_safe else z + upd
+        if self.c_s > 0:
+            s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias)
+            s = s + self.single_transition(s)
+        return s, z
+
+
+class PairformerStack(nn.Module):
+    """Algorithm 17 stack (pairformer.py:276-451); no activation checkpointing
+    (inference)."""
+
+    def __init__(self, n_blocks: int = 48, n_heads: int = 16, c_z: int = 128, c_s: int = 384,
+                 num_intermediate_factor: int = 4, blocks_per_ckpt: Optional[int] = None,
+                 hidden_scale_up: bool = False) -> None:
+        super().__init__()
+        self.n_blocks = n_blocks
+        self.n_heads = n_heads
+        self.blocks_per_ckpt = blocks_per_ckpt
+        self.blocks = nn.ModuleList(
+            PairformerBlock(n_heads=n_heads, c_z=c_z, c_s=c_s,
+                            num_intermediate_factor=num_intermediate_factor,
+                            hidden_scale_up=hidden_scale_up) for _ in range(n_blocks))
+
+    def forward(self, s, z, pair_mask, triangle_multiplicative: str = "torch",
+                triangle_attention: str = "torch", inplace_safe: bool = False,
+                chunk_size: Optional[int] = None, extra_attn_bias=None):
+        for b in self.blocks:
+            s, z = b(s, z, pair_mask, triangle_multiplicative=triangle_multiplicative,
+                     triangle_attention=triangle_attention, inplace_safe=inplace_safe,
+                     chunk_size=chunk_size, extra_attn_bias=extra_attn_bias)
+        return s, z

@@ -1,0 +1,112 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/opendde_amd.h declares, its struct layouts match the ctypes
+mirrors (sizes and field offsets as gcc computes them from the header), and
+invalid arguments come back as status codes with a message (no device call
+is reached on those paths)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from opendde_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "opendde_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(odde_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"missing export {name}"
+    assert set(declared) == set(_lib.SYMBOLS), "ctypes binding and header disagree"
+    assert lib.odde_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("cname,pyty", [("odde_triatt_args", _lib.TriattArgs),
+                                        ("odde_triatt_core_args", _lib.TriattCoreArgs),
+                                        ("odde_trimul_args", _lib.TrimulArgs)])
+def test_struct_layout_matches_header(cname, pyty):
+    fields = [f for f, _ in pyty._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
+           f'printf("%zu\\n", sizeof({cname}));']
+    src += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
+    src += ["return 0;}"]
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        exe = os.path.join(d, "t")
+        open(c, "w").write("\n".join(src))
+        subprocess.run(["gcc", "-std=c99", c, "-o", exe], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True,
+                                               check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(pyty)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(pyty, f).offset == off, f
+
+
+def _status(fn, args):
+    lib = _lib.load()
+    rc = getattr(lib, fn)(ctypes.byref(args), ctypes.c_void_p(0))
+    return rc, lib.odde_last_error().decode()
+
+
+def test_bad_arguments_return_status_and_message():
+    a = _lib.TriattArgs()
+    a.struct_size = ctypes.sizeof(a) - 4
+    rc, msg = _status("odde_triatt_fwd", a)
+    assert rc == -1 and "struct_size" in msg
+    a.struct_size = ctypes.sizeof(a)
+    a.n, a.c, a.heads, a.head_dim = 64, 128, 4, 16
+    rc, msg = _status("odde_triatt_fwd", a)
+    assert rc == -2 and "head_dim" in msg
+    a.head_dim = 32
+    a.z_dtype = a.compute_dtype = 0
+    rc, msg = _status("odde_triatt_fwd", a)
+    assert rc == -1 and "null" in msg
+    t = _lib.TrimulArgs()
+    t.struct_size = ctypes.sizeof(t)
+    t.n, t.c, t.c_hidden = 32, 100, 128
+    rc, msg = _status("odde_trimul_fwd", t)
+    assert rc == -2 and "c_hidden" in msg
+
+
+def test_workspace_query_and_too_small_workspace():
+    lib = _lib.load()
+    t = _lib.TrimulArgs()
+    t.struct_size = ctypes.sizeof(t)
+    t.n, t.c, t.c_hidden = 100, 128, 128
+    t.z_dtype, t.compute_dtype = 0, 1
+    nb = ctypes.c_uint64(0)
+    assert lib.odde_trimul_workspace_bytes(ctypes.byref(t), ctypes.byref(nb)) == 0
+    np_ = 128
+    assert nb.value >= 3 * 128 * np_ * np_ * 2
+    # non-null pointers but no workspace -> EWORKSPACE before any launch
+    fake = ctypes.c_void_p(0x1000)
+    for f in ("z", "out", "norm_in_weight", "norm_in_bias", "norm_out_weight", "norm_out_bias",
+              "p_in_weight", "g_in_weight", "p_out_weight", "g_out_weight"):
+        setattr(t, f, fake)
+    rc = lib.odde_trimul_fwd(ctypes.byref(t), ctypes.c_void_p(0))
+    assert rc == -3 and "workspace" in lib.odde_last_error().decode()
+
+
+def test_loader_caches_failure(monkeypatch):
+    _lib.reset_loader_for_tests()
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libopendde_amd.so")
+    with pytest.raises(ImportError):
+        _lib.load()
+    monkeypatch.setattr(_lib, "LIB_PATH", os.path.join(ROOT, "opendde_amd", "lib",
+                                                        "libopendde_amd.so"))
+    with pytest.raises(ImportError):  # cached failure, no second attempt
+        _lib.load()
+    _lib.reset_loader_for_tests()
+    assert _lib.load() is not None

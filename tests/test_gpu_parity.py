@@ -1,0 +1,179 @@
+"""GPU parity: the HIP kernels (called through the C ABI by the drop-in
+modules) against the CPU oracle on identical seeded inputs and weights.
+
+Tiers: fp32 kernels max-abs <= 1e-4 vs the fp32 oracle; bf16 kernels
+rel-L2 <= 1e-2 and max-abs <= 5e-2 vs the fp32 oracle fed the same
+(bf16-representable) input.
+"""
+
+import pytest
+import torch
+
+from helpers import (assert_bf16, assert_fp32, params_of, say, seeded, token_pair_mask)
+from oracle import reference as ref
+from opendde_amd import _lib
+from opendde_amd.pairformer import PairformerBlock
+from opendde_amd.triangular import (Attention, TriangleAttention, TriangleMultiplicationIncoming,
+                                    TriangleMultiplicationOutgoing)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+STD = 0.1  # larger than the workload's 0.02 so that every term is visible
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    say(f"[gpu] {request.node.nodeid}")
+    yield
+    torch.cuda.synchronize()
+
+
+def _z(n, c, seed, dtype=torch.float32):
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(seed))
+    return z.to(dtype)
+
+
+# ---------------------------------------------------------------- attention
+
+
+@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("starting", [True, False])
+def test_triangle_attention_fp32(n, starting):
+    mod = seeded(TriangleAttention(128, 32, 4, starting=starting), 100 + n, STD)
+    z = _z(n, 128, n)
+    mask = token_pair_mask(n, max(1, n // 10))
+    exp = ref.triangle_attention(z, mask, params_of(mod), 4, starting=starting)
+    before = _lib.launch_count(_lib.K_TRIATT_CORE)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
+    assert _lib.launch_count(_lib.K_TRIATT_CORE) == before + 1
+    assert_fp32(got, exp, f"triatt n={n} start={starting}")
+
+
+@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("starting", [True, False])
+def test_triangle_attention_bf16(n, starting):
+    mod = seeded(TriangleAttention(128, 32, 4, starting=starting), 200 + n, STD)
+    z = _z(n, 128, n + 1, torch.bfloat16)
+    mask = token_pair_mask(n, max(1, n // 10))
+    exp = ref.triangle_attention(z.float(), mask, params_of(mod), 4, starting=starting)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
+    assert got.dtype == torch.bfloat16
+    assert_bf16(got, exp, f"triatt bf16 n={n} start={starting}")
+
+
+@pytest.mark.parametrize("c,h", [(64, 2), (256, 8), (384, 12)])
+def test_triangle_attention_channel_shapes(c, h):
+    n = 40
+    mod = seeded(TriangleAttention(c, 32, h), 300 + c, STD)
+    z = _z(n, c, c)
+    mask = token_pair_mask(n, 3)
+    exp = ref.triangle_attention(z, mask, params_of(mod), h)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="cuequivariance")
+    assert_fp32(got, exp, f"triatt c={c} h={h}")
+
+
+def test_triangle_attention_no_mask_and_in_place_add():
+    n = 48
+    mod = seeded(TriangleAttention(128, 32, 4), 7, STD).to(DEV)
+    z = _z(n, 128, 8).to(DEV)
+    upd = mod(z, None, triangle_attention="hip")
+    exp = ref.triangle_attention(z.cpu(), None, params_of(mod), 4)
+    assert_fp32(upd, exp, "triatt no mask")
+    z2 = z.clone()
+    out = mod.hip_apply(z2, None, out=z2, add_residual=True)
+    assert out.data_ptr() == z2.data_ptr()
+    assert_fp32(z2, z.cpu() + exp, "triatt in-place add")
+
+
+def test_attention_core_slot_matches_oracle():
+    # Attention.forward with the accelerated kwarg -> hip_triangular_attn slot
+    n, c, h = 45, 128, 4
+    tri = seeded(TriangleAttention(128, 32, 4), 11, STD)
+    att = tri.mha
+    x = torch.randn(n, n, c, generator=torch.Generator().manual_seed(12))
+    mask = token_pair_mask(n, 5)
+    mask_bias = (1e9 * (mask - 1))[..., :, None, None, :]
+    tb = (x @ tri.linear.weight.t()).movedim(-1, -3).unsqueeze(-4)
+    q = (x @ att.linear_q.weight.t()).view(n, n, h, 32).transpose(-2, -3) / 32 ** 0.5
+    k = (x @ att.linear_k.weight.t()).view(n, n, h, 32).transpose(-2, -3)
+    v = (x @ att.linear_v.weight.t()).view(n, n, h, 32).transpose(-2, -3)
+    o = ref.attention_core(q, k, v, [mask_bias, tb]).transpose(-2, -3)
+    g = torch.sigmoid(x @ att.linear_g.weight.t()).view(n, n, h, 32)
+    exp = (o * g).reshape(n, n, h * 32) @ att.linear_o.weight.t()
+    before = _lib.launch_count(_lib.K_TRIATT_RELAYOUT)
+    att = att.to(DEV)
+    got = att(x.to(DEV), x.to(DEV), biases=[mask_bias.to(DEV), tb.to(DEV)],
+              triangle_attention="hip")
+    assert _lib.launch_count(_lib.K_TRIATT_RELAYOUT) == before + 1
+    assert_fp32(got, exp, "core slot")
+
+
+# ---------------------------------------------------------- multiplication
+
+
+@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_fp32(n, outgoing):
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(128, 128), 400 + n, STD)
+    z = _z(n, 128, 3 * n)
+    mask = token_pair_mask(n, max(1, n // 10), seed=n, random=True)
+    exp = ref.triangle_multiplication(z, mask, params_of(mod), outgoing)
+    before = _lib.launch_count(_lib.K_TRIMUL_CONTRACT)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_multiplicative="hip")
+    assert _lib.launch_count(_lib.K_TRIMUL_CONTRACT) == before + 1
+    assert_fp32(got, exp, f"trimul n={n} out={outgoing}")
+
+
+@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_bf16(n, outgoing):
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(128, 128), 500 + n, STD)
+    z = _z(n, 128, 5 * n, torch.bfloat16)
+    mask = token_pair_mask(n, max(1, n // 10), seed=n, random=True)
+    exp = ref.triangle_multiplication(z.float(), mask, params_of(mod), outgoing)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_multiplicative="hip")
+    assert_bf16(got, exp, f"trimul bf16 n={n} out={outgoing}")
+
+
+@pytest.mark.parametrize("c,ch", [(64, 128), (64, 64), (384, 384), (128, 256)])
+def test_triangle_multiplication_channel_shapes(c, ch):
+    n = 40
+    mod = seeded(TriangleMultiplicationIncoming(c, ch), 600 + c + ch, STD)
+    z = _z(n, c, c + ch)
+    exp = ref.triangle_multiplication(z, None, params_of(mod), False)
+    got = mod.to(DEV)(z.to(DEV), None, triangle_multiplicative="hip")
+    assert_fp32(got, exp, f"trimul c={c} ch={ch}")
+
+
+def test_triangle_multiplication_in_place_add():
+    n = 70
+    mod = seeded(TriangleMultiplicationOutgoing(128, 128), 9, STD).to(DEV)
+    z = _z(n, 128, 10).to(DEV)
+    mask = token_pair_mask(n, 6).to(DEV)
+    exp = z.cpu() + ref.triangle_multiplication(z.cpu(), mask.cpu(), params_of(mod), True)
+    z2 = z.clone()
+    out = mod(z2, mask, inplace_safe=True, _add_with_inplace=True, triangle_multiplicative="hip")
+    assert out.data_ptr() == z2.data_ptr()
+    assert_fp32(z2, exp, "trimul in-place add")
+
+
+# ------------------------------------------------------------------- block
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_pairformer_block_fp32(inplace):
+    n = 36
+    blk = seeded(PairformerBlock(n_heads=16, c_z=128, c_s=384), 21, 0.05)
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(n, n, 128, generator=g)
+    s = torch.randn(n, 384, generator=g)
+    mask = token_pair_mask(n, 4)
+    se, ze = ref.pairformer_block(s, z, mask, params_of(blk), no_heads_pair=4, n_heads=16)
+    blk = blk.to(DEV)
+    with torch.no_grad():
+        sg, zg = blk(s.to(DEV), z.to(DEV).clone(), mask.to(DEV), triangle_multiplicative="hip",
+                     triangle_attention="hip", inplace_safe=inplace)
+    assert_fp32(zg, ze, "block z")
+    assert_fp32(sg, se, "block s")

@@ -1,0 +1,247 @@
+"""Pins for the CPU oracle (oracle/reference.py).
+
+Each oracle function is checked against something that does not restate its
+own formula: float64 scalar loops written from the algorithm definitions
+(tests/brute_force.py), library routines (F.layer_norm, SDPA), closed forms
+and invariants.  CPU only.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import brute_force as bf
+from oracle import reference as ref
+from opendde_amd import workload as wl
+
+D64 = torch.float64
+
+
+def _params(specs, seed, std=0.3):
+    # A larger std than the workload's 0.02 so every term matters numerically.
+    p = wl.param_values(specs, wl.generator(seed), std)
+    return {k: v.to(D64) for k, v in p.items()}
+
+
+def _rand_mask(n, seed, p_drop=0.3, full_rows=()):
+    g = torch.Generator().manual_seed(seed)
+    m = (torch.rand((n, n), generator=g) > p_drop).to(D64)
+    m[:, 0] = 1.0  # keep one unmasked key/entry per row and column
+    m[0, :] = 1.0
+    for r in full_rows:
+        m[r, :] = 0.0
+    return m
+
+
+def _strip(p, prefix):
+    return {k[len(prefix):]: v for k, v in p.items() if k.startswith(prefix)}
+
+
+# ---------------------------------------------------------------- primitives
+
+
+def test_layer_norm_matches_library_and_loops():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 7, 16, generator=g, dtype=D64) * 3 + 1
+    w = torch.randn(16, generator=g, dtype=D64)
+    b = torch.randn(16, generator=g, dtype=D64)
+    y = ref.layer_norm(x, w, b)
+    torch.testing.assert_close(y, F.layer_norm(x, (16,), w, b, 1e-5), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(y.numpy(), bf.layer_norm_rows(x, w, b), rtol=1e-10, atol=1e-10)
+
+
+def test_attention_core_is_sdpa_without_bias():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(3, 2, 9, 4, generator=g, dtype=D64) for _ in range(3))
+    bias = torch.randn(3, 2, 9, 9, generator=g, dtype=D64)
+    out = ref.attention_core(q, k, v, [bias])
+    exp = F.scaled_dot_product_attention(q, k, v, attn_mask=bias, scale=1.0)
+    torch.testing.assert_close(out, exp, rtol=1e-10, atol=1e-10)
+
+
+def test_attention_core_key_permutation_invariance():
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(2, 11, 8, generator=g, dtype=D64) for _ in range(3))
+    bias = torch.randn(2, 11, 11, generator=g, dtype=D64)
+    perm = torch.randperm(11, generator=g)
+    a = ref.attention_core(q, k, v, [bias])
+    b = ref.attention_core(q, k[:, perm], v[:, perm], [bias[..., perm]])
+    torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+# ----------------------------------------------------------- tri attention
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triangle_attention_brute_force(starting):
+    n, c, h, d = 5, 8, 2, 4
+    p = _params(wl.triatt_specs(c, h, d), 10)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(3), dtype=D64)
+    mask = _rand_mask(n, 4)
+    out = ref.triangle_attention(z, mask, p, h, starting=starting)
+    exp = bf.triangle_attention(z, mask, p, h, starting=starting)
+    np.testing.assert_allclose(out.numpy(), exp, rtol=1e-9, atol=1e-9)
+
+
+def test_triangle_attention_chunked_equals_unchunked():
+    n, c, h, d = 9, 8, 2, 4
+    p = _params(wl.triatt_specs(c, h, d), 11)
+    z = torch.randn(1, n, n, c, generator=torch.Generator().manual_seed(5), dtype=D64)
+    mask = _rand_mask(n, 6)[None]
+    a = ref.triangle_attention(z, mask, p, h)
+    for cs in (1, 2, 4, 100):
+        b = ref.triangle_attention(z, mask, p, h, chunk_size=cs)
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_triangle_attention_fully_masked_row_is_mean_of_v_fp32():
+    """inf*(mask-1) with inf=1e9 is additive; in float32 the logits of a fully
+    masked row all round to -1e9, so the softmax is uniform and the row's
+    output is W_o(sigmoid(g) * mean_k V)."""
+    n, c, h, d = 12, 16, 2, 8
+    p = {k: v.float() for k, v in _params(wl.triatt_specs(c, h, d), 12, std=0.1).items()}
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(7))
+    t = torch.ones(n)
+    t[-3:] = 0
+    mask = t[:, None] * t[None, :]
+    out = ref.triangle_attention(z, mask, p, h)
+    x = F.layer_norm(z, (c,), p["layer_norm.weight"], p["layer_norm.bias"], 1e-5)
+    v = x @ p["mha.linear_v.weight"].t()
+    g = torch.sigmoid(x @ p["mha.linear_g.weight"].t())
+    for i in range(n - 3, n):
+        exp = (g[i] * v[i].mean(0, keepdim=True)) @ p["mha.linear_o.weight"].t()
+        torch.testing.assert_close(out[i], exp, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------- tri mul
+
+
+def test_combine_projections_loops_and_in_out_relation():
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(6, 6, 3, generator=g, dtype=D64)
+    b = torch.randn(6, 6, 3, generator=g, dtype=D64)
+    for outgoing in (True, False):
+        np.testing.assert_allclose(ref.combine_projections(a, b, outgoing).numpy(),
+                                   bf.contract(a, b, outgoing), rtol=1e-12, atol=1e-12)
+    aT, bT = a.transpose(0, 1), b.transpose(0, 1)
+    torch.testing.assert_close(ref.combine_projections(a, b, False),
+                               ref.combine_projections(aT, bT, True))
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_brute_force(outgoing):
+    n, c, ch = 5, 8, 6
+    p = _params(wl.trimul_specs(c, ch), 20)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(9), dtype=D64)
+    mask = _rand_mask(n, 10)
+    out = ref.triangle_multiplication(z, mask, p, outgoing)
+    exp = bf.triangle_multiplication(z, mask, p, outgoing)
+    np.testing.assert_allclose(out.numpy(), exp, rtol=1e-9, atol=1e-9)
+
+
+def test_triangle_multiplication_special_cases():
+    n, c, ch = 6, 8, 4
+    p = _params(wl.trimul_specs(c, ch), 21)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(11), dtype=D64)
+    # "final" init of linear_z -> the update is exactly zero.
+    pz = dict(p)
+    pz["linear_z.weight"] = torch.zeros_like(p["linear_z.weight"])
+    assert torch.count_nonzero(ref.triangle_multiplication(z, None, pz, True)) == 0
+    # Masking the whole pair tensor zeroes a and b, so p == 0 and LN_out(0)
+    # is its bias: the update is W_z(beta_out) * sigmoid(W_g LN_in(z)).
+    m0 = torch.zeros(n, n, dtype=D64)
+    out = ref.triangle_multiplication(z, m0, p, False)
+    zn = F.layer_norm(z, (c,), p["layer_norm_in.weight"], p["layer_norm_in.bias"], 1e-5)
+    exp = (p["linear_z.weight"] @ p["layer_norm_out.bias"]) * torch.sigmoid(
+        zn @ p["linear_g.weight"].t())
+    torch.testing.assert_close(out, exp, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("n,chunk", [(7, 2), (8, 3), (9, 4), (5, 256), (1, 256)])
+def test_triangle_multiplication_inplace_equals_standard_plus_z(outgoing, n, chunk):
+    c, ch = 8, 6
+    p = _params(wl.trimul_specs(c, ch), 22)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(12), dtype=D64)
+    mask = _rand_mask(n, 13) if n > 1 else None
+    std = z + ref.triangle_multiplication(z, mask, p, outgoing)
+    inp = ref.triangle_multiplication_inplace(z, mask, p, outgoing, chunk=chunk)
+    torch.testing.assert_close(inp, std, rtol=1e-10, atol=1e-10)
+    no_add = ref.triangle_multiplication_inplace(z, mask, p, outgoing, chunk=chunk,
+                                                 with_add=False)
+    torch.testing.assert_close(no_add, std - z, rtol=1e-10, atol=1e-10)
+
+
+# ---------------------------------------------------------- block members
+
+
+def test_transition_brute_force():
+    p = _params(wl.transition_specs(8, 4), 30)
+    x = torch.randn(3, 4, 8, generator=torch.Generator().manual_seed(14), dtype=D64)
+    np.testing.assert_allclose(ref.transition(x, p).numpy(), bf.transition(x, p),
+                               rtol=1e-10, atol=1e-10)
+
+
+def test_attention_pair_bias_brute_force():
+    n, c_s, c_z, nh = 6, 8, 4, 2
+    p = _params(wl.apb_specs(c_s, c_z, nh), 31)
+    g = torch.Generator().manual_seed(15)
+    s = torch.randn(n, c_s, generator=g, dtype=D64)
+    z = torch.randn(n, n, c_z, generator=g, dtype=D64)
+    np.testing.assert_allclose(ref.attention_pair_bias(s, z, p, nh).numpy(),
+                               bf.attention_pair_bias(s, z, p, nh), rtol=1e-9, atol=1e-9)
+
+
+def _small_block(seed, c_s=8):
+    dims = dict(c_z=8, c_s=c_s, h=2, d=4, ch=6, n_heads=2)
+    return _params(wl.block_specs(**dims), seed), dims
+
+
+def test_pairformer_block_brute_force():
+    n = 4
+    p, dims = _small_block(40)
+    g = torch.Generator().manual_seed(16)
+    z = torch.randn(n, n, 8, generator=g, dtype=D64)
+    s = torch.randn(n, 8, generator=g, dtype=D64)
+    mask = _rand_mask(n, 17)
+    so, zo = ref.pairformer_block(s, z, mask, p, no_heads_pair=2, n_heads=2)
+    sb, zb = bf.pairformer_block(s, z, mask, p, 2, 2)
+    np.testing.assert_allclose(zo.numpy(), zb, rtol=1e-8, atol=1e-8)
+    np.testing.assert_allclose(so.numpy(), sb, rtol=1e-8, atol=1e-8)
+
+
+def test_pairformer_block_inplace_branch_same_math():
+    n = 7
+    p, _ = _small_block(41)
+    g = torch.Generator().manual_seed(18)
+    z = torch.randn(n, n, 8, generator=g, dtype=D64)
+    s = torch.randn(n, 8, generator=g, dtype=D64)
+    mask = _rand_mask(n, 19)
+    a = ref.pairformer_block(s, z, mask, p, no_heads_pair=2, n_heads=2)
+    b = ref.pairformer_block(s, z, mask, p, no_heads_pair=2, n_heads=2, inplace=True,
+                             chunk_size=3)
+    torch.testing.assert_close(a[1], b[1], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(a[0], b[0], rtol=1e-10, atol=1e-10)
+
+
+def test_pairformer_stack_is_sequential_blocks():
+    n = 4
+    dims = dict(c_z=8, c_s=0, h=2, d=4, ch=6, n_heads=2)
+    p = _params(wl.stack_specs(2, **dims), 42)
+    z = torch.randn(n, n, 8, generator=torch.Generator().manual_seed(20), dtype=D64)
+    mask = _rand_mask(n, 21)
+    _, z2 = ref.pairformer_stack(None, z, mask, p, 2, no_heads_pair=2)
+    _, z1 = ref.pairformer_block(None, z, mask, _strip(p, "blocks.0."), no_heads_pair=2)
+    _, z1 = ref.pairformer_block(None, z1, mask, _strip(p, "blocks.1."), no_heads_pair=2)
+    torch.testing.assert_close(z1, z2, rtol=0, atol=0)
+
+
+def test_flop_accounting_closed_forms():
+    # Block totals quoted for the path's workloads (N=128: 22.2 GF; N=1024: 2.831 TF).
+    assert abs(ref.flops_block(128) / 1e9 - 22.2) < 0.1
+    assert abs(ref.flops_block(1024) / 1e12 - 2.831) < 0.005
+    assert abs(ref.flops_triatt_core(1024, 4, 32) / 1e9 - 549.8) < 0.1
+    assert abs(ref.flops_trimul_contract(768, 128) / 1e9 - 115.96) < 0.01
