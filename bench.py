@@ -1,0 +1,214 @@
+"""Benchmark: 48-block Pairformer trunk forward at N=1024 tokens, bf16 compute.
+
+One step = one full PairformerStack forward (48 blocks, c_z=128, c_s=384,
+4 triangle heads x 32, tri-mul hidden 128, 16 single heads; 5% random token
+padding; synthetic z, s ~ N(0,1), random weights ~ N(0, 0.02), seed 3) with
+the HIP triangle kernels, in place (inference form), residual stream z in
+float32 and module arithmetic in bf16 (CUDA autocast, the reference's bf16
+inference mode).  Inputs are resident in HBM before timing; each step starts
+by restoring z from a resident copy (a 512 MB device copy, ~0.1 ms).
+
+Prints ONE JSON line.  ``value`` is the trunk's algorithmic throughput in
+TFLOP/s (flop counts of the path, multiply-add = 2); per-kernel figures come
+from HIP events recorded by the library around every launch on the stream it
+runs on, over the timed steps.  ``cpu_baseline`` times the CPU oracle (fp32)
+on one block of the same workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from opendde_amd import _lib  # noqa: E402
+from opendde_amd import workload as wl  # noqa: E402
+from opendde_amd.pairformer import PairformerStack  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X fp32 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def flops(n, c_z=128, c_s=384, h=4, d=32, ch=128, n_heads=16):
+    """Algorithmic flops per launch / per block (same formulas as the oracle's
+    accounting; restated here so the product path does not import the oracle)."""
+    core = 4.0 * n ** 3 * h * d
+    att_lin = 2.0 * n * n * c_z * (5 * h * d + h)
+    contract = 2.0 * n ** 3 * ch
+    mul_lin = 2.0 * n * n * (4 * c_z * ch + c_z * c_z + ch * c_z)
+    trans = 2.0 * n * n * (2 * c_z * 4 * c_z + 4 * c_z * c_z)
+    single = (2.0 * n * n * c_z * n_heads + 8.0 * n * c_s * c_s + 4.0 * n * n * c_s
+              + 2.0 * n * c_s * c_s + 2.0 * n * (2 * c_s * 4 * c_s + 4 * c_s * c_s))
+    block = 2 * (core + att_lin) + 2 * (contract + mul_lin) + trans + (single if c_s else 0)
+    return dict(core=core, att_lin=att_lin, contract=contract, mul_lin=mul_lin, block=block)
+
+
+def kernel_bytes(n, c_z=128, h=4, ch=128, z_bytes=4, ct_bytes=2):
+    """Algorithmic HBM bytes per launch of the memory-bound kernels."""
+    jp = (n + 63) // 64 * 64
+    np_ = (n + 127) // 128 * 128
+    hd = h * 32
+    zrw = n * n * c_z * z_bytes
+    return {
+        "triatt_proj": zrw + 4 * n * jp * hd * ct_bytes + h * jp * jp * ct_bytes + n * jp * 4,
+        "triatt_out": n * jp * hd * ct_bytes + 2 * zrw,
+        "trimul_proj": zrw + 2 * ch * np_ * np_ * ct_bytes,
+        "trimul_out": ch * np_ * np_ * ct_bytes + 2 * zrw,
+    }
+
+
+def cpu_baseline(n: int, chunk: int):
+    """Time the CPU oracle (fp32) on one PairformerBlock of the workload at n."""
+    from oracle import reference as ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = wl.PairConfig("cpu_sample", n, n_pad=max(0, n * 5 // 100), random_pad=True, seed=3)
+    z, s, mask, gen = wl.make_inputs(cfg)
+    params = wl.param_values(wl.block_specs(), gen)
+    # warm the thread pool and allocator on a tiny block
+    ref.pairformer_block(s[:16], z[:16, :16], mask[:16, :16], params, chunk_size=chunk)
+    t0 = time.perf_counter()
+    ref.pairformer_block(s, z, mask, params, chunk_size=chunk)
+    dt = time.perf_counter() - t0
+    f = flops(n)["block"]
+    return {
+        "value": round(f / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle (CPU PyTorch restatement of the reference torch path) fp32, one "
+                  f"PairformerBlock at N={n} (tri-attn row chunk {chunk}), {dt:.2f} s; "
+                  f"CPU {platform.processor() or platform.machine()}, "
+                  f"{cores} cores in affinity",
+        "block_ms": round(dt * 1e3, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--n", type=int, default=1024)
+    ap.add_argument("--blocks", type=int, default=48)
+    ap.add_argument("--cpu-sample-n", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on one GPU only: this build measures the single-GPU pair-stack "
+              "kernels; multi-GPU runs are not part of it.", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = wl.PairConfig("trunk", args.n, n_blocks=args.blocks, n_pad=args.n * 5 // 100,
+                        random_pad=True, seed=3)
+    z0, s0, mask, gen = wl.make_inputs(cfg)
+    stack = PairformerStack(n_blocks=args.blocks, c_z=128, c_s=384)
+    wl.init_module_(stack, gen)
+    stack = stack.to(dev).eval()
+    z0, s0, mask = z0.to(dev), s0.to(dev), mask.to(dev)
+    z = torch.empty_like(z0)
+
+    def step():
+        z.copy_(z0)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            s, _ = stack(s0, z, mask, triangle_multiplicative="hip", triangle_attention="hip",
+                         inplace_safe=True)
+        return s
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        s_out = step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    _lib.timing_enable(False)
+    assert torch.isfinite(z).all() and torch.isfinite(s_out).all(), "non-finite trunk output"
+
+    n = args.n
+    f = flops(n)
+    ms_step = dt * 1e3 / args.steps
+    trunk_flops = f["block"] * args.blocks
+    value = trunk_flops / (ms_step * 1e-3) / 1e12
+
+    kb = kernel_bytes(n)
+    kernels = {}
+    for kid, name in _lib.KERNEL_NAMES.items():
+        tot, cnt = _lib.timing_query(kid)
+        if cnt == 0:
+            continue
+        avg = tot / cnt
+        ent = {"launches": cnt, "avg_ms": round(avg, 4), "total_ms_per_step": round(tot / args.steps, 3)}
+        if name == "triatt_core":
+            t = f["core"] / (avg * 1e-3) / 1e12
+            ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
+        elif name == "trimul_contract":
+            t = f["contract"] / (avg * 1e-3) / 1e12
+            ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
+        elif name in kb:
+            gbs = kb[name] / (avg * 1e-3) / 1e9
+            ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_HBM_GBS, 2))
+        kernels[name] = ent
+    dom = max(kernels, key=lambda k: kernels[k]["total_ms_per_step"])
+    d = kernels[dom]
+    if "tflops" in d:
+        achieved = d["tflops"]
+        roof = {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    else:
+        achieved = d["gbs"]
+        roof = {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+
+    att_mod_ms = sum(kernels.get(k, {}).get("avg_ms", 0) for k in ("triatt_proj", "triatt_core", "triatt_out"))
+    mul_mod_ms = sum(kernels.get(k, {}).get("avg_ms", 0) for k in ("trimul_proj", "trimul_contract", "trimul_out"))
+    out = {
+        "metric": "Pairformer block ms + tri-attn/tri-mul TFLOP/s (% MFMA peak) at N=1024 bf16",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"pairformer_trunk_{args.blocks}x_n{n}", "n_tokens": n,
+                   "n_blocks": args.blocks, "c_z": 128, "c_s": 384, "tri_heads": 4,
+                   "head_dim": 32, "c_hidden_mul": 128, "pad_tokens": n * 5 // 100,
+                   "residual_dtype": "fp32", "compute_dtype": "bf16", "seed": 3},
+        "block_ms": round(ms_step / args.blocks, 3),
+        "tri_attn_core_tflops": kernels.get("triatt_core", {}).get("tflops"),
+        "tri_attn_core_pct_peak": kernels.get("triatt_core", {}).get("pct_bf16_peak"),
+        "tri_attn_module_tflops": round((f["core"] + f["att_lin"]) / (att_mod_ms * 1e-3) / 1e12, 2)
+        if att_mod_ms else None,
+        "tri_mul_contract_tflops": kernels.get("trimul_contract", {}).get("tflops"),
+        "tri_mul_contract_pct_peak": kernels.get("trimul_contract", {}).get("pct_bf16_peak"),
+        "tri_mul_module_tflops": round((f["contract"] + f["mul_lin"]) / (mul_mod_ms * 1e-3) / 1e12, 2)
+        if mul_mod_ms else None,
+        "kernels": kernels,
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_sample_n, chunk=128)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -10,6 +10,7 @@ missing library raise.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -63,29 +64,35 @@ def _pair_view_ok(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be square in its pair dims")
 
 
-# Converted weights are cached per (parameter storage, version, dtype) so the
-# per-call cost is a dictionary lookup once weights are in place.
-_wcache: Dict[Tuple, torch.Tensor] = {}
+# Converted weights are cached per source tensor *object* (held by weak
+# reference, so a freed parameter whose device address is reused by a new one
+# can never hit) and its version counter (in-place updates invalidate).
+_wcache: Dict[Tuple, Tuple] = {}
+
+
+def _cached(key, srcs, make):
+    ent = _wcache.get(key)
+    if ent is not None:
+        refs, versions, val = ent
+        if all(r() is s for r, s in zip(refs, srcs)) and versions == tuple(s._version for s in srcs):
+            return val
+    if len(_wcache) > 4096:
+        _wcache.clear()
+    val = make()
+    _wcache[key] = (tuple(weakref.ref(s) for s in srcs), tuple(s._version for s in srcs), val)
+    return val
 
 
 def prepared(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    key = (t.data_ptr(), t._version, tuple(t.shape), t.dtype, dtype, t.device)
-    hit = _wcache.get(key)
-    if hit is None:
-        if len(_wcache) > 4096:
-            _wcache.clear()
-        hit = t.detach().to(dtype).contiguous()
-        _wcache[key] = hit
-    return hit
+    """``t`` as a contiguous ``dtype`` tensor, converted once per version."""
+    return _cached((id(t), dtype), (t,), lambda: t.detach().to(dtype).contiguous())
 
 
 def prepared_cat(ts, dtype: torch.dtype) -> torch.Tensor:
-    key = ("cat",) + tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in ts) + (dtype,)
-    hit = _wcache.get(key)
-    if hit is None:
-        hit = torch.cat([t.detach() for t in ts], 0).to(dtype).contiguous()
-        _wcache[key] = hit
-    return hit
+    """Row-concatenation of ``ts`` as a contiguous ``dtype`` tensor (cached)."""
+    ts = tuple(ts)
+    return _cached(("cat",) + tuple(id(t) for t in ts) + (dtype,), ts,
+                   lambda: torch.cat([t.detach() for t in ts], 0).to(dtype).contiguous())
 
 
 def _mask_view(mask: Optional[torch.Tensor], n: int, device) -> Tuple[Optional[torch.Tensor], int, int]:
