@@ -30,6 +30,12 @@ DEVICE_FLAGS = [
     "-Wno-unused-variable",
     # Never select packed-FP32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: avoids AGPR<->VGPR copies around the
+    # softmax rescale and GEMM epilogues.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # No NaN inputs are assumed, so fmaxf needs no quieting canonicalisation
+    # (infinities are still honoured: padded keys use -inf).
+    "-fno-honor-nans",
 ]
 
 

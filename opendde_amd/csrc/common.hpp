@@ -130,6 +130,29 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Same reductions with the gfx950 lane-swap instructions (one v_permlane*_swap
+// each instead of an LDS-crossbar permute): after swapping a register with a
+// copy of itself, the two results hold the values of lanes l and l^32 (or
+// l^16), so one max/add completes that butterfly step.
+__device__ __forceinline__ float swap32_max(float v) {
+  auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float swap16_max(float v) {
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float swap32_add(float v) {
+  auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float swap16_add(float v) {
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float group_max_fast(float v) { return swap32_max(swap16_max(v)); }
+__device__ __forceinline__ float group_sum_fast(float v) { return swap32_add(swap16_add(v)); }
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

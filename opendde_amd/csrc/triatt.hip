@@ -1,32 +1,117 @@
 // Triangle attention (starting node over a strided pair view) for gfx950.
 //
-// Three kernels, stream ordered:
-//   1. triatt_proj  — LayerNorm + one pass of bias-free projections per pair
-//                     row: q (pre-scaled by log2(e)/sqrt(D)), k, v, sigmoid(g),
-//                     the triangle bias (pre-scaled by log2(e)) and the
-//                     additive mask row, written in the layouts the core
-//                     reads with whole-fragment 16-byte loads.
-//   2. triatt_core  — flash-style attention: per (row i, head h, 32-query
-//                     tile) stream 32-key blocks, S^T = bias + mask + K Q^T
-//                     on MFMA (bias folded into the accumulator init), online
-//                     softmax in fp32 with exp2, O^T += V^T P^T on MFMA with
-//                     P kept in registers; epilogue 1/l and the sigmoid gate.
-//                     The N x N x N logits never touch memory.
-//   3. triatt_out   — o W_o^T on MFMA plus the residual add, written through
-//                     the (possibly transposed) output strides.
+// Kernels, stream ordered:
+//   0. triatt_prep   — per pair row: does it keep any key?  Initialises the
+//                      per-row flags and the bound accumulators.
+//   1. triatt_proj   — LayerNorm + one pass of bias-free projections per pair
+//                      row: q (pre-scaled by log2(e)/sqrt(D)), k, v (zeroed on
+//                      masked keys of rows that keep some key), sigmoid(g),
+//                      the triangle bias (pre-scaled by log2(e)), the additive
+//                      mask row and per-key keep flags, plus max |k| per
+//                      (row, head) and max bias per (head, query).
+//   2a. triatt_core_fast — flash attention without a running max: with
+//                      s = q.k + bias (log2 units) bounded above by
+//                      |q| max|k| + max bias, p = exp2(s) cannot overflow
+//                      when that bound is small; masked keys drop out because
+//                      their v rows are zero and the row sum is
+//                      sum_k keep[k] p[k].  The only per-logit vector work
+//                      is one exp2, half a convert and half a dot2.  Rows
+//                      whose bound is too large, whose row sum underflows, or
+//                      that keep no key at all are flagged for 2b.
+//   2b. triatt_core_exact — online softmax with a running max and the exact
+//                      additive mask (inf*(mask-1)); runs only for flagged
+//                      rows (others exit at once).  A fully masked row gets a
+//                      uniform softmax, i.e. the mean of v, as in the
+//                      reference's float32 arithmetic.
+//   3. triatt_out    — o W_o^T on MFMA plus the residual add, written through
+//                      the (possibly transposed) output strides.
+// The N x N x N logits never touch memory.
 //
-// Workspace layouts (CT = compute type, Jp = N rounded up to 64):
+// Workspace layouts (CT = compute type, Jp = N rounded up to 64, I = rows):
 //   q, k, gate : [I][H][Jp][32]
-//   v          : [I][H][Jp/32][2][64][8]   MFMA-ready V^T fragments: block of
-//                32 keys x 32 channels; channel half db, lane (d%16 + 16*g),
-//                slot e holds key 4g+e (e<4) or 16+4g+(e-4) (e>=4)
-//   bias       : [Bb][H][Jp][Jp]   (log2e-scaled tri bias; Bb bias batches)
-//   mb         : [I][Jp] f32       (log2e-scaled additive mask; -inf on pads)
-//   o          : [I][Jp][H*32]     (gated attention output, module path)
+//   v          : [I][H][Jp/32][2][64][8]  MFMA-ready V^T fragments: per block
+//                of 32 keys, channel half db, lane (d%16 + 16*g), slot e holds
+//                key 4g+e (e<4) or 16+4g+(e-4) (e>=4)
+//   keep       : [I][Jp/32][4][8]          the same key-slot order, 1 = kept
+//   bias       : [Bb][H][Jp][Jp] f32       log2e-scaled tri bias (Bb batches)
+//   mb         : [I][Jp] f32               log2e-scaled additive mask, -inf pads
+//   mflag      : [I][Jp/32]                block holds a masked or padded key
+//   kmax       : [I][H]   (f32 bits)       max over keys of |k|
+//   bmax       : [Bb][H][Jp] (ordered int) max over keys of the bias row
+//   rowflag    : [I]                       row needs the exact path
+//   anykeep    : [I]                       row keeps at least one key
+//   o          : [I][Jp][H*32]             gated attention output (module path)
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "common.hpp"
 #include "runtime.hpp"
 
 namespace odde {
+
+// order-preserving float <-> int keys for atomicMax on signed values
+__device__ __forceinline__ int fkey(float f) {
+  const int b = __float_as_int(f);
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+  return v;
+}
+__device__ __forceinline__ float lanes16_max(float v) {
+#pragma unroll
+  for (int s = 1; s < 16; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+  return v;
+}
+
+__device__ __forceinline__ size_t vperm_offset(int row, int h, int heads, int jp, int j, int d) {
+  const int kb = j >> 5, jj = j & 31;
+  const int half = jj >> 4, gp = (jj & 15) >> 2, e = 4 * half + (jj & 3);
+  const int db = d >> 4, dl = d & 15;
+  return (((((size_t)row * heads + h) * (jp >> 5) + kb) * 2 + db) * 64 + dl + 16 * gp) * 8 + e;
+}
+// slot (g, e) of a 32-key block -> key offset within the block
+__device__ __forceinline__ int slot_key(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
+// key offset within a 32-key block -> index g*8+e of its slot
+__device__ __forceinline__ int key_slot(int jj) {
+  const int half = jj >> 4, gp = (jj & 15) >> 2;
+  return gp * 8 + 4 * half + (jj & 3);
+}
+
+constexpr float kFastBound = 100.0f;      // log2 units; exp2 overflows past 128
+constexpr float kUnderflowSum = 1e-30f;   // row sums below this go to the exact path
+
+// ---------------------------------------------------------------------------
+// 0. per-row preparation (module path): one workgroup per row
+// ---------------------------------------------------------------------------
+struct PrepArgs {
+  const float* mask;
+  int64_t m_s0, m_s1;
+  int* anykeep;
+  int* rowflag;
+  unsigned* kmax;
+  int* bmax;
+  int n, jp, heads;
+};
+
+__global__ __launch_bounds__(256) void triatt_prep_kernel(PrepArgs a) {
+  const int i = blockIdx.x;
+  int keep = 0;
+  for (int k = threadIdx.x; k < a.n; k += 256)
+    keep |= a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)k * a.m_s1] == 1.0f : 1;
+  keep = __syncthreads_or(keep);
+  if (threadIdx.x == 0) {
+    a.anykeep[i] = keep;
+    a.rowflag[i] = !keep;
+  }
+  if (threadIdx.x < a.heads) {
+    a.kmax[i * a.heads + threadIdx.x] = 0u;
+    a.bmax[threadIdx.x * a.jp + i] = fkey(-INFINITY);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // 1. projection
@@ -48,20 +133,18 @@ struct TriattProjArgs {
   CT* k;
   CT* v;
   CT* gate;
-  CT* bias;
+  CT* keep;
+  float* bias;
   float* mb;
+  int* mflag;
+  unsigned* kmax;
+  int* bmax;
+  const int* anykeep;
   int n, jp, heads;
   float q_scale;   // log2(e) / sqrt(D)
   float mask_inf;  // inf * log2(e)
   float eps;
 };
-
-__device__ __forceinline__ size_t vperm_offset(int row, int h, int heads, int jp, int j, int d) {
-  const int kb = j >> 5, jj = j & 31;
-  const int half = jj >> 4, gp = (jj & 15) >> 2, e = 4 * half + (jj & 3);
-  const int db = d >> 4, dl = d & 15;
-  return (((((size_t)row * heads + h) * (jp >> 5) + kb) * 2 + db) * 64 + dl + 16 * gp) * 8 + e;
-}
 
 template <typename ZT, typename CT, int kC>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
@@ -77,7 +160,35 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 
   const int H = a.heads, HD = H * 32, jp = a.jp;
 
+  // mask row: additive form for the exact core, keep flags for the fast one
+  __shared__ float keep_s[64];
+  __shared__ int wmasked[4];
+  float mv = -INFINITY, kp = 0.f;
+  if (valid) {
+    const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
+    mv = (m - 1.0f) * a.mask_inf;
+    kp = m == 1.0f ? 1.f : 0.f;
+  }
+  if (g == 0) {
+    a.mb[(size_t)i * jp + jl] = mv;
+    keep_s[w * 16 + r16] = kp;
+  }
+  const bool any_masked = __any(mv != 0.f);
+  if (l == 0) wmasked[w] = any_masked ? 1 : 0;
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const int b = threadIdx.x;  // 32-key block b of this 64-key tile = waves 2b, 2b+1
+    a.mflag[(size_t)i * (jp >> 5) + blockIdx.x * 2 + b] = wmasked[2 * b] | wmasked[2 * b + 1];
+  }
+  if (threadIdx.x < 64) {
+    const int t = threadIdx.x, kb = t >> 5, s = t & 31;
+    a.keep[((size_t)i * (jp >> 5) + blockIdx.x * 2 + kb) * 32 + s] =
+        from_f32<CT>(keep_s[kb * 32 + slot_key(s >> 3, s & 7)]);
+  }
+  const bool zero_v = a.anykeep[i] != 0;
+
   // q, k, gate: product W x^T -> lane holds pair row jl, channels o..o+3.
+  float ss = 0.f;
   for (int ob = 0; ob < HD / 16; ++ob) {
     f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ak = aq, ag = aq;
 #pragma unroll
@@ -97,10 +208,19 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     store4(a.q + off, aq[0] * s, aq[1] * s, aq[2] * s, aq[3] * s);
     store4(a.k + off, ak[0], ak[1], ak[2], ak[3]);
     store4(a.gate + off, sigmoidf_(ag[0]), sigmoidf_(ag[1]), sigmoidf_(ag[2]), sigmoidf_(ag[3]));
+    ss += ak[0] * ak[0] + ak[1] * ak[1] + ak[2] * ak[2] + ak[3] * ak[3];
+    if (ob & 1) {  // the 32 channels of head ob/2 are complete
+      const float nrm = lanes16_max(sqrtf(group_sum_fast(ss)));
+      if (l == 0) atomicMax(&a.kmax[i * H + (ob >> 1)], __float_as_uint(nrm));
+      ss = 0.f;
+    }
   }
 
   // v: product x W^T -> lane holds channel o, pair rows j0+4g .. +3.
   const int jb = j0 + 4 * g;
+  float vk[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) vk[e] = zero_v ? keep_s[w * 16 + 4 * g + e] : 1.f;
   for (int ob = 0; ob < HD / 16; ++ob) {
     f32x4 av = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -110,7 +230,8 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
       mma(av, x[t], f);
     }
     const int o = ob * 16 + r16;
-    store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), av[0], av[1], av[2], av[3]);
+    store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), av[0] * vk[0], av[1] * vk[1],
+           av[2] * vk[2], av[3] * vk[3]);
   }
 
   // triangle bias: channel h = r16 (< H), rows jb..jb+3 -> bias[h][i][jb..]
@@ -122,142 +243,443 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
       load_w_frag(a.wb, C, 0, H, t, f);
       mma(ab, x[t], f);
     }
+    const float s = kLog2e;
+    const float bm = group_max_fast(fmaxf(fmaxf(ab[0], ab[1]), fmaxf(ab[2], ab[3])) * s);
     if (r16 < H) {
-      const float s = kLog2e;
       store4(a.bias + ((size_t)r16 * jp + i) * jp + jb, ab[0] * s, ab[1] * s, ab[2] * s,
              ab[3] * s);
+      if (g == 0) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
     }
-  }
-
-  // additive mask row: mb[i][j] = inf*(mask-1)*log2e, -inf past the last token
-  if (g == 0) {
-    float v = -INFINITY;
-    if (valid) {
-      const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
-      v = (m - 1.0f) * a.mask_inf;
-    }
-    a.mb[(size_t)i * jp + jl] = v;
   }
 }
 
 // ---------------------------------------------------------------------------
-// 2. flash core
+// 2. flash cores
 // ---------------------------------------------------------------------------
 template <typename CT>
 struct TriattCoreArgs {
   const CT* q;
   const CT* k;
   const CT* v;
-  const CT* bias;
-  const float* mb;
-  const CT* gate;  // may be null
+  const CT* keep;
+  const float* bias;  // [Bb][H][Jp][Jp] f32, log2e-scaled
+  const float* mb;    // [rows][Jp] f32, log2e-scaled additive mask, -inf on pads
+  const int* mflag;   // [rows][Jp/32] nonzero if that key block needs the mask
+  const unsigned* kmax;
+  const int* bmax;
+  int* rowflag;
+  const CT* gate;     // may be null
   CT* out;
   int64_t o_row, o_h, o_j;  // element strides of out[row][h][q][d]
   int rows, heads, n, jp, rows_per_bias;
 };
 
-template <typename CT>
-__global__ __launch_bounds__(256) void triatt_core_kernel(TriattCoreArgs<CT> a) {
-  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
-  const int row = blockIdx.y * 4 + w;
-  if (row >= a.rows) return;  // no barriers in this kernel: an early exit is safe
-  const int h = blockIdx.z;
-  const int q0 = blockIdx.x * 32;
-  const int jp = a.jp, n = a.n;
-  const size_t rh = (size_t)row * a.heads + h;
-  const CT* Q = a.q + rh * jp * 32;
-  const CT* K = a.k + rh * jp * 32;
-  const CT* V = a.v + rh * jp * 32;
-  const CT* B = a.bias + ((size_t)(row / a.rows_per_bias) * a.heads + h) * jp * jp;
-  const float* MB = a.mb + (size_t)row * jp;
-
-  Frag<CT> qf[2];
-  const CT* brow[2];
+// Row sums of the probabilities: bf16 pairs through v_dot2 (the same rounded
+// values the PV product consumes), f32 by fused multiply-adds.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float psum8(const Frag<bf16>& p, const Frag<bf16>& wgt, float acc) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qq = q0 + 16 * qb + r16;
-    qf[qb].load(Q + (size_t)qq * 32 + 8 * g);
-    brow[qb] = B + (size_t)min(qq, n - 1) * jp;
+  for (int e = 0; e < 8; e += 2) {
+    bf16x2_t pr = {p.v[e], p.v[e + 1]};
+    bf16x2_t wr = {wgt.v[e], wgt.v[e + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, wr, acc, false);
+  }
+  return acc;
+}
+__device__ __forceinline__ float psum8(const Frag<float>& p, const Frag<float>& wgt, float acc) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf(p.get(e), wgt.get(e), acc);
+  return acc;
+}
+__device__ __forceinline__ Frag<bf16> ones_frag(bf16) {
+  Frag<bf16> f;
+  for (int e = 0; e < 8; ++e) f.v[e] = (bf16)1.0f;
+  return f;
+}
+__device__ __forceinline__ Frag<float> ones_frag(float) {
+  Frag<float> f;
+  f.lo = f32x4{1.f, 1.f, 1.f, 1.f};
+  f.hi = f.lo;
+  return f;
+}
+
+// Epilogue shared by both cores: 1/l, sigmoid gate, store.
+template <typename CT, int R, int QB>
+__device__ __forceinline__ void core_store(const TriattCoreArgs<CT>& a, int row0, int h, int q0,
+                                           f32x4 (&o)[R][2][QB], const float (&inv)[R][QB]) {
+  const int g = lane_id() >> 4, r16 = lane_id() & 15;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qq = q0 + 16 * qb + r16;
+      if (row >= a.rows || qq >= a.n) continue;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const int d0 = 16 * db + 4 * g;
+        float ov[4];
+        for (int e = 0; e < 4; ++e) ov[e] = o[r][db][qb][e] * inv[r][qb];
+        if (a.gate) {
+          float gv[4];
+          load4(a.gate + (((size_t)row * a.heads + h) * a.jp + qq) * 32 + d0, gv);
+          for (int e = 0; e < 4; ++e) ov[e] *= gv[e];
+        }
+        store4(a.out + (int64_t)row * a.o_row + (int64_t)h * a.o_h + (int64_t)qq * a.o_j + d0,
+               ov[0], ov[1], ov[2], ov[3]);
+      }
+    }
+  }
+}
+
+// LDS staging of one 32-key block for a workgroup: K and V blocks of its
+// R_WG rows, their keep flags, and the f32 bias tile of its Q_WG queries.
+// 16-byte chunks are placed so that fragment reads are bank-conflict free:
+// a K key row's chunks are xor-swizzled by (key / 4) % 4 (bf16), a bias row's
+// eight chunks by q % 8.
+template <typename CT, int R_WG, int Q_WG>
+struct CoreStage {
+  static constexpr int VEC = 16 / sizeof(CT);        // elements per chunk
+  static constexpr int KCH = 32 / VEC;               // chunks per key row (4 bf16, 8 f32)
+  static constexpr int K_CHUNKS = R_WG * 32 * KCH;   // K (and V) chunks per stage
+  static constexpr int KP_CHUNKS = R_WG * KCH;       // keep chunks (32 flags per row)
+  static constexpr int B_CHUNKS = Q_WG * 8;          // bias chunks (32 f32 per query)
+  static constexpr int TOTAL = 2 * K_CHUNKS + KP_CHUNKS + B_CHUNKS;
+  f32x4 k[K_CHUNKS];
+  f32x4 v[K_CHUNKS];
+  f32x4 kp[KP_CHUNKS];
+  f32x4 b[B_CHUNKS];
+};
+
+__device__ __forceinline__ int kswz(int key, int chunk, int kch) {
+  return kch == 4 ? (chunk ^ ((key >> 2) & 3)) : chunk;
+}
+
+// One workgroup = RG x QS waves over R_WG = RG*R rows and Q_WG = QS*16*QB
+// queries of one head.  Per 32-key block the workgroup stages K, V, keep and
+// the bias tile in LDS once (double buffered, loads for block t+1 in flight
+// while block t is computed), so each byte fetched from L2 feeds R_WG rows x
+// Q_WG queries.  Wave (rg, qs) owns rows rg*R.. and queries qs*16*QB..: S^T =
+// K Q^T on MFMA with the accumulator initialised from the bias fragment
+// (shared by its R rows), p = exp2(s), row sums sum_k keep[k] p[k] by dot2,
+// O^T += V^T P^T on MFMA.
+template <typename CT, int R, int QB, int RG, int QS>
+__global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a) {
+  constexpr int NT = 64 * RG * QS;
+  constexpr int R_WG = RG * R, Q_WG = QS * 16 * QB;
+  typedef CoreStage<CT, R_WG, Q_WG> Stage;
+  constexpr int VEC = Stage::VEC, KCH = Stage::KCH;
+  constexpr int ROUNDS = (Stage::TOTAL + NT - 1) / NT;
+  __shared__ Stage st[2];
+
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int rg = w / QS, qs = w % QS;
+  const int h = blockIdx.z;
+  const int jp = a.jp, n = a.n;
+  const int wg_row0 = blockIdx.y * R_WG;
+  const int wg_q0 = blockIdx.x * Q_WG;
+  const int row0 = wg_row0 + rg * R;
+  const int q0 = wg_q0 + qs * 16 * QB;
+  const int bb = min(wg_row0, a.rows - 1) / a.rows_per_bias;
+  const float* B = a.bias + ((size_t)bb * a.heads + h) * jp * jp;
+
+  // ---- staging plan: this thread's chunks (same for every key block) ----
+  const CT* src[ROUNDS];
+  int dst[ROUNDS];  // chunk index into the stage, or -1
+#pragma unroll
+  for (int rd = 0; rd < ROUNDS; ++rd) {
+    int idx = rd * NT + threadIdx.x;
+    src[rd] = nullptr;
+    dst[rd] = -1;
+    if (idx < 2 * Stage::K_CHUNKS) {  // K then V
+      const bool isv = idx >= Stage::K_CHUNKS;
+      if (isv) idx -= Stage::K_CHUNKS;
+      const int rr = idx / (32 * KCH), key = (idx / KCH) % 32, ch = idx % KCH;
+      const int row = min(wg_row0 + rr, a.rows - 1);
+      const size_t rh = (size_t)row * a.heads + h;
+      if (!isv) {
+        src[rd] = a.k + (rh * jp + key) * 32 + ch * VEC;
+        dst[rd] = (rr * 32 + key) * KCH + kswz(key, ch, KCH);
+      } else {  // V blocks are already in fragment order: copy 1:1
+        src[rd] = a.v + rh * jp * 32 + idx % (32 * KCH) * VEC;
+        dst[rd] = Stage::K_CHUNKS + idx;
+      }
+    } else if ((idx -= 2 * Stage::K_CHUNKS) < Stage::KP_CHUNKS) {
+      const int rr = idx / KCH, ch = idx % KCH;
+      const int row = min(wg_row0 + rr, a.rows - 1);
+      src[rd] = a.keep + (size_t)row * jp + ch * VEC;
+      dst[rd] = 2 * Stage::K_CHUNKS + idx;
+    } else if ((idx -= Stage::KP_CHUNKS) < Stage::B_CHUNKS) {
+      const int qq = idx >> 3, ch = idx & 7;
+      const int qrow = min(min(wg_q0 + qq, n - 1), jp - 1);
+      src[rd] = reinterpret_cast<const CT*>(B + (size_t)qrow * jp + ch * 4);
+      dst[rd] = 2 * Stage::K_CHUNKS + Stage::KP_CHUNKS + qq * 8 + (ch ^ (qq & 7));
+    }
+  }
+  // per key block the K/V/keep sources advance by 32 keys, bias sources by 32 f32
+  auto advance = [&](int rd, int k0) -> const f32x4* {
+    const int idx = rd * NT + threadIdx.x;
+    size_t step;
+    if (idx < Stage::K_CHUNKS) step = (size_t)k0 * 32;                  // K rows
+    else if (idx < 2 * Stage::K_CHUNKS) step = (size_t)k0 * 32;         // V blocks (1024/32 keys)
+    else if (idx < 2 * Stage::K_CHUNKS + Stage::KP_CHUNKS) step = (size_t)k0;
+    else step = (size_t)k0 * sizeof(float) / sizeof(CT);
+    return reinterpret_cast<const f32x4*>(src[rd] + step);
+  };
+  f32x4 stage_reg[ROUNDS];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int rd = 0; rd < ROUNDS; ++rd)
+      if (dst[rd] >= 0) stage_reg[rd] = *advance(rd, k0);
+  };
+  auto commit = [&](int buf) {
+    f32x4* base = reinterpret_cast<f32x4*>(&st[buf]);
+#pragma unroll
+    for (int rd = 0; rd < ROUNDS; ++rd)
+      if (dst[rd] >= 0) base[dst[rd]] = stage_reg[rd];
+  };
+
+  // ---- per-wave state ----
+  int rr[R];
+  bool skip = true;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rr[r] = min(row0 + r, a.rows - 1);
+    skip = skip && (row0 + r >= a.rows || a.rowflag[rr[r]] != 0);
+  }
+  Frag<CT> qf[R][QB];
+  bool over = false;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qq = min(q0 + 16 * qb + r16, jp - 1);
+    const float bq = fkey_inv(a.bmax[((size_t)bb * a.heads + h) * jp + min(qq, n - 1)]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      qf[r][qb].load(a.q + (((size_t)rr[r] * a.heads + h) * jp + qq) * 32 + 8 * g);
+      float q2 = 0.f;
+      for (int e = 0; e < 8; ++e) q2 += qf[r][qb].get(e) * qf[r][qb].get(e);
+      const float km = __uint_as_float(a.kmax[(size_t)rr[r] * a.heads + h]);
+      over = over || (sqrtf(group_sum_fast(q2)) * km + bq > kFastBound);
+    }
+  }
+  if (__any(over) && !skip) {
+    if (l < R && row0 + l < a.rows) a.rowflag[row0 + l] = 1;
+    skip = true;
   }
 
-  f32x4 o[2][2];
+  f32x4 o[R][2][QB];
+  float lsum[R][QB];
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
-    for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {-1e30f, -1e30f};
-  float lsum[2] = {0.f, 0.f};
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      o[r][0][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      o[r][1][qb] = o[r][0][qb];
+      lsum[r][qb] = 0.f;
+    }
+
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  const int nblk = jp >> 5;
+  for (int t = 0; t < nblk; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < nblk) fetch((t + 1) * 32);
+    if (!skip) {
+      const Stage& S = st[buf];
+      const CT* Ks = reinterpret_cast<const CT*>(S.k);
+      const CT* Vs = reinterpret_cast<const CT*>(S.v);
+      const CT* KPs = reinterpret_cast<const CT*>(S.kp);
+      const float* Bs = reinterpret_cast<const float*>(S.b);
+      f32x4 bfr[2][QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int ql = qs * 16 * QB + 16 * qb + r16;  // query row within the tile
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          bfr[kb][qb] = *reinterpret_cast<const f32x4*>(Bs + (ql * 8 + ((4 * kb + g) ^ (ql & 7))) * 4);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int lr = rg * R + r;  // row within the workgroup
+        Frag<CT> kf[2], vf[2], kpf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int key = 16 * kb + r16;
+          if constexpr (KCH == 4) {
+            kf[kb].load(Ks + ((lr * 32 + key) * KCH + kswz(key, g, KCH)) * VEC);
+          } else {
+            kf[kb].load(Ks + (lr * 32 + key) * 32 + 8 * g);
+          }
+          vf[kb].load(Vs + ((size_t)lr * 1024 + (kb * 64 + l) * 8));
+        }
+        kpf.load(KPs + lr * 32 + 8 * g);
+        f32x4 s[2][QB];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            s[kb][qb] = bfr[kb][qb];
+            mma(s[kb][qb], kf[kb], qf[r][qb]);
+          }
+        Frag<CT> pf[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e]));
+          lsum[r][qb] = psum8(pf[qb], kpf, lsum[r][qb]);
+        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+      }
+    }
+    if (t + 1 < nblk) commit(buf ^ 1);
+    __syncthreads();
+  }
+  if (skip) return;
+
+  float inv[R][QB];
+  bool under = false;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float lt = group_sum_fast(lsum[r][qb]);
+      under = under || !(lt >= kUnderflowSum);
+      inv[r][qb] = 1.0f / lt;
+    }
+  if (__any(under) && l < R && row0 + l < a.rows) a.rowflag[row0 + l] = 1;
+  if (q0 >= jp) return;
+  core_store<CT, R, QB>(a, row0, h, q0, o, inv);
+}
+
+// Exact online softmax (running max, additive mask as in the reference), run
+// for the rows the fast core flagged; every other wave exits at once.
+template <typename CT, int R, int QB>
+__global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<CT> a) {
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int row0 = (blockIdx.y * 4 + w) * R;
+  if (row0 >= a.rows) return;
+  int rr[R];
+  bool any_flagged = false;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rr[r] = __builtin_amdgcn_readfirstlane(min(row0 + r, a.rows - 1));
+    any_flagged = any_flagged || (row0 + r < a.rows && a.rowflag[rr[r]] != 0);
+  }
+  if (!any_flagged) return;
+  const int h = blockIdx.z;
+  const int q0 = blockIdx.x * (16 * QB);
+  const int jp = a.jp, n = a.n;
+  const float* B = a.bias + ((size_t)(row0 / a.rows_per_bias) * a.heads + h) * jp * jp;
+
+  const CT* Qp[R];
+  const CT* Kp[R];
+  const CT* Vp[R];
+  const float* MBp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const size_t rh = (size_t)rr[r] * a.heads + h;
+    Qp[r] = a.q + rh * jp * 32;
+    Kp[r] = a.k + rh * jp * 32;
+    Vp[r] = a.v + rh * jp * 32;
+    MBp[r] = a.mb + (size_t)rr[r] * jp;
+  }
+  Frag<CT> qf[R][QB];
+  const float* brow[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qq = q0 + 16 * qb + r16;
+    brow[qb] = B + (size_t)min(qq, n - 1) * jp + 4 * g;
+#pragma unroll
+    for (int r = 0; r < R; ++r) qf[r][qb].load(Qp[r] + (size_t)qq * 32 + 8 * g);
+  }
+  const Frag<CT> ones = ones_frag(CT());
+
+  f32x4 o[R][2][QB];
+  float m[R][QB], lsum[R][QB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      o[r][0][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      o[r][1][qb] = o[r][0][qb];
+      m[r][qb] = -1e30f;
+      lsum[r][qb] = 0.f;
+    }
 
   for (int k0 = 0; k0 < jp; k0 += 32) {
-    Frag<CT> kf[2];
-    float mbv[2][4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      kf[kb].load(K + (size_t)(k0 + 16 * kb + r16) * 32 + 8 * g);
-      load4(MB + k0 + 16 * kb + 4 * g, mbv[kb]);
-    }
-    f32x4 s[2][2];
+    f32x4 bfr[2][QB];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        float bv[4];
-        load4(brow[qb] + k0 + 16 * kb + 4 * g, bv);
-        s[kb][qb] = f32x4{bv[0] + mbv[kb][0], bv[1] + mbv[kb][1], bv[2] + mbv[kb][2],
-                          bv[3] + mbv[kb][3]};
-        mma(s[kb][qb], kf[kb], qf[qb]);
+      for (int qb = 0; qb < QB; ++qb)
+        bfr[kb][qb] = *reinterpret_cast<const f32x4*>(brow[qb] + k0 + 16 * kb);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      Frag<CT> kf[2], vf[2];
+      f32x4 mbv[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        kf[kb].load(Kp[r] + (size_t)(k0 + 16 * kb + r16) * 32 + 8 * g);
+        vf[kb].load(Vp[r] + (size_t)(k0 >> 5) * 1024 + (kb * 64 + l) * 8);
+        mbv[kb] = *reinterpret_cast<const f32x4*>(MBp[r] + k0 + 16 * kb + 4 * g);
       }
-    Frag<CT> pf[2];
+      f32x4 s[2][QB];
+      if (a.mflag[(size_t)rr[r] * (jp >> 5) + (k0 >> 5)]) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      float mx = s[0][qb][0];
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][qb][r]);
-      mx = group_max(mx);
-      const float mnew = fmaxf(m[qb], mx);
-      const float sc = __builtin_amdgcn_exp2f(m[qb] - mnew);
-      m[qb] = mnew;
-      float ps = 0.f;
+          for (int qb = 0; qb < QB; ++qb) {
+            s[kb][qb] = bfr[kb][qb] + mbv[kb];
+            mma(s[kb][qb], kf[kb], qf[r][qb]);
+          }
+      } else {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(s[kb][qb][r] - mnew);
-          ps += p;
-          pf[qb].set(4 * kb + r, p);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            s[kb][qb] = bfr[kb][qb];
+            mma(s[kb][qb], kf[kb], qf[r][qb]);
+          }
+      }
+      Frag<CT> pf[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float mx = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
+                         fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3])));
+        mx = group_max_fast(mx);
+        if (__any(mx > m[r][qb])) {
+          const float mnew = fmaxf(m[r][qb], mx);
+          const float sc = __builtin_amdgcn_exp2f(m[r][qb] - mnew);
+          m[r][qb] = mnew;
+          lsum[r][qb] *= sc;
+          o[r][0][qb] *= sc;
+          o[r][1][qb] *= sc;
         }
-      lsum[qb] = lsum[qb] * sc + ps;
+        const float mm = m[r][qb];
 #pragma unroll
-      for (int db = 0; db < 2; ++db) o[db][qb] *= sc;
-    }
-    const CT* vb = V + (size_t)(k0 >> 5) * 1024;
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      Frag<CT> vf;
-      vf.load(vb + (db * 64 + l) * 8);
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], vf, pf[qb]);
-    }
-  }
-
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float inv = 1.0f / group_sum(lsum[qb]);
-    const int qq = q0 + 16 * qb + r16;
-    if (qq >= n) continue;
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      const int d0 = 16 * db + 4 * g;
-      float ov[4];
-      for (int r = 0; r < 4; ++r) ov[r] = o[db][qb][r] * inv;
-      if (a.gate) {
-        float gv[4];
-        load4(a.gate + (rh * jp + qq) * 32 + d0, gv);
-        for (int r = 0; r < 4; ++r) ov[r] *= gv[r];
+          for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e] - mm));
+        lsum[r][qb] = psum8(pf[qb], ones, lsum[r][qb]);
       }
-      store4(a.out + (int64_t)row * a.o_row + (int64_t)h * a.o_h + (int64_t)qq * a.o_j + d0,
-             ov[0], ov[1], ov[2], ov[3]);
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
     }
   }
+  float inv[R][QB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) inv[r][qb] = 1.0f / group_sum_fast(lsum[r][qb]);
+  core_store<CT, R, QB>(a, row0, h, q0, o, inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -279,7 +701,7 @@ template <typename ZT, typename CT, int kHD>
 __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a) {
   constexpr int HD = kHD * 32;
   const int i = blockIdx.y;
-  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
   const int jl = blockIdx.x * 64 + w * 16 + r16;
   const bool valid = jl < a.n;
   Frag<CT> x[kHD];
@@ -307,7 +729,7 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
 }
 
 // ---------------------------------------------------------------------------
-// 4. relayout for the core-only slot: strided q/k/v/bias/mask -> core layouts
+// 4. core-only slot: strided q/k/v/bias/mask -> core layouts
 // ---------------------------------------------------------------------------
 template <typename CT>
 struct RelayoutArgs {
@@ -316,42 +738,62 @@ struct RelayoutArgs {
   const CT* v; int64_t v_sb, v_si, v_sh, v_sj;
   const float* bias; int64_t b_sb, b_sh, b_sq, b_sk;
   const uint8_t* mask; int64_t m_sb, m_si, m_sk;
-  CT* wq; CT* wk; CT* wv; CT* wbias; float* wmb;
+  CT* wq; CT* wk; CT* wv; CT* wkeep; float* wbias; float* wmb;
+  int* anykeep; int* rowflag; unsigned* kmax; int* bmax;
   int batch, rows, heads, n, jp;
   float q_scale, mask_inf;
 };
 
-// One thread per (row r = b*I+i, head h, key j) moves 32 channels of q, k, v;
-// threads with h == 0 also write the additive mask row.
+// One workgroup per flattened row r = b*I + i: keep test and initialisation.
+template <typename CT>
+__global__ __launch_bounds__(256) void triatt_slot_prep_kernel(RelayoutArgs<CT> a) {
+  const int r = blockIdx.x;
+  const int b = r / a.rows, i = r % a.rows;
+  int keep = 0;
+  for (int k = threadIdx.x; k < a.n; k += 256)
+    keep |= a.mask ? a.mask[b * a.m_sb + i * a.m_si + (int64_t)k * a.m_sk] != 0 : 1;
+  keep = __syncthreads_or(keep);
+  if (threadIdx.x == 0) {
+    a.anykeep[r] = keep;
+    a.rowflag[r] = !keep;
+  }
+  if (threadIdx.x < a.heads) a.kmax[r * a.heads + threadIdx.x] = 0u;
+}
+
+// One thread per (row r, head h, key j): 32 channels of q, k, v; max |k| per
+// (row, head) via one atomic per wave (a wave holds 64 keys of one (r, h));
+// threads with h == 0 also write the mask row and keep flags.
 template <typename CT>
 __global__ __launch_bounds__(256) void triatt_relayout_kernel(RelayoutArgs<CT> a) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)a.batch * a.rows * a.heads * a.jp;
-  if (tid >= total) return;
+  if (tid >= total) return;  // jp % 64 == 0: whole waves exit together
   const int j = (int)(tid % a.jp);
   const int h = (int)((tid / a.jp) % a.heads);
   const int64_t r = tid / ((int64_t)a.jp * a.heads);
   const int b = (int)(r / a.rows), i = (int)(r % a.rows);
   const bool valid = j < a.n;
+  const bool keep = valid && (a.mask ? a.mask[b * a.m_sb + i * a.m_si + (int64_t)j * a.m_sk] != 0 : true);
+  const float vmul = (a.anykeep[r] && !keep) ? 0.f : 1.f;
   const size_t off = (((size_t)r * a.heads + h) * a.jp + j) * 32;
   const CT* qs = a.q + b * a.q_sb + i * a.q_si + h * a.q_sh + (int64_t)(valid ? j : 0) * a.q_sj;
   const CT* ks = a.k + b * a.k_sb + i * a.k_si + h * a.k_sh + (int64_t)(valid ? j : 0) * a.k_sj;
   const CT* vs = a.v + b * a.v_sb + i * a.v_si + h * a.v_sh + (int64_t)(valid ? j : 0) * a.v_sj;
+  float k2 = 0.f;
   for (int d = 0; d < 32; ++d) {
     const float qv = valid ? to_f32(qs[d]) * a.q_scale : 0.f;
     const float kv = valid ? to_f32(ks[d]) : 0.f;
-    const float vv = valid ? to_f32(vs[d]) : 0.f;
+    const float vv = valid ? to_f32(vs[d]) * vmul : 0.f;
+    k2 += kv * kv;
     a.wq[off + d] = from_f32<CT>(qv);
     a.wk[off + d] = from_f32<CT>(kv);
     a.wv[vperm_offset((int)r, h, a.heads, a.jp, j, d)] = from_f32<CT>(vv);
   }
+  const float km = wave_max(sqrtf(k2));
+  if (lane_id() == 0) atomicMax(&a.kmax[r * a.heads + h], __float_as_uint(km));
   if (h == 0) {
-    float mv = -INFINITY;
-    if (valid) {
-      const bool keep = a.mask ? a.mask[b * a.m_sb + i * a.m_si + (int64_t)j * a.m_sk] != 0 : true;
-      mv = keep ? 0.f : -a.mask_inf;
-    }
-    a.wmb[(size_t)r * a.jp + j] = mv;
+    a.wmb[(size_t)r * a.jp + j] = valid ? (keep ? 0.f : -a.mask_inf) : -INFINITY;
+    a.wkeep[(size_t)r * a.jp + (j & ~31) + key_slot(j & 31)] = from_f32<CT>(keep ? 1.f : 0.f);
   }
 }
 
@@ -369,7 +811,33 @@ __global__ __launch_bounds__(256) void triatt_bias_relayout_kernel(RelayoutArgs<
   float bv = 0.f;
   if (q < a.n && k < a.n)
     bv = a.bias[b * a.b_sb + h * a.b_sh + (int64_t)q * a.b_sq + (int64_t)k * a.b_sk] * kLog2e;
-  a.wbias[tid] = from_f32<CT>(bv);
+  a.wbias[tid] = bv;
+}
+
+// Max of each relaid bias row over its n keys (one thread per (b, h, q)).
+__global__ __launch_bounds__(256) void triatt_bmax_fold_kernel(const float* wbias, int* bmax,
+                                                               int bh_count, int n, int jp) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= (int64_t)bh_count * jp) return;
+  const int q = (int)(tid % jp);
+  const float* row = wbias + tid * jp;
+  float m = -INFINITY;
+  if (q < n)
+    for (int k = 0; k < n; ++k) m = fmaxf(m, row[k]);
+  bmax[tid] = fkey(m);
+}
+
+// One thread per (row, 32-key block): flag blocks whose additive mask row has
+// any nonzero entry (masked or padded keys).
+__global__ __launch_bounds__(256) void triatt_mflag_kernel(const float* mb, int* mflag, int rows,
+                                                           int jp) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = jp >> 5;
+  if (tid >= (int64_t)rows * nb) return;
+  const float* p = mb + (tid / nb) * jp + (tid % nb) * 32;
+  int any = 0;
+  for (int e = 0; e < 32; ++e) any |= p[e] != 0.f;
+  mflag[tid] = any;
 }
 
 }  // namespace odde
@@ -381,24 +849,39 @@ using namespace odde;
 
 namespace {
 
-struct TriattWs {
-  void* q; void* k; void* v; void* gate; void* o; void* bias; float* mb;
-  uint64_t bytes;
+struct CoreBufs {
+  void* q; void* k; void* v; void* keep; float* bias; float* mb; int* mflag;
+  unsigned* kmax; int* bmax; int* rowflag; int* anykeep;
 };
 
-TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int dt) {
-  const int jp = round_up(n, 64);
+// Workspace common to both entry points; `bias_batches` bias planes.
+void carve_core_bufs(Carver& c, CoreBufs& w, int rows, int heads, int jp, int bias_batches,
+                     int dt) {
   const uint64_t es = dtype_size(dt);
-  const uint64_t per = (uint64_t)n * heads * jp * 32;
-  Carver c(base, size);
-  TriattWs w;
+  const uint64_t per = (uint64_t)rows * heads * jp * 32;
   w.q = c.take<char>(per * es);
   w.k = c.take<char>(per * es);
   w.v = c.take<char>(per * es);
-  w.gate = c.take<char>(per * es);
-  w.o = c.take<char>(per * es);
-  w.bias = c.take<char>((uint64_t)heads * jp * jp * es);
-  w.mb = c.take<float>((uint64_t)n * jp);
+  w.keep = c.take<char>((uint64_t)rows * jp * es);
+  w.bias = c.take<float>((uint64_t)bias_batches * heads * jp * jp);
+  w.mb = c.take<float>((uint64_t)rows * jp);
+  w.mflag = c.take<int>((uint64_t)rows * (jp / 32));
+  w.kmax = c.take<unsigned>((uint64_t)rows * heads);
+  w.bmax = c.take<int>((uint64_t)bias_batches * heads * jp);
+  w.rowflag = c.take<int>((uint64_t)rows);
+  w.anykeep = c.take<int>((uint64_t)rows);
+}
+
+struct TriattWs { CoreBufs c; void* gate; void* o; uint64_t bytes; };
+
+TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int dt) {
+  const int jp = round_up(n, 64);
+  const uint64_t per = (uint64_t)n * heads * jp * 32 * dtype_size(dt);
+  Carver c(base, size);
+  TriattWs w;
+  carve_core_bufs(c, w.c, n, heads, jp, 1, dt);
+  w.gate = c.take<char>(per);
+  w.o = c.take<char>(per);
   w.bytes = (c.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -430,12 +913,70 @@ void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD>), grid, dim3(256), 0, st, p);
 }
 
+// Core tiling: waves own R rows x 16*QB queries; a workgroup of RG x QS
+// waves shares its staged K/V (R_WG = RG*R rows) and bias (Q_WG = QS*16*QB
+// queries).  The default was chosen by measurement on MI355X;
+// ODDE_TRIATT_TILE="R,QB,RG,QS" selects another instantiation.
+struct CoreTile { int r, qb, rg, qs; };
+
+CoreTile core_tile(int rows_per_bias, int batches, bool f32) {
+  // f32 fragments are twice as wide: the bf16 tile would spill
+  static CoreTile env = [] {
+    CoreTile d{0, 0, 0, 0};
+    if (const char* e = getenv("ODDE_TRIATT_TILE")) {
+      int r = 0, qb = 0, rg = 0, qs = 0;
+      if (sscanf(e, "%d,%d,%d,%d", &r, &qb, &rg, &qs) == 4) d = CoreTile{r, qb, rg, qs};
+    }
+    return d;
+  }();
+  const CoreTile t = env.r ? env : (f32 ? CoreTile{2, 2, 2, 4} : CoreTile{2, 4, 2, 4});
+  // all rows of a workgroup share one bias batch
+  if (batches > 1 && rows_per_bias % (t.r * t.rg) != 0) return CoreTile{1, t.qb, 1, t.qs};
+  return t;
+}
+
+template <typename CT, int R, int QB, int RG, int QS>
+void launch_core_t(const TriattCoreArgs<CT>& p, hipStream_t st) {
+  constexpr int R_WG = R * RG, Q_WG = 16 * QB * QS;
+  dim3 grid((p.jp + Q_WG - 1) / Q_WG, (p.rows + R_WG - 1) / R_WG, p.heads);
+  hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>), grid, dim3(64 * RG * QS), 0,
+                     st, p);
+  // the exact core keeps a modest tile: it only runs for flagged rows
+  dim3 grid2(p.jp / 32, (p.rows + 3) / 4, p.heads);
+  hipLaunchKernelGGL((triatt_core_exact_kernel<CT, 1, 2>), grid2, dim3(256), 0, st, p);
+}
+
 template <typename CT>
-int launch_core(const TriattCoreArgs<CT>& p, hipStream_t st) {
-  dim3 grid(p.jp / 32, (p.rows + 3) / 4, p.heads);
+int launch_core(const TriattCoreArgs<CT>& p, int batches, hipStream_t st) {
+  const CoreTile t = core_tile(p.rows_per_bias, batches, sizeof(CT) == 4);
   LaunchScope ls(ODDE_K_TRIATT_CORE, st);
-  hipLaunchKernelGGL((triatt_core_kernel<CT>), grid, dim3(256), 0, st, p);
+#define ODDE_TILE(R, QB, RG, QS)                                              \
+  else if (t.r == R && t.qb == QB && t.rg == RG && t.qs == QS)                \
+    launch_core_t<CT, R, QB, RG, QS>(p, st);
+  if (false) {}
+  ODDE_TILE(2, 4, 2, 4)
+  ODDE_TILE(2, 4, 2, 2)
+  ODDE_TILE(2, 2, 2, 4)
+  ODDE_TILE(2, 4, 1, 4)
+  ODDE_TILE(1, 4, 4, 2)
+  ODDE_TILE(2, 2, 4, 2)
+  ODDE_TILE(1, 4, 1, 4)
+  ODDE_TILE(1, 4, 1, 1)
+  ODDE_TILE(1, 2, 1, 4)
+  ODDE_TILE(1, 2, 1, 1)
+  else return set_error(ODDE_EINVAL, "ODDE_TRIATT_TILE: unsupported R,QB,RG,QS");
+#undef ODDE_TILE
   return check_launch("triatt_core");
+}
+
+template <typename CT>
+void fill_core_args(TriattCoreArgs<CT>& c, const CoreBufs& b) {
+  c.q = static_cast<const CT*>(b.q);
+  c.k = static_cast<const CT*>(b.k);
+  c.v = static_cast<const CT*>(b.v);
+  c.keep = static_cast<const CT*>(b.keep);
+  c.bias = b.bias; c.mb = b.mb; c.mflag = b.mflag; c.kmax = b.kmax; c.bmax = b.bmax;
+  c.rowflag = b.rowflag;
 }
 
 template <typename ZT, typename CT>
@@ -454,14 +995,19 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   p.wk = static_cast<const CT*>(a->w_k);
   p.wv = static_cast<const CT*>(a->w_v);
   p.wg = static_cast<const CT*>(a->w_g);
-  p.q = static_cast<CT*>(ws.q); p.k = static_cast<CT*>(ws.k); p.v = static_cast<CT*>(ws.v);
-  p.gate = static_cast<CT*>(ws.gate); p.bias = static_cast<CT*>(ws.bias); p.mb = ws.mb;
+  p.q = static_cast<CT*>(ws.c.q); p.k = static_cast<CT*>(ws.c.k); p.v = static_cast<CT*>(ws.c.v);
+  p.gate = static_cast<CT*>(ws.gate); p.keep = static_cast<CT*>(ws.c.keep);
+  p.bias = ws.c.bias; p.mb = ws.c.mb; p.mflag = ws.c.mflag; p.kmax = ws.c.kmax;
+  p.bmax = ws.c.bmax; p.anykeep = ws.c.anykeep;
   p.n = n; p.jp = jp; p.heads = H;
   p.q_scale = kLog2e / sqrtf((float)a->head_dim);
   p.mask_inf = a->inf * kLog2e;
   p.eps = a->eps;
   {
     LaunchScope ls(ODDE_K_TRIATT_PROJ, st);
+    PrepArgs pa{a->mask, a->mask_s0, a->mask_s1, ws.c.anykeep, ws.c.rowflag, ws.c.kmax,
+                ws.c.bmax, n, jp, H};
+    hipLaunchKernelGGL(triatt_prep_kernel, dim3(n), dim3(256), 0, st, pa);
     switch (C) {
       case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
       case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
@@ -474,11 +1020,12 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   }
 
   TriattCoreArgs<CT> c;
-  c.q = p.q; c.k = p.k; c.v = p.v; c.bias = p.bias; c.mb = p.mb; c.gate = p.gate;
+  fill_core_args(c, ws.c);
+  c.gate = static_cast<const CT*>(ws.gate);
   c.out = static_cast<CT*>(ws.o);
   c.o_row = (int64_t)jp * HD; c.o_h = 32; c.o_j = HD;
   c.rows = n; c.heads = H; c.n = n; c.jp = jp; c.rows_per_bias = n;
-  int rc = launch_core<CT>(c, st);
+  int rc = launch_core<CT>(c, 1, st);
   if (rc) return rc;
 
   TriattOutArgs<ZT, CT> o;
@@ -539,20 +1086,13 @@ int odde_triatt_fwd(const odde_triatt_args* a, void* stream) {
 // ---------------------------------------------------------------------------
 namespace {
 
-struct CoreWs { void* q; void* k; void* v; void* bias; float* mb; uint64_t bytes; };
+struct CoreWs { CoreBufs c; uint64_t bytes; };
 
 CoreWs carve_core(void* base, uint64_t size, const odde_triatt_core_args* a) {
   const int jp = round_up(a->n, 64);
-  const uint64_t es = dtype_size(a->dtype);
-  const uint64_t rows = (uint64_t)a->batch * a->rows;
-  const uint64_t per = rows * a->heads * jp * 32;
   Carver c(base, size);
   CoreWs w;
-  w.q = c.take<char>(per * es);
-  w.k = c.take<char>(per * es);
-  w.v = c.take<char>(per * es);
-  w.bias = c.take<char>((uint64_t)a->batch * a->heads * jp * jp * es);
-  w.mb = c.take<float>(rows * jp);
+  carve_core_bufs(c, w.c, a->batch * a->rows, a->heads, jp, a->batch, a->dtype);
   w.bytes = (c.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -564,6 +1104,7 @@ int check_core(const odde_triatt_core_args* a) {
   if (a->batch <= 0 || a->rows <= 0 || a->heads <= 0 || a->n <= 0)
     return set_error(ODDE_EINVAL, "triatt_core: sizes must be positive");
   if (a->head_dim != 32) return set_error(ODDE_EUNSUPPORTED, "triatt_core: head_dim must be 32");
+  if (a->heads > 256) return set_error(ODDE_EUNSUPPORTED, "triatt_core: at most 256 heads");
   if (!valid_dtype(a->dtype)) return set_error(ODDE_EINVAL, "triatt_core: bad dtype");
   return ODDE_OK;
 }
@@ -572,36 +1113,47 @@ template <typename CT>
 int run_core(const odde_triatt_core_args* a, hipStream_t st) {
   const int jp = round_up(a->n, 64);
   CoreWs ws = carve_core(a->workspace, a->workspace_bytes, a);
+  const int rows = a->batch * a->rows;
   RelayoutArgs<CT> r;
   r.q = static_cast<const CT*>(a->q); r.q_sb = a->q_sb; r.q_si = a->q_si; r.q_sh = a->q_sh; r.q_sj = a->q_sj;
   r.k = static_cast<const CT*>(a->k); r.k_sb = a->k_sb; r.k_si = a->k_si; r.k_sh = a->k_sh; r.k_sj = a->k_sj;
   r.v = static_cast<const CT*>(a->v); r.v_sb = a->v_sb; r.v_si = a->v_si; r.v_sh = a->v_sh; r.v_sj = a->v_sj;
   r.bias = a->bias; r.b_sb = a->b_sb; r.b_sh = a->b_sh; r.b_sq = a->b_sq; r.b_sk = a->b_sk;
   r.mask = a->mask; r.m_sb = a->m_sb; r.m_si = a->m_si; r.m_sk = a->m_sk;
-  r.wq = static_cast<CT*>(ws.q); r.wk = static_cast<CT*>(ws.k); r.wv = static_cast<CT*>(ws.v);
-  r.wbias = static_cast<CT*>(ws.bias); r.wmb = ws.mb;
+  r.wq = static_cast<CT*>(ws.c.q); r.wk = static_cast<CT*>(ws.c.k); r.wv = static_cast<CT*>(ws.c.v);
+  r.wkeep = static_cast<CT*>(ws.c.keep);
+  r.wbias = ws.c.bias; r.wmb = ws.c.mb;
+  r.anykeep = ws.c.anykeep; r.rowflag = ws.c.rowflag; r.kmax = ws.c.kmax; r.bmax = ws.c.bmax;
   r.batch = a->batch; r.rows = a->rows; r.heads = a->heads; r.n = a->n; r.jp = jp;
   r.q_scale = a->scale * kLog2e;
   r.mask_inf = a->inf_value * kLog2e;
   {
-    const int64_t total = (int64_t)a->batch * a->rows * a->heads * jp;
+    const int64_t total = (int64_t)rows * a->heads * jp;
     const int64_t total_b = (int64_t)a->batch * a->heads * jp * jp;
+    const int64_t nbh = (int64_t)a->batch * a->heads * jp;
+    const int64_t nflag = (int64_t)rows * (jp / 32);
     LaunchScope ls(ODDE_K_TRIATT_RELAYOUT, st);
+    hipLaunchKernelGGL((triatt_slot_prep_kernel<CT>), dim3(rows), dim3(256), 0, st, r);
     hipLaunchKernelGGL((triatt_relayout_kernel<CT>), dim3((unsigned)((total + 255) / 256)),
                        dim3(256), 0, st, r);
     hipLaunchKernelGGL((triatt_bias_relayout_kernel<CT>),
                        dim3((unsigned)((total_b + 255) / 256)), dim3(256), 0, st, r);
+    hipLaunchKernelGGL(triatt_bmax_fold_kernel, dim3((unsigned)((nbh + 255) / 256)), dim3(256),
+                       0, st, ws.c.bias, ws.c.bmax, a->batch * a->heads, a->n, jp);
+    hipLaunchKernelGGL(triatt_mflag_kernel, dim3((unsigned)((nflag + 255) / 256)), dim3(256), 0,
+                       st, ws.c.mb, ws.c.mflag, rows, jp);
     int rc = check_launch("triatt_relayout");
     if (rc) return rc;
   }
   TriattCoreArgs<CT> c;
-  c.q = r.wq; c.k = r.wk; c.v = r.wv; c.bias = r.wbias; c.mb = r.wmb; c.gate = nullptr;
+  fill_core_args(c, ws.c);
+  c.gate = nullptr;
   c.out = static_cast<CT*>(a->out);
-  c.o_row = a->o_si;  // rows are (b, i) with o_sb == rows * o_si checked by the caller
+  c.o_row = a->o_si;  // rows are (b, i): o_sb == rows * o_si is checked by the caller
   c.o_h = a->o_sh; c.o_j = a->o_sj;
-  c.rows = a->batch * a->rows; c.heads = a->heads; c.n = a->n; c.jp = jp;
+  c.rows = rows; c.heads = a->heads; c.n = a->n; c.jp = jp;
   c.rows_per_bias = a->rows;
-  return launch_core<CT>(c, st);
+  return launch_core<CT>(c, a->batch, st);
 }
 
 }  // namespace

@@ -177,3 +177,61 @@ def test_pairformer_block_fp32(inplace):
                      triangle_attention="hip", inplace_safe=inplace)
     assert_fp32(zg, ze, "block z")
     assert_fp32(sg, se, "block s")
+
+
+# ------------------------------------------- fast-path fallbacks (exact core)
+
+
+def _rel(got, exp):
+    g, e = got.double().cpu(), exp.double().cpu()
+    return float((g - e).abs().max() / e.abs().max())
+
+
+def test_triangle_attention_large_logits_take_exact_path():
+    # weights large enough that |q| max|k| exceeds the fast path's overflow
+    # bound: the rows are recomputed with a running max.
+    # Only rows that keep some key are compared: for a fully masked row with
+    # logits of hundreds of nats the reference's float32 result depends on how
+    # -1e9 + logit rounds (ulp 64), not on a well-defined limit.
+    n, pad = 72, 7
+    mod = seeded(TriangleAttention(128, 32, 4), 31, 0.6)
+    z = _z(n, 128, 32)
+    mask = token_pair_mask(n, pad)
+    exp = ref.triangle_attention(z, mask, params_of(mod), 4)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
+    r = _rel(got[: n - pad], exp[: n - pad])
+    say(f"    large-logit rel max err {r:.2e}")
+    # logits of hundreds of nats: a 1e-7 relative rounding difference in a
+    # logit moves its weight by ~1e-5, so the bound reflects conditioning;
+    # the overflowing fast path would be off by orders of magnitude
+    assert torch.isfinite(got).all() and r < 1e-3
+
+
+def test_triangle_attention_underflowing_rows_take_exact_path():
+    # LN offset 8 on every channel and tri-bias weights -0.5 make every logit
+    # about -8*0.5*128 = -512 nats: exp2 of the raw logits underflows to 0 and
+    # the rows must be recomputed with a running max.
+    n = 40
+    mod = seeded(TriangleAttention(128, 32, 4), 33, 0.05)
+    with torch.no_grad():
+        mod.layer_norm.bias.fill_(8.0)
+        mod.linear.weight.fill_(-0.5)
+    z = _z(n, 128, 34)
+    exp = ref.triangle_attention(z, None, params_of(mod), 4)
+    got = mod.to(DEV)(z.to(DEV), None, triangle_attention="hip")
+    r = _rel(got, exp)
+    say(f"    underflow rel max err {r:.2e}")
+    assert torch.isfinite(got).all() and r < 1e-5
+
+
+@pytest.mark.parametrize("n_pad", [0, 5, 39])
+def test_triangle_attention_fully_masked_rows_are_mean_of_v(n_pad):
+    # padded tokens give fully masked rows: the reference's float32 softmax of
+    # identical -1e9 logits is uniform, i.e. the mean of v over all keys
+    n = 40
+    mod = seeded(TriangleAttention(128, 32, 4), 35, STD)
+    z = _z(n, 128, 36)
+    mask = token_pair_mask(n, n_pad)
+    exp = ref.triangle_attention(z, mask, params_of(mod), 4)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
+    assert_fp32(got, exp, f"fully masked rows n_pad={n_pad}")
