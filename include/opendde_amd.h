@@ -45,7 +45,8 @@ extern "C" {
 #define ODDE_K_TRIMUL_CONTRACT 4
 #define ODDE_K_TRIMUL_OUT 5
 #define ODDE_K_TRIATT_RELAYOUT 6
-#define ODDE_K_COUNT 7
+#define ODDE_K_TRANSITION 7
+#define ODDE_K_COUNT 8
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -164,6 +165,34 @@ typedef struct odde_trimul_args {
 
 int odde_trimul_workspace_bytes(const odde_trimul_args* args, uint64_t* bytes);
 int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
+
+/*
+ * Fused SwiGLU transition on rows of c channels (block member of the pair
+ * stack; replaces Transition.forward, opendde/model/modules/primitives.py:
+ * 182-217, whose flat row chunking is numerically neutral):
+ *   y = LN(x); out = (add_residual ? x : 0) + (silu(y W_a^T) * (y W_b^T)) W_o^T
+ * x, out: [rows][c] contiguous (out may alias x); W_a, W_b: [n*c][c],
+ * W_o: [c][n*c] in compute_dtype (bf16 only); LN params f32.
+ */
+typedef struct odde_transition_args {
+  uint32_t struct_size;
+  int32_t c;
+  int32_t n_factor;
+  int32_t x_dtype;
+  int32_t compute_dtype;
+  int32_t add_residual;
+  int64_t rows;
+  const void* x;
+  void* out;
+  const float* ln_w;
+  const float* ln_b;
+  const void* w_a;
+  const void* w_b;
+  const void* w_o;
+  float eps;
+} odde_transition_args;
+
+int odde_transition_fwd(const odde_transition_args* args, void* hip_stream);
 
 /* Instrumentation (no counterpart in the reference): per-kernel launch
  * counters (always on), and optional HIP-event timing of every launch on the

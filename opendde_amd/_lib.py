@@ -24,10 +24,12 @@ F32, BF16 = 0, 1
 K_TRIATT_PROJ, K_TRIATT_CORE, K_TRIATT_OUT = 0, 1, 2
 K_TRIMUL_PROJ, K_TRIMUL_CONTRACT, K_TRIMUL_OUT = 3, 4, 5
 K_TRIATT_RELAYOUT = 6
+K_TRANSITION = 7
 KERNEL_NAMES = {
     K_TRIATT_PROJ: "triatt_proj", K_TRIATT_CORE: "triatt_core", K_TRIATT_OUT: "triatt_out",
     K_TRIMUL_PROJ: "trimul_proj", K_TRIMUL_CONTRACT: "trimul_contract",
     K_TRIMUL_OUT: "trimul_out", K_TRIATT_RELAYOUT: "triatt_relayout",
+    K_TRANSITION: "transition",
 }
 
 _i32, _i64, _u32, _u64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
@@ -78,6 +80,15 @@ class TrimulArgs(ctypes.Structure):
     ]
 
 
+class TransitionArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", _u32), ("c", _i32), ("n_factor", _i32), ("x_dtype", _i32),
+        ("compute_dtype", _i32), ("add_residual", _i32), ("rows", _i64),
+        ("x", _vp), ("out", _vp), ("ln_w", _vp), ("ln_b", _vp),
+        ("w_a", _vp), ("w_b", _vp), ("w_o", _vp), ("eps", _f32),
+    ]
+
+
 # Every symbol include/opendde_amd.h declares, with its ctypes signature.
 SYMBOLS = {
     "odde_abi_version": (_i32, []),
@@ -88,6 +99,7 @@ SYMBOLS = {
     "odde_triatt_core_fwd": (_i32, [ctypes.POINTER(TriattCoreArgs), _vp]),
     "odde_trimul_workspace_bytes": (_i32, [ctypes.POINTER(TrimulArgs), ctypes.POINTER(_u64)]),
     "odde_trimul_fwd": (_i32, [ctypes.POINTER(TrimulArgs), _vp]),
+    "odde_transition_fwd": (_i32, [ctypes.POINTER(TransitionArgs), _vp]),
     "odde_launch_count": (_i64, [_i32]),
     "odde_timing_enable": (_i32, [_i32]),
     "odde_timing_reset": (_i32, []),

@@ -1,0 +1,199 @@
+// Fused pair/single Transition (SwiGLU) for gfx950:
+//   y = LN(x);  h = silu(y W_a^T) * (y W_b^T);  out = (add ? x : 0) + h W_o^T
+// with hidden = NF * C.  One workgroup (4 waves) owns 128 rows at a time
+// (persistent); every wave keeps its 32 rows' LN fragments and 32 x C output
+// accumulators in registers while the hidden dimension is walked in chunks
+// of 32: the chunk's W_a / W_b rows and W_o columns are staged in LDS once
+// per workgroup, GEMM1 (W x^T orientation) leaves each lane with hidden units
+// {4g..4g+3, 16+4g..16+4g+3} of its row -- exactly the eight contraction slots
+// of a K32 B-operand fragment -- so silu(a)*b feeds GEMM2 straight from
+// registers (W_o fragments are read with the same slot order).  The hidden
+// activations never touch memory.
+#include <algorithm>
+
+#include "common.hpp"
+#include "rowtile.hpp"
+#include "runtime.hpp"
+
+namespace odde {
+
+template <typename ZT, typename CT>
+struct TransitionArgs {
+  const ZT* x;
+  ZT* out;
+  const float* ln_w;
+  const float* ln_b;
+  const CT* wa;  // [NF*C][C]
+  const CT* wb;  // [NF*C][C]
+  const CT* wo;  // [C][NF*C]
+  int64_t rows;
+  int add;
+  float eps;
+};
+
+constexpr int kTrRows = 128;  // rows per workgroup tile
+constexpr int kTrHid = 32;    // hidden units per chunk
+
+template <typename ZT, typename CT, int kC, int NF>
+__global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, CT> a,
+                                                            int64_t ntiles) {
+  constexpr int C = kC * 32, HID = NF * C, NCB = C / 16;
+  constexpr int LDX = TileLD<CT, C>::value;          // x tile / W_a, W_b chunk rows
+  constexpr int LDO = kTrHid + 16 / (int)sizeof(CT); // W_o chunk rows
+  __shared__ __attribute__((aligned(16))) CT xs[kTrRows * LDX];
+  __shared__ __attribute__((aligned(16))) CT wab[2 * kTrHid * LDX];
+  __shared__ __attribute__((aligned(16))) CT wos[C * LDO];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  constexpr int VEC = 16 / sizeof(CT);
+
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r0 = tile * kTrRows;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      stage_ln_tile<ZT, CT, C>(
+          [&](int r) -> const ZT* {
+            const int64_t row = r0 + half * 64 + r;
+            return row < a.rows ? a.x + row * C : nullptr;
+          },
+          a.ln_w, a.ln_b, a.eps, xs + half * 64 * LDX);
+    __syncthreads();
+    Frag<CT> xf[2][kC];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) tile_frags<CT, C>(xs, 2 * w + rb, xf[rb]);
+    f32x4 acc[2][NCB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int h0 = 0; h0 < HID; h0 += kTrHid) {
+      __syncthreads();  // previous chunk's weights fully consumed
+      // W_a, W_b rows h0..h0+31 (C each) and W_o columns h0..h0+31 (C rows)
+      for (int ci = threadIdx.x; ci < 2 * kTrHid * (C / VEC); ci += 256) {
+        const int m = ci / (kTrHid * (C / VEC)), rem = ci % (kTrHid * (C / VEC));
+        const int r = rem / (C / VEC), cc = (rem % (C / VEC)) * VEC;
+        const CT* src = (m ? a.wb : a.wa) + (size_t)(h0 + r) * C + cc;
+        *reinterpret_cast<f32x4*>(wab + (m * kTrHid + r) * LDX + cc) =
+            *reinterpret_cast<const f32x4*>(src);
+      }
+      for (int ci = threadIdx.x; ci < C * (kTrHid / VEC); ci += 256) {
+        const int r = ci / (kTrHid / VEC), cc = (ci % (kTrHid / VEC)) * VEC;
+        *reinterpret_cast<f32x4*>(wos + r * LDO + cc) =
+            *reinterpret_cast<const f32x4*>(a.wo + (size_t)r * HID + h0 + cc);
+      }
+      __syncthreads();
+      // weight fragments of this chunk (shared by the wave's two row blocks)
+      Frag<CT> fa[2][kC], fb[2][kC];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+          fa[hb][t].load(wab + (hb * 16 + r16) * LDX + 32 * t + 8 * g);
+          fb[hb][t].load(wab + (kTrHid + hb * 16 + r16) * LDX + 32 * t + 8 * g);
+        }
+      Frag<CT> fo[NCB];  // W_o[c][h0 + slot]: hidden 4g..4g+3 and 16+4g..16+4g+3
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const CT* row = wos + (cb * 16 + r16) * LDO;
+        float v[8];
+        load4(row + 4 * g, v);
+        load4(row + 16 + 4 * g, v + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fo[cb].set(e, v[e]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        Frag<CT> hf;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+          for (int t = 0; t < kC; ++t) {
+            mma(sa, fa[hb][t], xf[rb][t]);
+            mma(sb, fb[hb][t], xf[rb][t]);
+          }
+          // lane: row (2w+rb)*16 + r16, hidden h0 + 16*hb + 4g + e
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float av = sa[e];
+            hf.set(4 * hb + e, av / (1.0f + __expf(-av)) * sb[e]);
+          }
+        }
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) mma(acc[rb][cb], fo[cb], hf);
+      }
+    }
+    // epilogue: lane holds row (2w+rb)*16 + r16, channels cb*16 + 4g + e
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int64_t row = r0 + (2 * w + rb) * 16 + r16;
+      if (row >= a.rows) continue;
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const int c0 = cb * 16 + 4 * g;
+        float base[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.add) load4(a.x + row * C + c0, base);
+        store4(a.out + row * C + c0, base[0] + acc[rb][cb][0], base[1] + acc[rb][cb][1],
+               base[2] + acc[rb][cb][2], base[3] + acc[rb][cb][3]);
+      }
+    }
+    __syncthreads();  // xs reused by the next tile
+  }
+}
+
+}  // namespace odde
+
+using namespace odde;
+
+namespace {
+
+template <typename ZT, typename CT, int kC, int NF>
+void launch_tr(const TransitionArgs<ZT, CT>& p, hipStream_t st) {
+  const int64_t ntiles = (p.rows + kTrRows - 1) / kTrRows;
+  const int grid = (int)std::min<int64_t>(ntiles, 2 * 256);
+  hipLaunchKernelGGL((transition_kernel<ZT, CT, kC, NF>), dim3(grid), dim3(256), 0, st, p, ntiles);
+}
+
+template <typename ZT, typename CT>
+int run_transition(const odde_transition_args* a, hipStream_t st) {
+  TransitionArgs<ZT, CT> p;
+  p.x = static_cast<const ZT*>(a->x);
+  p.out = static_cast<ZT*>(a->out);
+  p.ln_w = a->ln_w; p.ln_b = a->ln_b;
+  p.wa = static_cast<const CT*>(a->w_a);
+  p.wb = static_cast<const CT*>(a->w_b);
+  p.wo = static_cast<const CT*>(a->w_o);
+  p.rows = a->rows; p.add = a->add_residual; p.eps = a->eps;
+  LaunchScope ls(ODDE_K_TRANSITION, st);
+  if (a->c == 128 && a->n_factor == 4) launch_tr<ZT, CT, 4, 4>(p, st);
+  else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
+  else if (a->c == 256 && a->n_factor == 4) launch_tr<ZT, CT, 8, 4>(p, st);
+  else return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256} with n = 4");
+  return check_launch("transition");
+}
+
+}  // namespace
+
+extern "C" {
+
+int odde_transition_fwd(const odde_transition_args* a, void* stream) {
+  if (!a) return set_error(ODDE_EINVAL, "transition: null args");
+  if (a->struct_size != sizeof(odde_transition_args))
+    return set_error(ODDE_EINVAL, "transition: struct_size mismatch (ABI version skew)");
+  if (a->rows < 0 || a->c <= 0 || a->n_factor <= 0)
+    return set_error(ODDE_EINVAL, "transition: bad sizes");
+  if (!valid_dtype(a->x_dtype) || !valid_dtype(a->compute_dtype))
+    return set_error(ODDE_EINVAL, "transition: bad dtype");
+  if (a->compute_dtype != ODDE_BF16)
+    return set_error(ODDE_EUNSUPPORTED, "transition: the fused kernel computes in bf16");
+  if (!a->x || !a->out || !a->ln_w || !a->ln_b || !a->w_a || !a->w_b || !a->w_o)
+    return set_error(ODDE_EINVAL, "transition: null tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(a->x) | reinterpret_cast<uintptr_t>(a->out)) & 15)
+    return set_error(ODDE_EINVAL, "transition: x/out must be 16-byte aligned");
+  if (a->rows == 0) return ODDE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->x_dtype == ODDE_F32) return run_transition<float, bf16>(a, st);
+  return run_transition<bf16, bf16>(a, st);
+}
+
+}  // extern "C"

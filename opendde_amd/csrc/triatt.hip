@@ -45,6 +45,7 @@
 #include <stdlib.h>
 
 #include "common.hpp"
+#include "rowtile.hpp"
 #include "runtime.hpp"
 
 namespace odde {
@@ -250,6 +251,134 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
              ab[3] * s);
       if (g == 0) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
     }
+  }
+}
+
+// Weight-stationary form of the projection (used when each wave's weight
+// slice fits in registers, e.g. C = H*D = 128 in bf16): wave 0 holds W_q (and
+// the tri-bias rows), wave 1 W_k, wave 2 W_v, wave 3 W_g; the workgroup loops
+// over 64-row tiles (i, j0..j0+63), staging LN(z) once in LDS per tile.
+template <typename ZT, typename CT, int kC, int kHD>
+__global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<ZT, CT> a,
+                                                                int ntiles) {
+  constexpr int C = kC * 32, HD = kHD * 32, NB = HD / 16;
+  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ float keep_s[kTileRows];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int H = a.heads, jp = a.jp, n = a.n;
+  const CT* W = w == 0 ? a.wq : w == 1 ? a.wk : w == 2 ? a.wv : a.wg;
+  Frag<CT> wf[NB][kC];
+  load_w_slice<CT, NB, kC>(W, C, 0, HD, wf);
+  Frag<CT> wbf[kC];
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    if (w == 0) load_w_frag(a.wb, C, 0, H, t, wbf[t]);
+    else wbf[t].zero();
+  }
+  const int tiles_per_row = jp / kTileRows;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int i = tile / tiles_per_row;
+    const int j0 = (tile % tiles_per_row) * kTileRows;
+    stage_ln_tile<ZT, CT, C>(
+        [&](int r) -> const ZT* {
+          const int j = j0 + r;
+          return j < n ? a.z + (int64_t)i * a.z_s0 + (int64_t)j * a.z_s1 : nullptr;
+        },
+        a.ln_w, a.ln_b, a.eps, xs);
+    if (w == 0) {  // mask row of the tile's 64 keys (lane l = key j0 + l)
+      const int j = j0 + l;
+      float mv = -INFINITY, kp = 0.f;
+      if (j < n) {
+        const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)j * a.m_s1] : 1.0f;
+        mv = (m - 1.0f) * a.mask_inf;
+        kp = m == 1.0f ? 1.f : 0.f;
+      }
+      a.mb[(size_t)i * jp + j] = mv;
+      keep_s[l] = kp;
+      const uint64_t bal = __ballot(mv != 0.f);
+      if (l < 2)
+        a.mflag[(size_t)i * (jp >> 5) + (j0 >> 5) + l] =
+            ((l == 0 ? bal : bal >> 32) & 0xffffffffull) != 0;
+    }
+    __syncthreads();
+    if (threadIdx.x < kTileRows) {
+      const int t = threadIdx.x, kb = t >> 5, sl = t & 31;
+      a.keep[((size_t)i * (jp >> 5) + (j0 >> 5) + kb) * 32 + sl] =
+          from_f32<CT>(keep_s[kb * 32 + slot_key(sl >> 3, sl & 7)]);
+    }
+    const bool zero_v = a.anykeep[i] != 0;
+    float knm[kHD];
+#pragma unroll
+    for (int h = 0; h < kHD; ++h) knm[h] = 0.f;
+    float bmx = -INFINITY;
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      Frag<CT> xf[kC];
+      tile_frags<CT, C>(xs, rb, xf);
+      if (w == 2) {  // v: x W^T -> lane holds channel o, rows jb..jb+3
+        const int jb = j0 + rb * 16 + 4 * g;
+        float vk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vk[e] = zero_v ? keep_s[rb * 16 + 4 * g + e] : 1.f;
+#pragma unroll
+        for (int ob = 0; ob < NB; ++ob) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < kC; ++t) mma(acc, xf[t], wf[ob][t]);
+          const int o = ob * 16 + r16;
+          store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), acc[0] * vk[0],
+                 acc[1] * vk[1], acc[2] * vk[2], acc[3] * vk[3]);
+        }
+      } else {  // q / k / gate: W x^T -> lane holds row jr, channels o..o+3
+        const int jr = j0 + rb * 16 + r16;
+        float ss = 0.f;
+#pragma unroll
+        for (int ob = 0; ob < NB; ++ob) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < kC; ++t) mma(acc, wf[ob][t], xf[t]);
+          const int o = ob * 16 + 4 * g;
+          const size_t off = (((size_t)i * H + (o >> 5)) * jp + jr) * 32 + (o & 31);
+          if (w == 0) {
+            const float sc = a.q_scale;
+            store4(a.q + off, acc[0] * sc, acc[1] * sc, acc[2] * sc, acc[3] * sc);
+          } else if (w == 1) {
+            store4(a.k + off, acc[0], acc[1], acc[2], acc[3]);
+            ss += acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2] + acc[3] * acc[3];
+            if (ob & 1) {
+              knm[ob >> 1] = fmaxf(knm[ob >> 1], sqrtf(group_sum_fast(ss)));
+              ss = 0.f;
+            }
+          } else {
+            store4(a.gate + off, sigmoidf_(acc[0]), sigmoidf_(acc[1]), sigmoidf_(acc[2]),
+                   sigmoidf_(acc[3]));
+          }
+        }
+        if (w == 0) {  // tri bias: lane h = r16, rows jb..jb+3
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < kC; ++t) mma(acc, xf[t], wbf[t]);
+          const float sc = kLog2e;
+          const int jb = j0 + rb * 16 + 4 * g;
+          if (r16 < H)
+            store4(a.bias + ((size_t)r16 * jp + i) * jp + jb, acc[0] * sc, acc[1] * sc,
+                   acc[2] * sc, acc[3] * sc);
+          bmx = fmaxf(bmx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])) * sc);
+        }
+      }
+    }
+    if (w == 1) {
+#pragma unroll
+      for (int h = 0; h < kHD; ++h) {
+        const float v = lanes16_max(knm[h]);
+        if (l == 0 && h < H) atomicMax(&a.kmax[i * H + h], __float_as_uint(v));
+      }
+    }
+    if (w == 0) {
+      const float bm = group_max_fast(bmx);
+      if (g == 0 && r16 < H) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
+    }
+    __syncthreads();  // xs and keep_s are reused by the next tile
   }
 }
 
@@ -728,6 +857,53 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
   }
 }
 
+// Weight-stationary output projection: wave w holds the W_o rows of output
+// channels [w*C/4, (w+1)*C/4); the workgroup loops over 64-row tiles of o,
+// staged in LDS.
+template <typename ZT, typename CT, int kHD, int kC>
+__global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT, CT> a, int ntiles) {
+  constexpr int HD = kHD * 32, C = kC * 32, NBO = C / 64;
+  constexpr int LD = TileLD<CT, HD>::value;
+  __shared__ __attribute__((aligned(16))) CT xo[kTileRows * LD];
+  const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
+  Frag<CT> wof[NBO][kHD];
+  load_w_slice<CT, NBO, kHD>(a.wo, HD, w * (C / 4), C, wof);
+  const int jp = a.jp, n = a.n, tiles_per_row = jp / kTileRows;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int i = tile / tiles_per_row;
+    const int j0 = (tile % tiles_per_row) * kTileRows;
+    {
+      constexpr int VEC = 16 / sizeof(CT), PER_ROW = HD / VEC;
+      const CT* src = a.o + ((size_t)i * jp + j0) * HD;
+      for (int ci = threadIdx.x; ci < kTileRows * PER_ROW; ci += 256) {
+        const int r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
+        *reinterpret_cast<f32x4*>(xo + r * LD + cc) =
+            *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      Frag<CT> xf[kHD];
+      tile_frags<CT, HD>(xo, rb, xf);
+      const int jr = j0 + rb * 16 + r16;
+#pragma unroll
+      for (int cb = 0; cb < NBO; ++cb) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < kHD; ++t) mma(acc, wof[cb][t], xf[t]);
+        if (jr >= n) continue;
+        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        float base[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.add) load4(a.res + (int64_t)i * a.r_s0 + (int64_t)jr * a.r_s1 + c0, base);
+        store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jr * a.o_s1 + c0, base[0] + acc[0],
+               base[1] + acc[1], base[2] + acc[2], base[3] + acc[3]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 4. core-only slot: strided q/k/v/bias/mask -> core layouts
 // ---------------------------------------------------------------------------
@@ -907,6 +1083,48 @@ void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st)
   hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
 }
 
+// Persistent weight-stationary projection where the per-wave weight slice
+// fits in registers (bf16: (HD/16)*(C/32) <= 32 fragments); false otherwise.
+template <typename ZT, typename CT, int kC, int kHD>
+void launch_proj_ws_t(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
+  const int ntiles = n * (jp / kTileRows);
+  const int grid = min(ntiles, 2 * 256);
+  hipLaunchKernelGGL((triatt_proj_ws_kernel<ZT, CT, kC, kHD>), dim3(grid), dim3(256), 0, st, p,
+                     ntiles);
+}
+
+template <typename ZT, typename CT>
+bool launch_proj_ws(const TriattProjArgs<ZT, CT>& p, int C, int HD, int n, int jp, hipStream_t st) {
+  if constexpr (sizeof(CT) != 2) {
+    return false;
+  } else {
+  if (C == 128 && HD == 128) { launch_proj_ws_t<ZT, CT, 4, 4>(p, n, jp, st); return true; }
+  if (C == 64 && HD == 64) { launch_proj_ws_t<ZT, CT, 2, 2>(p, n, jp, st); return true; }
+  if (C == 128 && HD == 64) { launch_proj_ws_t<ZT, CT, 4, 2>(p, n, jp, st); return true; }
+  if (C == 64 && HD == 128) { launch_proj_ws_t<ZT, CT, 2, 4>(p, n, jp, st); return true; }
+    return false;
+  }
+}
+
+template <typename ZT, typename CT, int kHD, int kC>
+void launch_out_ws_t(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
+  const int ntiles = n * (jp / kTileRows);
+  hipLaunchKernelGGL((triatt_out_ws_kernel<ZT, CT, kHD, kC>), dim3(min(ntiles, 2 * 256)),
+                     dim3(256), 0, st, p, ntiles);
+}
+template <typename ZT, typename CT>
+bool launch_out_ws(const TriattOutArgs<ZT, CT>& p, int HD, int C, int n, int jp, hipStream_t st) {
+  if constexpr (sizeof(CT) != 2) {
+    return false;
+  } else {
+  if (HD == 128 && C == 128) { launch_out_ws_t<ZT, CT, 4, 4>(p, n, jp, st); return true; }
+  if (HD == 64 && C == 64) { launch_out_ws_t<ZT, CT, 2, 2>(p, n, jp, st); return true; }
+  if (HD == 64 && C == 128) { launch_out_ws_t<ZT, CT, 2, 4>(p, n, jp, st); return true; }
+  if (HD == 128 && C == 64) { launch_out_ws_t<ZT, CT, 4, 2>(p, n, jp, st); return true; }
+    return false;
+  }
+}
+
 template <typename ZT, typename CT, int kHD>
 void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   dim3 grid(jp / 64, n);
@@ -929,7 +1147,7 @@ CoreTile core_tile(int rows_per_bias, int batches, bool f32) {
     }
     return d;
   }();
-  const CoreTile t = env.r ? env : (f32 ? CoreTile{2, 2, 2, 4} : CoreTile{2, 4, 2, 4});
+  const CoreTile t = env.r ? env : (f32 ? CoreTile{2, 2, 2, 4} : CoreTile{2, 4, 2, 2});
   // all rows of a workgroup share one bias batch
   if (batches > 1 && rows_per_bias % (t.r * t.rg) != 0) return CoreTile{1, t.qb, 1, t.qs};
   return t;
@@ -1008,12 +1226,14 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
     PrepArgs pa{a->mask, a->mask_s0, a->mask_s1, ws.c.anykeep, ws.c.rowflag, ws.c.kmax,
                 ws.c.bmax, n, jp, H};
     hipLaunchKernelGGL(triatt_prep_kernel, dim3(n), dim3(256), 0, st, pa);
-    switch (C) {
-      case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
-      case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
-      case 256: launch_proj<ZT, CT, 8>(p, n, jp, st); break;
-      case 384: launch_proj<ZT, CT, 12>(p, n, jp, st); break;
-      default: return set_error(ODDE_EUNSUPPORTED, "triatt: c must be 64, 128, 256 or 384");
+    if (!launch_proj_ws<ZT, CT>(p, C, HD, n, jp, st)) {
+      switch (C) {
+        case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
+        case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
+        case 256: launch_proj<ZT, CT, 8>(p, n, jp, st); break;
+        case 384: launch_proj<ZT, CT, 12>(p, n, jp, st); break;
+        default: return set_error(ODDE_EUNSUPPORTED, "triatt: c must be 64, 128, 256 or 384");
+      }
     }
     int rc = check_launch("triatt_proj");
     if (rc) return rc;
@@ -1036,6 +1256,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   o.n = n; o.jp = jp; o.c = C; o.add = a->add_residual;
   {
     LaunchScope ls(ODDE_K_TRIATT_OUT, st);
+    if (launch_out_ws<ZT, CT>(o, HD, C, n, jp, st)) return check_launch("triatt_out");
     switch (HD) {
       case 64: launch_out<ZT, CT, 2>(o, n, jp, st); break;
       case 128: launch_out<ZT, CT, 4>(o, n, jp, st); break;

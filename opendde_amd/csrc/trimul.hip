@@ -19,6 +19,7 @@
 // Workspace (CT = compute type, Np = N rounded up to 128):
 //   A, B, P : [Ch][Np][Np]
 #include "common.hpp"
+#include "rowtile.hpp"
 #include "runtime.hpp"
 
 namespace odde {
@@ -257,6 +258,162 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a
   }
 }
 
+// ---------------------------------------------------------------------------
+// weight-stationary forms (per-wave weight slices in registers, LN'd row
+// tiles staged once in LDS, persistent over 64-row tiles)
+// ---------------------------------------------------------------------------
+
+// Projection: wave w holds the gate and value rows of a (w < 2) or b (w >= 2)
+// for channels [(w & 1) * Ch/2, (w & 1 + 1) * Ch/2).
+template <typename ZT, typename CT, int kC, int kCH>
+__global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<ZT, CT> a,
+                                                                int ntiles) {
+  constexpr int C = kC * 32, CH = kCH * 32, NB = kCH;  // NB blocks of 16 = Ch/2 channels
+  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ float mk_s[kTileRows];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int which = w >> 1, half = w & 1;
+  const int o0 = which * CH + half * (CH / 2);
+  Frag<CT> wpf[NB][kC], wgf[NB][kC];
+  load_w_slice<CT, NB, kC>(a.wp, C, o0, 2 * CH, wpf);
+  load_w_slice<CT, NB, kC>(a.wg, C, o0, 2 * CH, wgf);
+  CT* dst = which ? a.B : a.A;
+  const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int x = tile / tiles_per_row;
+    const int y0 = (tile % tiles_per_row) * kTileRows;
+    stage_ln_tile<ZT, CT, C>(
+        [&](int r) -> const ZT* {
+          const int y = y0 + r;
+          return (x < n && y < n) ? a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 : nullptr;
+        },
+        a.ln_w, a.ln_b, a.eps, xs);
+    if (w == 0) {
+      const int y = y0 + l;
+      mk_s[l] = (x < n && y < n)
+                    ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
+                    : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      Frag<CT> xf[kC];
+      tile_frags<CT, C>(xs, rb, xf);
+      const int yb = y0 + rb * 16 + 4 * g;
+      float mk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mk[e] = mk_s[rb * 16 + 4 * g + e];
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap;
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+          mma(ap, xf[t], wpf[cb][t]);
+          mma(ag, xf[t], wgf[cb][t]);
+        }
+        const int c = half * (CH / 2) + cb * 16 + r16;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = mk[e] * sigmoidf_(ag[e]) * ap[e];
+        store4(dst + ((size_t)c * np + x) * np + yb, v[0], v[1], v[2], v[3]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Epilogue: wave w produces output channels [w*C/4, (w+1)*C/4): W_z and W_g
+// slices in registers; LN_out(P) (P staged transposed from its channel-major
+// planes) and LN_in(z) tiles in LDS.
+template <typename ZT, typename CT, int kC, int kCH>
+__global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT, CT> a, int ntiles) {
+  constexpr int C = kC * 32, CH = kCH * 32, NBO = C / 64;
+  constexpr int LDP = TileLD<CT, CH>::value;
+  __shared__ __attribute__((aligned(16))) CT xp[kTileRows * LDP];
+  __shared__ __attribute__((aligned(16))) CT xz[kTileRows * TileLD<CT, C>::value];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
+  load_w_slice<CT, NBO, kCH>(a.wz, CH, w * (C / 4), C, wzf);
+  load_w_slice<CT, NBO, kC>(a.wg, C, w * (C / 4), C, wgf);
+  const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int x = tile / tiles_per_row;
+    const int y0 = (tile % tiles_per_row) * kTileRows;
+    {  // P[:, x, y0:y0+64] -> xp[y][c]
+      constexpr int VEC = 16 / sizeof(CT), PER_C = kTileRows / VEC;
+      const CT* src = a.P + (size_t)x * np + y0;
+      for (int ci = threadIdx.x; ci < CH * PER_C; ci += 256) {
+        const int c = ci / PER_C, yy = (ci % PER_C) * VEC;
+        CT v[VEC];
+        *reinterpret_cast<f32x4*>(v) =
+            *reinterpret_cast<const f32x4*>(src + (size_t)c * np * np + yy);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xp[(yy + e) * LDP + c] = v[e];
+      }
+    }
+    stage_ln_tile<ZT, CT, C>(
+        [&](int r) -> const ZT* {
+          const int y = y0 + r;
+          return y < n ? a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 : nullptr;
+        },
+        a.ln_in_w, a.ln_in_b, a.eps, xz);
+    __syncthreads();
+    {  // LN_out over the channels of each staged P row, in place
+      constexpr int Q = CH / 4;
+      const int r = threadIdx.x >> 2, quarter = threadIdx.x & 3;
+      CT* row = xp + r * LDP + quarter * Q;
+      float v[Q];
+#pragma unroll
+      for (int e = 0; e < Q; e += 8) load8(row + e, v + e);
+      float sm = 0.f;
+#pragma unroll
+      for (int e = 0; e < Q; ++e) sm += v[e];
+      sm += __shfl_xor(sm, 1, 64);
+      sm += __shfl_xor(sm, 2, 64);
+      const float mean = sm * (1.0f / CH);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < Q; ++e) q += (v[e] - mean) * (v[e] - mean);
+      q += __shfl_xor(q, 1, 64);
+      q += __shfl_xor(q, 2, 64);
+      const float rstd = rsqrtf(q * (1.0f / CH) + a.eps);
+#pragma unroll
+      for (int e = 0; e < Q; e += 4) {
+        float wv[4], bv[4];
+        load4(a.ln_out_w + quarter * Q + e, wv);
+        load4(a.ln_out_b + quarter * Q + e, bv);
+        store4(row + e, (v[e] - mean) * rstd * wv[0] + bv[0], (v[e + 1] - mean) * rstd * wv[1] + bv[1],
+               (v[e + 2] - mean) * rstd * wv[2] + bv[2], (v[e + 3] - mean) * rstd * wv[3] + bv[3]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      Frag<CT> pf[kCH], zf[kC];
+      tile_frags<CT, CH>(xp, rb, pf);
+      tile_frags<CT, C>(xz, rb, zf);
+      const int yr = y0 + rb * 16 + r16;
+#pragma unroll
+      for (int cb = 0; cb < NBO; ++cb) {
+        f32x4 ay = {0.f, 0.f, 0.f, 0.f}, ag = ay;
+#pragma unroll
+        for (int t = 0; t < kCH; ++t) mma(ay, wzf[cb][t], pf[t]);
+#pragma unroll
+        for (int t = 0; t < kC; ++t) mma(ag, wgf[cb][t], zf[t]);
+        if (yr >= n) continue;
+        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        float base[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.add) load4(a.z + (int64_t)x * a.z_s0 + (int64_t)yr * a.z_s1 + c0, base);
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[e] * sigmoidf_(ag[e]);
+        store4(a.out + (int64_t)x * a.o_s0 + (int64_t)yr * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace odde
 
 // ===========================================================================
@@ -311,6 +468,43 @@ void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
 }
 
+// Weight-stationary launches where the per-wave weight slices fit in
+// registers (bf16, C and Ch in {64, 128}); false otherwise.
+template <typename ZT, typename CT, int kC, int kCH>
+void launch_tp_ws_t(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
+  const int ntiles = p.np * (p.np / kTileRows);
+  hipLaunchKernelGGL((trimul_proj_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, 2 * 256)),
+                     dim3(256), 0, st, p, ntiles);
+}
+template <typename ZT, typename CT>
+bool launch_tp_ws(const TrimulProjArgs<ZT, CT>& p, int C, int ch, hipStream_t st) {
+  if constexpr (sizeof(CT) != 2) {
+    return false;
+  } else {
+  if (C == 128 && ch == 128) { launch_tp_ws_t<ZT, CT, 4, 4>(p, st); return true; }
+  if (C == 64 && ch == 64) { launch_tp_ws_t<ZT, CT, 2, 2>(p, st); return true; }
+  if (C == 64 && ch == 128) { launch_tp_ws_t<ZT, CT, 2, 4>(p, st); return true; }
+    return false;
+  }
+}
+template <typename ZT, typename CT, int kC, int kCH>
+void launch_to_ws_t(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
+  const int ntiles = p.n * (p.np / kTileRows);
+  hipLaunchKernelGGL((trimul_out_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, 2 * 256)),
+                     dim3(256), 0, st, p, ntiles);
+}
+template <typename ZT, typename CT>
+bool launch_to_ws(const TrimulOutArgs<ZT, CT>& p, int C, int ch, hipStream_t st) {
+  if constexpr (sizeof(CT) != 2) {
+    return false;
+  } else {
+  if (C == 128 && ch == 128) { launch_to_ws_t<ZT, CT, 4, 4>(p, st); return true; }
+  if (C == 64 && ch == 64) { launch_to_ws_t<ZT, CT, 2, 2>(p, st); return true; }
+  if (C == 64 && ch == 128) { launch_to_ws_t<ZT, CT, 2, 4>(p, st); return true; }
+    return false;
+  }
+}
+
 template <typename ZT, typename CT, int kC, int kCh>
 void launch_to(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
   dim3 grid(p.np / 64, p.n);
@@ -350,11 +544,13 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   p.n = n; p.np = np; p.ch = ch; p.eps = a->eps;
   {
     LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
-    switch (C) {
-      case 64: launch_tp<ZT, CT, 2>(p, st); break;
-      case 128: launch_tp<ZT, CT, 4>(p, st); break;
-      case 256: launch_tp<ZT, CT, 8>(p, st); break;
-      case 384: launch_tp<ZT, CT, 12>(p, st); break;
+    if (!launch_tp_ws<ZT, CT>(p, C, ch, st)) {
+      switch (C) {
+        case 64: launch_tp<ZT, CT, 2>(p, st); break;
+        case 128: launch_tp<ZT, CT, 4>(p, st); break;
+        case 256: launch_tp<ZT, CT, 8>(p, st); break;
+        case 384: launch_tp<ZT, CT, 12>(p, st); break;
+      }
     }
     int rc = check_launch("trimul_proj");
     if (rc) return rc;
@@ -381,8 +577,8 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   o.n = n; o.np = np; o.c = C; o.add = a->add_residual; o.eps = a->eps;
   {
     LaunchScope ls(ODDE_K_TRIMUL_OUT, st);
-    bool ok = false;
-    switch (C) {
+    bool ok = launch_to_ws<ZT, CT>(o, C, ch, st);
+    if (!ok) switch (C) {
       case 64: ok = dispatch_to<ZT, CT, 2>(o, ch, st); break;
       case 128: ok = dispatch_to<ZT, CT, 4>(o, ch, st); break;
       case 256: ok = dispatch_to<ZT, CT, 8>(o, ch, st); break;

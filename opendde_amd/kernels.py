@@ -282,3 +282,39 @@ def triangle_attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     a.workspace, a.workspace_bytes = _ptr(work), work.numel()
     _lib.check(lib.odde_triatt_core_fwd(ctypes.byref(a), _stream(q.device)), "odde_triatt_core_fwd")
     return out[0] if squeeze else out
+
+
+TRANSITION_CHANNELS = (64, 128, 256)
+
+
+def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torch.Tensor] = None,
+               add_residual: bool = False, eps: float = 1e-5) -> torch.Tensor:
+    """Fused SwiGLU transition over the last dim of ``x`` (bf16 arithmetic):
+    out = (x if add_residual else 0) + W_o(silu(W_a LN(x)) * W_b LN(x)).
+    ``out`` may be ``x`` (in-place residual update)."""
+    _require_gpu(x)
+    c = x.shape[-1]
+    nf = w_a.shape[0] // c
+    if c not in TRANSITION_CHANNELS or nf != 4 or w_a.shape[0] != nf * c:
+        raise NotImplementedError(f"HIP transition supports c in {TRANSITION_CHANNELS}, n=4")
+    if not x.is_contiguous():
+        raise ValueError("transition input must be contiguous")
+    if out is None:
+        out = torch.empty_like(x)
+    if not out.is_contiguous() or out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must be a contiguous tensor like x")
+    bf = torch.bfloat16
+    keep = [prepared(ln_w, torch.float32), prepared(ln_b, torch.float32),
+            prepared(w_a, bf), prepared(w_b, bf), prepared(w_o, bf)]
+    a = _lib.TransitionArgs()
+    a.struct_size = ctypes.sizeof(_lib.TransitionArgs)
+    a.c, a.n_factor = c, nf
+    a.x_dtype, a.compute_dtype = dtype_code(x.dtype), _lib.BF16
+    a.add_residual = 1 if add_residual else 0
+    a.rows = x.numel() // c
+    a.x, a.out = _ptr(x), _ptr(out)
+    a.ln_w, a.ln_b, a.w_a, a.w_b, a.w_o = (_ptr(t) for t in keep)
+    a.eps = float(eps)
+    _lib.check(_lib.load().odde_transition_fwd(ctypes.byref(a), _stream(x.device)),
+               "odde_transition_fwd")
+    return out

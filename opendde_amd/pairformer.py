@@ -20,6 +20,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import hook
+from . import kernels as K
 from .layers import LayerNorm, Linear, LinearNoBias
 from .triangular import (TriangleAttention, TriangleMultiplicationIncoming,
                          TriangleMultiplicationOutgoing)
@@ -41,6 +42,19 @@ class Transition(nn.Module):
                                              initializer="relu")
         self.linear_no_bias = LinearNoBias(in_features=n * c_in, out_features=c_in,
                                            initializer="zeros")
+
+    def hip_supported(self, x: torch.Tensor) -> bool:
+        """The fused HIP kernel runs bf16 arithmetic: bf16 inputs, or float32
+        inputs under bf16 autocast (the reference's bf16 mode)."""
+        return (x.is_cuda and self.n == 4 and self.c_in in K.TRANSITION_CHANNELS
+                and K.autocast_compute_dtype(x) == torch.bfloat16 and x.is_contiguous())
+
+    def hip_apply(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                  add_residual: bool = False) -> torch.Tensor:
+        return K.transition(x, ln_w=self.layernorm1.weight, ln_b=self.layernorm1.bias,
+                            w_a=self.linear_no_bias_a.weight, w_b=self.linear_no_bias_b.weight,
+                            w_o=self.linear_no_bias.weight, out=out, add_residual=add_residual,
+                            eps=self.layernorm1.eps)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         other = x.shape[:-1]
@@ -202,8 +216,12 @@ class PairformerBlock(nn.Module):
             zt = zt.add_(upd) if inplace_safe else zt + upd
             z = zt.transpose(-2, -3).contiguous()
 
-        upd = self.pair_transition(z)
-        z = z.add_(upd) if inplace_safe else z + upd
+        if (hip_mul or hip_att) and self.pair_transition.hip_supported(z):
+            z = self.pair_transition.hip_apply(z, out=z if inplace_safe else None,
+                                               add_residual=True)
+        else:
+            upd = self.pair_transition(z)
+            z = z.add_(upd) if inplace_safe else z + upd
         if self.c_s > 0:
             s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias)
             s = s + self.single_transition(s)

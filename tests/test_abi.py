@@ -35,7 +35,8 @@ def test_library_exports_every_declared_symbol():
 
 @pytest.mark.parametrize("cname,pyty", [("odde_triatt_args", _lib.TriattArgs),
                                         ("odde_triatt_core_args", _lib.TriattCoreArgs),
-                                        ("odde_trimul_args", _lib.TrimulArgs)])
+                                        ("odde_trimul_args", _lib.TrimulArgs),
+                                        ("odde_transition_args", _lib.TransitionArgs)])
 def test_struct_layout_matches_header(cname, pyty):
     fields = [f for f, _ in pyty._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",

@@ -235,3 +235,54 @@ def test_triangle_attention_fully_masked_rows_are_mean_of_v(n_pad):
     exp = ref.triangle_attention(z, mask, params_of(mod), 4)
     got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
     assert_fp32(got, exp, f"fully masked rows n_pad={n_pad}")
+
+
+# -------------------------------------------------------------- transition
+
+
+@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130)])
+def test_transition_bf16(c, rows):
+    from opendde_amd.pairformer import Transition
+    # weights scaled so the output stays O(1) at every width (the absolute
+    # bound of the bf16 tier is scale dependent)
+    mod = seeded(Transition(c, 4), 700 + c, STD * (128 / c) ** 0.5)
+    x = torch.randn(rows, c, generator=torch.Generator().manual_seed(c)).to(torch.bfloat16)
+    exp = ref.transition(x.float(), params_of(mod))
+    before = _lib.launch_count(_lib.K_TRANSITION)
+    mod = mod.to(DEV)
+    got = mod.hip_apply(x.to(DEV))
+    assert _lib.launch_count(_lib.K_TRANSITION) == before + 1
+    assert_bf16(got, exp, f"transition c={c} rows={rows}")
+
+
+def test_transition_fp32_residual_under_autocast_in_place():
+    from opendde_amd.pairformer import Transition
+    mod = seeded(Transition(128, 4), 711, STD).to(DEV)
+    x = torch.randn(64, 64, 128, generator=torch.Generator().manual_seed(3))
+    exp = x + ref.transition(x, params_of(mod))
+    xg = x.to(DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        assert mod.hip_supported(xg)
+        out = mod.hip_apply(xg, out=xg, add_residual=True)
+    assert out.data_ptr() == xg.data_ptr() and out.dtype == torch.float32
+    assert_bf16(out - x.to(DEV), exp - x, "transition in-place update")
+
+
+def test_pairformer_block_bf16_autocast():
+    # the bench's mode: float32 residual stream, bf16 module arithmetic
+    n = 70
+    blk = seeded(PairformerBlock(n_heads=16, c_z=128, c_s=384), 41, 0.05)
+    g = torch.Generator().manual_seed(42)
+    z = torch.randn(n, n, 128, generator=g)
+    s = torch.randn(n, 384, generator=g)
+    mask = token_pair_mask(n, 6, seed=1, random=True)
+    se, ze = ref.pairformer_block(s, z, mask, params_of(blk), no_heads_pair=4, n_heads=16)
+    blk = blk.to(DEV)
+    before = _lib.launch_count(_lib.K_TRANSITION)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        sg, zg = blk(s.to(DEV), z.to(DEV).clone(), mask.to(DEV), triangle_multiplicative="hip",
+                     triangle_attention="hip", inplace_safe=True)
+    assert _lib.launch_count(_lib.K_TRANSITION) == before + 1
+    assert zg.dtype == torch.float32
+    assert_bf16(zg - z.to(DEV), ze - z, "block update z (bf16 arithmetic)")
+    assert_bf16(sg - s.to(DEV), se - s, "block update s (bf16 arithmetic)")
