@@ -173,6 +173,13 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  *   y = LN(x); out = (add_residual ? x : 0) + (silu(y W_a^T) * (y W_b^T)) W_o^T
  * x, out: [rows][c] contiguous (out may alias x); W_a, W_b: [n*c][c],
  * W_o: [c][n*c] in compute_dtype (bf16 only); LN params f32.
+ * Optional (pb_heads = 16; 0 = off): the pair-bias projection that the single
+ * track's AttentionPairBias takes from the updated pair tensor
+ * (linear_nobias_z(layernorm_z(z)), opendde/model/modules/transformer.py:
+ * 599-602), computed from the rows as written:
+ *   pb_out[h][r] = sum_c LN'(out[r])[c] * pb_w[h][c]     (f32, [16][rows])
+ * with LN' = LayerNorm(pb_ln_w, pb_ln_b (may be NULL), pb_eps); pb_w is
+ * [16][c] in compute_dtype.  This saves the separate pass over all of z.
  */
 typedef struct odde_transition_args {
   uint32_t struct_size;
@@ -190,6 +197,12 @@ typedef struct odde_transition_args {
   const void* w_b;
   const void* w_o;
   float eps;
+  int32_t pb_heads;
+  const float* pb_ln_w;
+  const float* pb_ln_b;
+  const void* pb_w;
+  float* pb_out;
+  float pb_eps;
 } odde_transition_args;
 
 int odde_transition_fwd(const odde_transition_args* args, void* hip_stream);

@@ -86,6 +86,8 @@ class TransitionArgs(ctypes.Structure):
         ("compute_dtype", _i32), ("add_residual", _i32), ("rows", _i64),
         ("x", _vp), ("out", _vp), ("ln_w", _vp), ("ln_b", _vp),
         ("w_a", _vp), ("w_b", _vp), ("w_o", _vp), ("eps", _f32),
+        ("pb_heads", _i32), ("pb_ln_w", _vp), ("pb_ln_b", _vp), ("pb_w", _vp), ("pb_out", _vp),
+        ("pb_eps", _f32),
     ]
 
 

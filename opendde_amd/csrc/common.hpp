@@ -34,6 +34,8 @@ __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+// x rounded to T's precision and widened back
+template <typename T> __device__ __forceinline__ float round_to(float x) { return (float)from_f32<T>(x); }
 
 // ----------------------------------------------------------------------------
 // K32 fragments

@@ -29,10 +29,79 @@ struct TransitionArgs {
   int64_t rows;
   int add;
   float eps;
+  // optional 16-head projection of LN'(out) (null pb_out = off)
+  const float* pb_ln_w;
+  const float* pb_ln_b;  // may be null
+  const CT* pb_w;        // [16][C]
+  float* pb_out;         // [16][rows]
+  float pb_eps;
 };
 
 constexpr int kTrRows = 128;  // rows per workgroup tile
 constexpr int kTrHid = 32;    // hidden units per chunk
+
+// Pair-bias projection of the rows just written (AttentionPairBias's
+// linear_nobias_z(layernorm_z(z)) over the updated z): the wave's 16 rows sit
+// in the output accumulators, lane (g, r16) holding channels cb*16 + 4g + e of
+// row r16.  LayerNorm statistics come from a reduction over the four lanes of
+// a row; the normalised row feeds an MFMA as the B operand in that same
+// channel order (K32 block t = channel blocks 2t, 2t+1), with W rows read in
+// the matching order, giving heads 4g + e of row r16 per lane.
+template <typename ZT, typename CT, int kC>
+__device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>& a,
+                                                   const f32x4 (&zacc)[kC * 2], int64_t row,
+                                                   bool valid) {
+  constexpr int C = kC * 32, NCB = C / 16;
+  const int l = lane_id(), g = l >> 4, r16 = l & 15;
+  float zv[NCB][4];
+  float s = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      zv[cb][e] = round_to<ZT>(zacc[cb][e]);  // the value as stored
+      s += zv[cb][e];
+    }
+  s += __shfl_xor(s, 16, 64);
+  s += __shfl_xor(s, 32, 64);
+  const float mean = s * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = zv[cb][e] - mean;
+      q += d * d;
+    }
+  q += __shfl_xor(q, 16, 64);
+  q += __shfl_xor(q, 32, 64);
+  const float rstd = rsqrtf(q * (1.0f / C) + a.pb_eps);
+  f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    float lw[8], lb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, wv[8];
+    load4(a.pb_ln_w + 32 * t + 4 * g, lw);
+    load4(a.pb_ln_w + 32 * t + 16 + 4 * g, lw + 4);
+    if (a.pb_ln_b) {
+      load4(a.pb_ln_b + 32 * t + 4 * g, lb);
+      load4(a.pb_ln_b + 32 * t + 16 + 4 * g, lb + 4);
+    }
+    load4(a.pb_w + r16 * C + 32 * t + 4 * g, wv);
+    load4(a.pb_w + r16 * C + 32 * t + 16 + 4 * g, wv + 4);
+    Frag<CT> yf, wf;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = zv[2 * t + (e >> 2)][e & 3];
+      yf.set(e, (z - mean) * rstd * lw[e] + lb[e]);
+      wf.set(e, wv[e]);
+    }
+    mma(pacc, wf, yf);
+  }
+  if (valid) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a.pb_out[(size_t)(4 * g + e) * a.rows + row] = pacc[e];
+  }
+}
 
 template <typename ZT, typename CT, int kC, int NF>
 __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, CT> a,
@@ -127,15 +196,18 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       const int64_t row = r0 + (2 * w + rb) * 16 + r16;
-      if (row >= a.rows) continue;
+      const bool valid = row < a.rows;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         const int c0 = cb * 16 + 4 * g;
         float base[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.add) load4(a.x + row * C + c0, base);
-        store4(a.out + row * C + c0, base[0] + acc[rb][cb][0], base[1] + acc[rb][cb][1],
-               base[2] + acc[rb][cb][2], base[3] + acc[rb][cb][3]);
+        if (valid && a.add) load4(a.x + row * C + c0, base);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[rb][cb][e] += base[e];
+        if (valid) store4(a.out + row * C + c0, acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2],
+                          acc[rb][cb][3]);
       }
+      if (a.pb_out) pair_bias_epilogue<ZT, CT, kC>(a, acc[rb], row, valid);
     }
     __syncthreads();  // xs reused by the next tile
   }
@@ -164,6 +236,10 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
   p.wb = static_cast<const CT*>(a->w_b);
   p.wo = static_cast<const CT*>(a->w_o);
   p.rows = a->rows; p.add = a->add_residual; p.eps = a->eps;
+  p.pb_ln_w = a->pb_ln_w; p.pb_ln_b = a->pb_ln_b;
+  p.pb_w = static_cast<const CT*>(a->pb_w);
+  p.pb_out = a->pb_heads ? a->pb_out : nullptr;
+  p.pb_eps = a->pb_eps;
   LaunchScope ls(ODDE_K_TRANSITION, st);
   if (a->c == 128 && a->n_factor == 4) launch_tr<ZT, CT, 4, 4>(p, st);
   else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
@@ -190,6 +266,15 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
     return set_error(ODDE_EINVAL, "transition: null tensor pointer");
   if ((reinterpret_cast<uintptr_t>(a->x) | reinterpret_cast<uintptr_t>(a->out)) & 15)
     return set_error(ODDE_EINVAL, "transition: x/out must be 16-byte aligned");
+  if (a->pb_heads != 0) {
+    if (a->pb_heads != 16)
+      return set_error(ODDE_EUNSUPPORTED, "transition: pair-bias projection needs 16 heads");
+    if (!a->pb_ln_w || !a->pb_w || !a->pb_out)
+      return set_error(ODDE_EINVAL, "transition: null pair-bias pointer");
+    if ((reinterpret_cast<uintptr_t>(a->pb_ln_w) | reinterpret_cast<uintptr_t>(a->pb_ln_b) |
+         reinterpret_cast<uintptr_t>(a->pb_w)) & 15)
+      return set_error(ODDE_EINVAL, "transition: pair-bias parameters must be 16-byte aligned");
+  }
   if (a->rows == 0) return ODDE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (a->x_dtype == ODDE_F32) return run_transition<float, bf16>(a, st);

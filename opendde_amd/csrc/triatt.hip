@@ -397,6 +397,7 @@ struct TriattCoreArgs {
   const unsigned* kmax;
   const int* bmax;
   int* rowflag;
+  const int* anykeep; // [rows] row keeps at least one key
   const CT* gate;     // may be null
   CT* out;
   int64_t o_row, o_h, o_j;  // element strides of out[row][h][q][d]
@@ -705,6 +706,52 @@ __global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<C
   const int q0 = blockIdx.x * (16 * QB);
   const int jp = a.jp, n = a.n;
   const float* B = a.bias + ((size_t)(row0 / a.rows_per_bias) * a.heads + h) * jp * jp;
+
+  // Rows that keep no key: every logit carries the same -inf*log2e term, which
+  // absorbs q.k + bias in f32, so the softmax is uniform over the n keys and
+  // the output is mean_k v (the reference's f32 result for such rows).
+  bool all_masked = true;
+#pragma unroll
+  for (int r = 0; r < R; ++r) all_masked = all_masked && (row0 + r >= a.rows || a.anykeep[rr[r]] == 0);
+  if (all_masked) {
+    f32x4 o[R][2][QB];
+    float inv[R][QB];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const CT* Vr = a.v + ((size_t)rr[r] * a.heads + h) * jp * 32;
+      float sum[2] = {0.f, 0.f};
+      for (int k0 = 0; k0 < jp; k0 += 32) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          Frag<CT> vf;  // lane: channel 16*db + r16, keys k0 + slot_key(g, e)
+          vf.load(Vr + (size_t)(k0 >> 5) * 1024 + (db * 64 + l) * 8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k0 + slot_key(g, e) < n) sum[db] += vf.get(e);
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        float t = sum[db];
+        t += __shfl_xor(t, 16, 64);
+        t += __shfl_xor(t, 32, 64);
+        sum[db] = t;  // every lane with this r16 holds channel 16*db + r16
+      }
+      // accumulator layout: lane (g, r16) holds channels 16*db + 4g + e of query r16
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t = __shfl(sum[db], 4 * g + e, 64);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) o[r][db][qb][e] = t;
+        }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) inv[r][qb] = 1.0f / (float)n;
+    }
+    core_store<CT, R, QB>(a, row0, h, q0, o, inv);
+    return;
+  }
 
   const CT* Qp[R];
   const CT* Kp[R];
@@ -1194,7 +1241,7 @@ void fill_core_args(TriattCoreArgs<CT>& c, const CoreBufs& b) {
   c.v = static_cast<const CT*>(b.v);
   c.keep = static_cast<const CT*>(b.keep);
   c.bias = b.bias; c.mb = b.mb; c.mflag = b.mflag; c.kmax = b.kmax; c.bmax = b.bmax;
-  c.rowflag = b.rowflag;
+  c.rowflag = b.rowflag; c.anykeep = b.anykeep;
 }
 
 template <typename ZT, typename CT>

@@ -288,10 +288,16 @@ TRANSITION_CHANNELS = (64, 128, 256)
 
 
 def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torch.Tensor] = None,
-               add_residual: bool = False, eps: float = 1e-5) -> torch.Tensor:
+               add_residual: bool = False, eps: float = 1e-5,
+               pair_bias: Optional[tuple] = None) -> torch.Tensor:
     """Fused SwiGLU transition over the last dim of ``x`` (bf16 arithmetic):
     out = (x if add_residual else 0) + W_o(silu(W_a LN(x)) * W_b LN(x)).
-    ``out`` may be ``x`` (in-place residual update)."""
+    ``out`` may be ``x`` (in-place residual update).
+
+    ``pair_bias = (ln_w, ln_b, w, eps, dest)`` also writes
+    ``dest[h, r] = (LN(out[r]) @ w.T)[h]`` (w: [16, c], dest: float32
+    [16, rows]) from the rows as written, i.e. AttentionPairBias's
+    ``linear_nobias_z(layernorm_z(z))`` over the updated pair tensor."""
     _require_gpu(x)
     c = x.shape[-1]
     nf = w_a.shape[0] // c
@@ -315,6 +321,24 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     a.x, a.out = _ptr(x), _ptr(out)
     a.ln_w, a.ln_b, a.w_a, a.w_b, a.w_o = (_ptr(t) for t in keep)
     a.eps = float(eps)
+    if pair_bias is not None:
+        pln_w, pln_b, pw, peps, dest = pair_bias
+        rows = a.rows
+        if pw.shape != (16, c):
+            raise NotImplementedError("pair-bias projection needs a [16, c] weight")
+        if dest.dtype != torch.float32 or dest.shape != (16, rows) or not dest.is_contiguous() \
+                or dest.device != x.device:
+            raise ValueError("pair-bias destination must be a contiguous float32 [16, rows] "
+                             "tensor on x's device")
+        pkeep = [prepared(pln_w, torch.float32), prepared(pw, bf)]
+        if pln_b is not None:
+            pkeep.append(prepared(pln_b, torch.float32))
+        keep += pkeep
+        a.pb_heads = 16
+        a.pb_ln_w, a.pb_w = _ptr(pkeep[0]), _ptr(pkeep[1])
+        a.pb_ln_b = _ptr(pkeep[2]) if pln_b is not None else None
+        a.pb_out = _ptr(dest)
+        a.pb_eps = float(peps)
     _lib.check(_lib.load().odde_transition_fwd(ctypes.byref(a), _stream(x.device)),
                "odde_transition_fwd")
     return out

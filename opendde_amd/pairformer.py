@@ -50,11 +50,11 @@ class Transition(nn.Module):
                 and K.autocast_compute_dtype(x) == torch.bfloat16 and x.is_contiguous())
 
     def hip_apply(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
-                  add_residual: bool = False) -> torch.Tensor:
+                  add_residual: bool = False, pair_bias: Optional[tuple] = None) -> torch.Tensor:
         return K.transition(x, ln_w=self.layernorm1.weight, ln_b=self.layernorm1.bias,
                             w_a=self.linear_no_bias_a.weight, w_b=self.linear_no_bias_b.weight,
                             w_o=self.linear_no_bias.weight, out=out, add_residual=add_residual,
-                            eps=self.layernorm1.eps)
+                            eps=self.layernorm1.eps, pair_bias=pair_bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         other = x.shape[:-1]
@@ -143,10 +143,26 @@ class AttentionPairBias(nn.Module):
         self.layernorm_z = LayerNorm(c_z, create_offset=create_offset_ln_z)
         self.linear_nobias_z = LinearNoBias(in_features=c_z, out_features=n_heads)
 
+    def hip_pair_bias_ok(self) -> bool:
+        """The pair-bias projection can be produced by the fused transition
+        kernel (16 heads, LN with a scale)."""
+        return self.n_heads == 16 and self.layernorm_z.weight is not None
+
+    def pair_bias_spec(self, dest: torch.Tensor) -> tuple:
+        return (self.layernorm_z.weight, self.layernorm_z.bias, self.linear_nobias_z.weight,
+                self.layernorm_z.eps, dest)
+
     def forward(self, a: torch.Tensor, s: Optional[torch.Tensor], z: torch.Tensor,
-                extra_attn_bias: Optional[torch.Tensor] = None, **_unused) -> torch.Tensor:
+                extra_attn_bias: Optional[torch.Tensor] = None,
+                z_bias: Optional[torch.Tensor] = None, **_unused) -> torch.Tensor:
+        """``z_bias`` ([heads, N, N]) is ``linear_nobias_z(layernorm_z(z))``
+        already computed from this z (the fused transition kernel makes it
+        while writing z); ``z`` is then not read."""
         a = self.layernorm_a(a)
-        bias = self.linear_nobias_z(self.layernorm_z(z)).movedim(-1, -3)
+        if z_bias is None:
+            bias = self.linear_nobias_z(self.layernorm_z(z)).movedim(-1, -3)
+        else:
+            bias = z_bias
         if extra_attn_bias is not None:
             eb = extra_attn_bias
             while eb.dim() < bias.dim() - 1:
@@ -216,14 +232,21 @@ class PairformerBlock(nn.Module):
             zt = zt.add_(upd) if inplace_safe else zt + upd
             z = zt.transpose(-2, -3).contiguous()
 
+        z_bias = None
         if (hip_mul or hip_att) and self.pair_transition.hip_supported(z):
+            pb = None
+            if self.c_s > 0 and z.dim() == 3 and self.attention_pair_bias.hip_pair_bias_ok():
+                z_bias = torch.empty((16, z.shape[0], z.shape[1]), dtype=torch.float32,
+                                     device=z.device)
+                pb = self.attention_pair_bias.pair_bias_spec(z_bias.view(16, -1))
             z = self.pair_transition.hip_apply(z, out=z if inplace_safe else None,
-                                               add_residual=True)
+                                               add_residual=True, pair_bias=pb)
         else:
             upd = self.pair_transition(z)
             z = z.add_(upd) if inplace_safe else z + upd
         if self.c_s > 0:
-            s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias)
+            s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias,
+                                             z_bias=z_bias)
             s = s + self.single_transition(s)
         return s, z
 

@@ -79,6 +79,18 @@ def test_bad_arguments_return_status_and_message():
     t.n, t.c, t.c_hidden = 32, 100, 128
     rc, msg = _status("odde_trimul_fwd", t)
     assert rc == -2 and "c_hidden" in msg
+    tr = _lib.TransitionArgs()
+    tr.struct_size = ctypes.sizeof(tr)
+    tr.c, tr.n_factor, tr.rows = 128, 4, 10
+    tr.x_dtype, tr.compute_dtype = 0, 1
+    for f in ("x", "out", "ln_w", "ln_b", "w_a", "w_b", "w_o"):
+        setattr(tr, f, ctypes.c_void_p(0x1000))
+    tr.pb_heads = 8
+    rc, msg = _status("odde_transition_fwd", tr)
+    assert rc == -2 and "16 heads" in msg
+    tr.pb_heads = 16
+    rc, msg = _status("odde_transition_fwd", tr)
+    assert rc == -1 and "pair-bias" in msg
 
 
 def test_workspace_query_and_too_small_workspace():

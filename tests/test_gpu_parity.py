@@ -268,6 +268,33 @@ def test_transition_fp32_residual_under_autocast_in_place():
     assert_bf16(out - x.to(DEV), exp - x, "transition in-place update")
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_transition_pair_bias_projection(x_dtype):
+    # the single track's pair bias linear_nobias_z(layernorm_z(z)) computed in
+    # the transition kernel's epilogue from the rows it writes
+    from opendde_amd import kernels as K
+    from opendde_amd.pairformer import AttentionPairBias, Transition
+    n = 75  # 5625 rows: ragged against the 128-row tiles
+    # smaller transition weights keep z's update O(1): with bf16 storage the
+    # written z also carries the rounding of |z| ~ 4 values (ulp 2^-5)
+    tr = seeded(Transition(128, 4), 720, STD / 2)
+    apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=128), 721, 0.1)
+    x = torch.randn(n, n, 128, generator=torch.Generator().manual_seed(5)).to(x_dtype)
+    xf = x.float()
+    z_new = xf + ref.transition(xf, params_of(tr))
+    pz = params_of(apb)
+    exp_bias = ref.linear(ref.layer_norm(z_new, pz["layernorm_z.weight"], pz["layernorm_z.bias"]),
+                          pz["linear_nobias_z.weight"]).permute(2, 0, 1)
+    tr, apb = tr.to(DEV), apb.to(DEV)
+    xg = x.to(DEV)
+    dest = torch.full((16, n, n), float("nan"), device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = tr.hip_apply(xg, out=xg, add_residual=True,
+                           pair_bias=apb.pair_bias_spec(dest.view(16, -1)))
+    assert_bf16(out.float() - xf.to(DEV), z_new - xf, f"transition update ({x_dtype})")
+    assert_bf16(dest, exp_bias, f"fused pair bias ({x_dtype})")
+
+
 def test_pairformer_block_bf16_autocast():
     # the bench's mode: float32 residual stream, bf16 module arithmetic
     n = 70
@@ -279,10 +306,15 @@ def test_pairformer_block_bf16_autocast():
     se, ze = ref.pairformer_block(s, z, mask, params_of(blk), no_heads_pair=4, n_heads=16)
     blk = blk.to(DEV)
     before = _lib.launch_count(_lib.K_TRANSITION)
+    ln_z_calls = []
+    hook = blk.attention_pair_bias.layernorm_z.register_forward_hook(
+        lambda *_: ln_z_calls.append(1))
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
         sg, zg = blk(s.to(DEV), z.to(DEV).clone(), mask.to(DEV), triangle_multiplicative="hip",
                      triangle_attention="hip", inplace_safe=True)
+    hook.remove()
     assert _lib.launch_count(_lib.K_TRANSITION) == before + 1
+    assert not ln_z_calls, "pair bias should come from the fused transition epilogue"
     assert zg.dtype == torch.float32
     assert_bf16(zg - z.to(DEV), ze - z, "block update z (bf16 arithmetic)")
     assert_bf16(sg - s.to(DEV), se - s, "block update s (bf16 arithmetic)")
