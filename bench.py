@@ -9,10 +9,14 @@ inference mode).  Inputs are resident in HBM before timing; each step starts
 by restoring z from a resident copy (a 512 MB device copy, ~0.1 ms).
 
 Prints ONE JSON line.  ``value`` is the trunk's algorithmic throughput in
-TFLOP/s (flop counts of the path, multiply-add = 2); per-kernel figures come
-from HIP events recorded by the library around every launch on the stream it
-runs on, over the timed steps.  ``cpu_baseline`` times the CPU oracle (fp32)
-on one block of the same workload on this host.
+TFLOP/s (flop counts of the path, multiply-add = 2) over the timed steps,
+which run without instrumentation.  Per-kernel figures come from one further
+step during which the library records HIP events around every launch on the
+stream it runs on.  ``roofline.traffic`` is the dominant kernel's HBM bytes
+per launch from the committed rocprofv3 --pmc summary of this workload
+(profiles/pmc_traffic_trunk_n<N>.json, made with ``--pmc-probe``), or null.
+``cpu_baseline`` times the CPU oracle (fp32) on one block of the same
+workload on this host.
 """
 
 from __future__ import annotations
@@ -66,6 +70,17 @@ def kernel_bytes(n, c_z=128, h=4, ch=128, z_bytes=4, ct_bytes=2):
     }
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(n: int, chunk: int):
     """Time the CPU oracle (fp32) on one PairformerBlock of the workload at n."""
     from oracle import reference as ref
@@ -85,10 +100,37 @@ def cpu_baseline(n: int, chunk: int):
         "kind": "port",
         "sample": f"oracle (CPU PyTorch restatement of the reference torch path) fp32, one "
                   f"PairformerBlock at N={n} (tri-attn row chunk {chunk}), {dt:.2f} s; "
-                  f"CPU {platform.processor() or platform.machine()}, "
+                  f"CPU {cpu_model()}, "
                   f"{cores} cores in affinity",
         "block_ms": round(dt * 1e3, 1),
     }
+
+
+CALIB_BYTES = 1 << 30  # bytes read (and written) by the calibration kernel
+
+
+def pmc_probe(step, dev):
+    """Dispatches for the HBM-traffic counters: a plain elementwise kernel
+    reading CALIB_BYTES and writing CALIB_BYTES (its FETCH_SIZE / WRITE_SIZE
+    give the counters' scale), then the trunk step's kernels."""
+    src = torch.ones(CALIB_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    torch.add(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    step()
+    torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+
+
+def load_traffic(n: int):
+    """HBM bytes per launch of each kernel as measured by the committed
+    rocprofv3 --pmc summary for this workload (or {} if there is none)."""
+    path = os.path.join(ROOT, "profiles", f"pmc_traffic_trunk_n{n}.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch", {})
 
 
 def main():
@@ -100,6 +142,9 @@ def main():
     ap.add_argument("--blocks", type=int, default=48)
     ap.add_argument("--cpu-sample-n", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "
+                         "size, then one trunk step over a single block; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build measures the single-GPU pair-stack "
@@ -124,19 +169,26 @@ def main():
                          inplace_safe=True)
         return s
 
+    if args.pmc_probe:
+        pmc_probe(step, dev)
+        return
+
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    _lib.timing_reset()
-    _lib.timing_enable(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         s_out = step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    _lib.timing_enable(False)
     assert torch.isfinite(z).all() and torch.isfinite(s_out).all(), "non-finite trunk output"
+    # per-kernel breakdown from one more step with HIP events recorded around
+    # every launch on its own stream (kept out of the timed region)
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    step()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
 
     n = args.n
     f = flops(n)
@@ -151,7 +203,7 @@ def main():
         if cnt == 0:
             continue
         avg = tot / cnt
-        ent = {"launches": cnt, "avg_ms": round(avg, 4), "total_ms_per_step": round(tot / args.steps, 3)}
+        ent = {"launches": cnt, "avg_ms": round(avg, 4), "total_ms_per_step": round(tot, 3)}
         if name == "triatt_core":
             t = f["core"] / (avg * 1e-3) / 1e12
             ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
@@ -164,14 +216,16 @@ def main():
         kernels[name] = ent
     dom = max(kernels, key=lambda k: kernels[k]["total_ms_per_step"])
     d = kernels[dom]
+    traffic = load_traffic(n).get(dom)
     if "tflops" in d:
         achieved = d["tflops"]
         roof = {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic}
     else:
         achieved = d["gbs"]
         roof = {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic}
 
     att_mod_ms = sum(kernels.get(k, {}).get("avg_ms", 0) for k in ("triatt_proj", "triatt_core", "triatt_out"))
     mul_mod_ms = sum(kernels.get(k, {}).get("avg_ms", 0) for k in ("trimul_proj", "trimul_contract", "trimul_out"))
