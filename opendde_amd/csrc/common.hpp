@@ -155,7 +155,24 @@ __device__ __forceinline__ float swap16_add(float v) {
 __device__ __forceinline__ float group_max_fast(float v) { return swap32_max(swap16_max(v)); }
 __device__ __forceinline__ float group_sum_fast(float v) { return swap32_add(swap16_add(v)); }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal (about 1 ulp
+// each): an IEEE division here would cost a dozen instructions per element.
+// Saturates correctly: exp2 -> inf gives 0, exp2 -> 0 gives 1.
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
+
+// Workgroup barrier without the memory fence __syncthreads() carries (that
+// fence waits for every outstanding global load, which would drain loads
+// issued ahead of time).  Callers first wait for what they need themselves
+// (s_waitcnt on their own loads and LDS traffic); the empty asm statements
+// keep the compiler from moving memory operations across the barrier.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }

@@ -70,6 +70,110 @@ __device__ __forceinline__ void stage_ln_tile(RowPtr row_ptr, const float* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Raw tile staging by direct global->LDS loads (global_load_lds_dwordx4): the
+// next tile's rows stream into LDS while the current tile is computed, with
+// no staging registers.  Each wave instruction writes 64 lanes x 16 bytes =
+// one contiguous KiB of LDS (lane l at +16*l), so the LDS layout is chosen
+// through the source each lane fetches: slot s of row r holds the row's
+// 16-byte chunk s ^ (r & 7).  The LayerNorm pass (4 threads per row, each
+// reading its quarter chunk by chunk) then hits 16 distinct 16-byte bank
+// groups per instruction.
+// ---------------------------------------------------------------------------
+template <typename ZT, int C>
+struct RawTile {
+  static constexpr int ROW_BYTES = C * (int)sizeof(ZT);
+  static constexpr int BYTES = kTileRows * ROW_BYTES;
+  static constexpr int CHUNKS = ROW_BYTES / 16;            // 16-byte chunks per row
+  static constexpr int ROWS_PER_OP = 64 / CHUNKS;          // rows per wave instruction
+  static constexpr int OPS_PER_WAVE = kTileRows / ROWS_PER_OP / 4;
+  static_assert(CHUNKS >= 8 && 64 % CHUNKS == 0, "row must be 8..64 chunks of 16 bytes");
+  static_assert(kTileRows % (4 * ROWS_PER_OP) == 0, "tile rows per wave");
+};
+
+// Issue the tile's loads.  row_ptr(r) must return a readable row for every
+// r < kTileRows (callers clamp rows past the end to a real row and mask them
+// in raw_tile_ln).  Completion is awaited by raw_tile_wait().
+template <typename ZT, int C, typename RowPtr>
+__device__ __forceinline__ void raw_tile_issue(RowPtr row_ptr, unsigned char* raw) {
+  using T = RawTile<ZT, C>;
+  const int w = wave_id(), l = lane_id();
+#pragma unroll 1
+  for (int op = 0; op < T::OPS_PER_WAVE; ++op) {  // one address live at a time
+    const int blk = w * T::OPS_PER_WAVE + op;
+    const int r = blk * T::ROWS_PER_OP + l / T::CHUNKS;
+    const int chunk = (l % T::CHUNKS) ^ (r & 7);
+    const unsigned char* src = reinterpret_cast<const unsigned char*>(row_ptr(r)) + chunk * 16;
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void*)src,
+        (__attribute__((address_space(3))) void*)(raw + blk * 1024), 16, 0, 0);
+  }
+}
+
+// All of this workgroup's tile loads have landed in LDS.
+__device__ __forceinline__ void raw_tile_wait() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// LayerNorm of the raw tile into `lds` (row stride TileLD), as stage_ln_tile;
+// rows with !valid(r) become zeros.  The caller synchronises afterwards.
+template <typename ZT, typename CT, int C, typename Valid>
+__device__ __forceinline__ void raw_tile_ln(const unsigned char* raw, Valid valid,
+                                            const float* __restrict__ ln_w,
+                                            const float* __restrict__ ln_b, float eps, CT* lds) {
+  using T = RawTile<ZT, C>;
+  constexpr int Q = C / 4;                        // channels per thread
+  constexpr int EPC = 16 / (int)sizeof(ZT);       // elements per chunk
+  constexpr int NCH = Q / EPC;                    // chunks per thread
+  constexpr int LD = TileLD<CT, C>::value;
+  const int t = threadIdx.x;
+  const int r = t >> 2, quarter = t & 3;
+  const bool ok = valid(r);
+  const unsigned char* row = raw + r * T::ROW_BYTES;
+  float x[Q];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int chunk = quarter * NCH + k;
+    const ZT* src = reinterpret_cast<const ZT*>(row + ((chunk ^ (r & 7)) * 16));
+    if constexpr (sizeof(ZT) == 4) {
+      load4(src, x + k * EPC);
+    } else {
+      load8(src, x + k * EPC);
+    }
+  }
+  if (!ok) {
+#pragma unroll
+    for (int e = 0; e < Q; ++e) x[e] = 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < Q; ++e) s += x[e];
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  const float mean = s * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < Q; ++e) {
+    const float d = x[e] - mean;
+    q += d * d;
+  }
+  q += __shfl_xor(q, 1, 64);
+  q += __shfl_xor(q, 2, 64);
+  const float rstd = rsqrtf(q * (1.0f / C) + eps);
+  CT* dst = lds + r * LD + quarter * Q;
+#pragma unroll
+  for (int e = 0; e < Q; e += 4) {
+    float w[4], b[4];
+    load4(ln_w + quarter * Q + e, w);
+    load4(ln_b + quarter * Q + e, b);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = ok ? (x[e + k] - mean) * rstd * w[k] + b[k] : 0.f;
+    store4(dst + e, y[0], y[1], y[2], y[3]);
+  }
+}
+
 // K32 fragments of tile row (rb*16 + lane%16), all C/32 contraction steps.
 template <typename CT, int C>
 __device__ __forceinline__ void tile_frags(const CT* lds, int rb, Frag<CT> (&f)[C / 32]) {

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <string>
 
@@ -41,5 +42,6 @@ struct Carver {
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int dtype_size(int dt) { return dt == ODDE_BF16 ? 2 : 4; }
 inline bool valid_dtype(int dt) { return dt == ODDE_F32 || dt == ODDE_BF16; }
+
 
 }  // namespace odde

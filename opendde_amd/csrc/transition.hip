@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float av = sa[e];
-            hf.set(4 * hb + e, av / (1.0f + __expf(-av)) * sb[e]);
+            hf.set(4 * hb + e, siluf_(av) * sb[e]);
           }
         }
 #pragma unroll

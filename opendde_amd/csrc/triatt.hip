@@ -257,12 +257,14 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 // Weight-stationary form of the projection (used when each wave's weight
 // slice fits in registers, e.g. C = H*D = 128 in bf16): wave 0 holds W_q (and
 // the tri-bias rows), wave 1 W_k, wave 2 W_v, wave 3 W_g; the workgroup loops
-// over 64-row tiles (i, j0..j0+63), staging LN(z) once in LDS per tile.
+// over 64-row tiles (i, j0..j0+63), staging LN(z) once in LDS per tile.  The
+// next tile's z rows stream into LDS (direct loads) while a tile is computed.
 template <typename ZT, typename CT, int kC, int kHD>
 __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<ZT, CT> a,
                                                                 int ntiles) {
   constexpr int C = kC * 32, HD = kHD * 32, NB = HD / 16;
   __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float keep_s[kTileRows];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int H = a.heads, jp = a.jp, n = a.n;
@@ -276,15 +278,21 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
     else wbf[t].zero();
   }
   const int tiles_per_row = jp / kTileRows;
+  // rows past n read row n-1 (always present) and are masked in the LN pass
+  auto issue = [&](int tl) {
+    const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
+    raw_tile_issue<ZT, C>(
+        [&](int r) -> const ZT* {
+          return a.z + (int64_t)ti * a.z_s0 + (int64_t)min(tj0 + r, n - 1) * a.z_s1;
+        },
+        raw);
+  };
+  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int i = tile / tiles_per_row;
     const int j0 = (tile % tiles_per_row) * kTileRows;
-    stage_ln_tile<ZT, CT, C>(
-        [&](int r) -> const ZT* {
-          const int j = j0 + r;
-          return j < n ? a.z + (int64_t)i * a.z_s0 + (int64_t)j * a.z_s1 : nullptr;
-        },
-        a.ln_w, a.ln_b, a.eps, xs);
+    raw_tile_wait();  // also: every wave is done with the previous tile's xs
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, a.ln_w, a.ln_b, a.eps, xs);
     if (w == 0) {  // mask row of the tile's 64 keys (lane l = key j0 + l)
       const int j = j0 + l;
       float mv = -INFINITY, kp = 0.f;
@@ -301,6 +309,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
             ((l == 0 ? bal : bal >> 32) & 0xffffffffull) != 0;
     }
     __syncthreads();
+    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
     if (threadIdx.x < kTileRows) {
       const int t = threadIdx.x, kb = t >> 5, sl = t & 31;
       a.keep[((size_t)i * (jp >> 5) + (j0 >> 5) + kb) * 32 + sl] =
@@ -378,7 +387,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
       const float bm = group_max_fast(bmx);
       if (g == 0 && r16 < H) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
     }
-    __syncthreads();  // xs and keep_s are reused by the next tile
+    // xs and keep_s are rewritten only after the barrier in raw_tile_wait()
   }
 }
 
@@ -493,8 +502,26 @@ __device__ __forceinline__ int kswz(int key, int chunk, int kch) {
 // K Q^T on MFMA with the accumulator initialised from the bias fragment
 // (shared by its R rows), p = exp2(s), row sums sum_k keep[k] p[k] by dot2,
 // O^T += V^T P^T on MFMA.
+// Workgroups are dealt to the 8 XCDs round-robin by linear id.  Map the
+// linear id L to (query block x, group) so that the nx query blocks of one
+// group (a set of rows of one head) run back to back on one XCD: that
+// group's K and V rows are then fetched into one L2 and reused from there,
+// instead of being fetched into every XCD's L2.  A plain row-major order is
+// used when the group count is not a multiple of 8.
+__device__ __forceinline__ void xcd_group_map(int L, int nx, int ngroups, int& x, int& grp) {
+  if (ngroups & 7) {
+    x = L % nx;
+    grp = L / nx;
+    return;
+  }
+  const int xcd = L & 7, s = L >> 3;
+  grp = xcd + 8 * (s / nx);
+  x = s % nx;
+}
+
 template <typename CT, int R, int QB, int RG, int QS>
-__global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a) {
+__global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a, int nx,
+                                                                        int ny) {
   constexpr int NT = 64 * RG * QS;
   constexpr int R_WG = RG * R, Q_WG = QS * 16 * QB;
   typedef CoreStage<CT, R_WG, Q_WG> Stage;
@@ -504,10 +531,12 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
 
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int rg = w / QS, qs = w % QS;
-  const int h = blockIdx.z;
+  int bx, grp;
+  xcd_group_map(blockIdx.x, nx, ny * a.heads, bx, grp);
+  const int h = grp / ny;
   const int jp = a.jp, n = a.n;
-  const int wg_row0 = blockIdx.y * R_WG;
-  const int wg_q0 = blockIdx.x * Q_WG;
+  const int wg_row0 = (grp % ny) * R_WG;
+  const int wg_q0 = bx * Q_WG;
   const int row0 = wg_row0 + rg * R;
   const int q0 = wg_q0 + qs * 16 * QB;
   const int bb = min(wg_row0, a.rows - 1) / a.rows_per_bias;
@@ -1203,9 +1232,9 @@ CoreTile core_tile(int rows_per_bias, int batches, bool f32) {
 template <typename CT, int R, int QB, int RG, int QS>
 void launch_core_t(const TriattCoreArgs<CT>& p, hipStream_t st) {
   constexpr int R_WG = R * RG, Q_WG = 16 * QB * QS;
-  dim3 grid((p.jp + Q_WG - 1) / Q_WG, (p.rows + R_WG - 1) / R_WG, p.heads);
-  hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>), grid, dim3(64 * RG * QS), 0,
-                     st, p);
+  const int nx = (p.jp + Q_WG - 1) / Q_WG, ny = (p.rows + R_WG - 1) / R_WG;
+  hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>),
+                     dim3((unsigned)(nx * ny * p.heads)), dim3(64 * RG * QS), 0, st, p, nx, ny);
   // the exact core keeps a modest tile: it only runs for flagged rows
   dim3 grid2(p.jp / 32, (p.rows + 3) / 4, p.heads);
   hipLaunchKernelGGL((triatt_core_exact_kernel<CT, 1, 2>), grid2, dim3(256), 0, st, p);
@@ -1229,6 +1258,9 @@ int launch_core(const TriattCoreArgs<CT>& p, int batches, hipStream_t st) {
   ODDE_TILE(1, 4, 1, 1)
   ODDE_TILE(1, 2, 1, 4)
   ODDE_TILE(1, 2, 1, 1)
+  ODDE_TILE(2, 2, 2, 2)
+  ODDE_TILE(2, 2, 1, 4)
+  ODDE_TILE(1, 4, 2, 2)
   else return set_error(ODDE_EINVAL, "ODDE_TRIATT_TILE: unsupported R,QB,RG,QS");
 #undef ODDE_TILE
   return check_launch("triatt_core");

@@ -180,6 +180,119 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(ContractArgs<CT> a
     }
 }
 
+// Large-tile form (bf16, Np a multiple of 256): TX x TY tiles per workgroup
+// of 8 waves (WX along x, 8/WX along y).  K advances in stages of 32 staged
+// by direct global -> LDS loads into NS buffers: stage s+NS-1 streams in
+// while stage s is multiplied.  One fence-free barrier per stage suffices:
+// each wave first waits for its own loads of stage s (vmcnt) and its own LDS
+// reads of stage s-1 (lgkmcnt), and the buffer refilled at stage s was last
+// read at stage s-1.  LDS rows are 64 bytes (4 chunks of 16); slot t of row r
+// holds chunk t ^ ((r >> 1) & 3), which spreads the K32 fragment reads of 16
+// consecutive rows over all banks.
+constexpr int kCk = 32;  // k per stage
+
+__device__ __forceinline__ int ct_swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+
+template <int TX, int TY, int WX, int NS>
+__global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<bf16> a) {
+  constexpr int WY = 8 / WX, MX = TX / WX / 16, MY = TY / WY / 16;  // fragments per wave
+  constexpr int OPS_A = TX / 16 / 8, OPS_B = TY / 16 / 8;          // 1 KiB loads per wave
+  constexpr int OPS = OPS_A + OPS_B;
+  __shared__ __attribute__((aligned(16))) bf16 sm[NS][(TX + TY) * kCk];  // [stage][A rows | B rows][k]
+  const int TXn = a.np / TX, TYn = a.np / TY;
+  const int tiles = TXn * TYn;
+  int bid = blockIdx.x, c, tile;
+  if ((a.ch & 7) == 0) {  // all tiles of a channel on one XCD
+    const int xcd = bid & 7, local = bid >> 3;
+    c = (local / tiles) * 8 + xcd;
+    tile = local % tiles;
+  } else {
+    c = bid / tiles;
+    tile = bid % tiles;
+  }
+  const int x0 = (tile / TYn) * TX, y0 = (tile % TYn) * TY;
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % WX, wy = w / WX;
+  const size_t plane = (size_t)a.np * a.np;
+  const bf16* Ab = a.A + c * plane + (size_t)x0 * a.np;
+  const bf16* Bb = a.B + c * plane + (size_t)y0 * a.np;
+
+  // Stage loads: 1 KiB (16 rows of 64 bytes) per wave instruction; wave w
+  // loads A blocks w*OPS_A.. and B blocks w*OPS_B..; source offsets are fixed
+  // per lane, only k advances.
+  int soff[OPS];
+#pragma unroll
+  for (int op = 0; op < OPS; ++op) {
+    const bool isb = op >= OPS_A;
+    const int blk = isb ? w * OPS_B + (op - OPS_A) : w * OPS_A + op;
+    const int row = blk * 16 + (l >> 2);
+    soff[op] = row * a.np + ct_swz(row, l & 3) * 8;
+  }
+  auto issue = [&](int st) {
+    const int k0 = st * kCk;
+    bf16* base = sm[st % NS];
+#pragma unroll
+    for (int op = 0; op < OPS; ++op) {
+      const bool isb = op >= OPS_A;
+      const int blk = isb ? w * OPS_B + (op - OPS_A) : w * OPS_A + op;
+      const bf16* src = (isb ? Bb : Ab) + soff[op] + k0;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(base + (isb ? TX * kCk : 0) + blk * 512),
+          16, 0, 0);
+    }
+  };
+
+  f32x4 acc[MX][MY];
+#pragma unroll
+  for (int i = 0; i < MX; ++i)
+#pragma unroll
+    for (int j = 0; j < MY; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // fragment offsets: the swizzle depends on r16 only (rows step by 16)
+  const int fsw = ct_swz(r16, g) * 8;
+  const int aoff = (wx * (TX / WX) + r16) * kCk + fsw;
+  const int boff = TX * kCk + (wy * (TY / WY) + r16) * kCk + fsw;
+
+  const int S = a.np / kCk;  // >= 8
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) issue(st);
+  for (int st = 0; st < S; ++st) {
+    // this wave's loads of stage st landed (up to NS-2 later stages in flight)
+    const int ahead = min(S - 1 - st, NS - 2);
+    if (ahead >= 2) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * OPS) : "memory");
+    } else if (ahead == 1) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // own reads of stage st-1 done
+    barrier_nofence();
+    if (st + NS - 1 < S) issue(st + NS - 1);
+    const bf16* base = sm[st % NS];
+    Frag<bf16> af[MX], bfr[MY];
+#pragma unroll
+    for (int j = 0; j < MY; ++j) bfr[j].load(base + boff + j * 16 * kCk);
+#pragma unroll
+    for (int i = 0; i < MX; ++i) af[i].load(base + aoff + i * 16 * kCk);
+#pragma unroll
+    for (int i = 0; i < MX; ++i)
+#pragma unroll
+      for (int j = 0; j < MY; ++j) mma(acc[i][j], bfr[j], af[i]);
+  }
+  // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16), rows y = y0 + wy*TY/WY + 16j + 4g + r
+  bf16* Pb = a.P + c * plane;
+#pragma unroll
+  for (int i = 0; i < MX; ++i)
+#pragma unroll
+    for (int j = 0; j < MY; ++j) {
+      const int xx = x0 + wx * (TX / WX) + i * 16 + r16;
+      const int yy = y0 + wy * (TY / WY) + j * 16 + 4 * g;
+      store4(Pb + (size_t)xx * a.np + yy, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // 3. LN_out + W_z, gate, residual
 // ---------------------------------------------------------------------------
@@ -270,6 +383,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
                                                                 int ntiles) {
   constexpr int C = kC * 32, CH = kCH * 32, NB = kCH;  // NB blocks of 16 = Ch/2 channels
   __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float mk_s[kTileRows];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int which = w >> 1, half = w & 1;
@@ -279,15 +393,23 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   load_w_slice<CT, NB, kC>(a.wg, C, o0, 2 * CH, wgf);
   CT* dst = which ? a.B : a.A;
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
+  // the next tile's z rows stream into LDS while a tile is computed; rows
+  // outside n x n read a real row and are masked in the LN pass
+  auto issue = [&](int tl) {
+    const int tx = min(tl / tiles_per_row, n - 1), ty0 = (tl % tiles_per_row) * kTileRows;
+    raw_tile_issue<ZT, C>(
+        [&](int r) -> const ZT* {
+          return a.z + (int64_t)tx * a.z_s0 + (int64_t)min(ty0 + r, n - 1) * a.z_s1;
+        },
+        raw);
+  };
+  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
-    stage_ln_tile<ZT, CT, C>(
-        [&](int r) -> const ZT* {
-          const int y = y0 + r;
-          return (x < n && y < n) ? a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 : nullptr;
-        },
-        a.ln_w, a.ln_b, a.eps, xs);
+    raw_tile_wait();  // also: every wave is done with the previous tile
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, a.ln_w, a.ln_b,
+                           a.eps, xs);
     if (w == 0) {
       const int y = y0 + l;
       mk_s[l] = (x < n && y < n)
@@ -295,6 +417,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
                     : 0.f;
     }
     __syncthreads();
+    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> xf[kC];
@@ -318,7 +441,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
         store4(dst + ((size_t)c * np + x) * np + yb, v[0], v[1], v[2], v[3]);
       }
     }
-    __syncthreads();
+    // xs and mk_s are rewritten only after the barrier in raw_tile_wait()
   }
 }
 
@@ -331,11 +454,21 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   constexpr int LDP = TileLD<CT, CH>::value;
   __shared__ __attribute__((aligned(16))) CT xp[kTileRows * LDP];
   __shared__ __attribute__((aligned(16))) CT xz[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
   load_w_slice<CT, NBO, kCH>(a.wz, CH, w * (C / 4), C, wzf);
   load_w_slice<CT, NBO, kC>(a.wg, C, w * (C / 4), C, wgf);
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
+  auto issue = [&](int tl) {  // the next tile's z rows (for LN_in), as in the projection
+    const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;
+    raw_tile_issue<ZT, C>(
+        [&](int r) -> const ZT* {
+          return a.z + (int64_t)tx * a.z_s0 + (int64_t)min(ty0 + r, n - 1) * a.z_s1;
+        },
+        raw);
+  };
+  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
@@ -351,13 +484,9 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         for (int e = 0; e < VEC; ++e) xp[(yy + e) * LDP + c] = v[e];
       }
     }
-    stage_ln_tile<ZT, CT, C>(
-        [&](int r) -> const ZT* {
-          const int y = y0 + r;
-          return y < n ? a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 : nullptr;
-        },
-        a.ln_in_w, a.ln_in_b, a.eps, xz);
-    __syncthreads();
+    raw_tile_wait();  // z rows landed; every wave is done with the previous tile
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return y0 + r < n; }, a.ln_in_w, a.ln_in_b, a.eps,
+                           xz);
     {  // LN_out over the channels of each staged P row, in place
       constexpr int Q = CH / 4;
       const int r = threadIdx.x >> 2, quarter = threadIdx.x & 3;
@@ -387,6 +516,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       }
     }
     __syncthreads();
+    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> pf[kCH], zf[kC];
@@ -559,9 +689,20 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   ContractArgs<CT> k;
   k.A = p.A; k.B = p.B; k.P = static_cast<CT*>(ws.P); k.np = np; k.ch = ch;
   {
-    const int tiles = (np / 128) * (np / 128);
     LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
-    hipLaunchKernelGGL((trimul_contract_kernel<CT>), dim3(tiles * ch), dim3(256), 0, st, k);
+    if constexpr (sizeof(CT) == 2) {
+      if (np % 256 == 0) {  // 256 x 128 tiles, two workgroups per CU
+        const int tiles = (np / 256) * (np / 128);
+        hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3>), dim3(tiles * ch),
+                           dim3(512), 0, st, k);
+      } else {
+        const int tiles = (np / 128) * (np / 128);
+        hipLaunchKernelGGL((trimul_contract_kernel<CT>), dim3(tiles * ch), dim3(256), 0, st, k);
+      }
+    } else {
+      const int tiles = (np / 128) * (np / 128);
+      hipLaunchKernelGGL((trimul_contract_kernel<CT>), dim3(tiles * ch), dim3(256), 0, st, k);
+    }
     int rc = check_launch("trimul_contract");
     if (rc) return rc;
   }
