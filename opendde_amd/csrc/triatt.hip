@@ -701,17 +701,22 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
   }
   if (skip) return;
 
+  // A row whose sum underflows (or that keeps no key) goes to the exact core;
+  // flagged one row at a time, as the exact core recomputes whole rows.
   float inv[R][QB];
-  bool under = false;
+  int under = 0;
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r) {
+    bool ur = false;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const float lt = group_sum_fast(lsum[r][qb]);
-      under = under || !(lt >= kUnderflowSum);
+      ur = ur || !(lt >= kUnderflowSum);
       inv[r][qb] = 1.0f / lt;
     }
-  if (__any(under) && l < R && row0 + l < a.rows) a.rowflag[row0 + l] = 1;
+    if (__any(ur)) under |= 1 << r;
+  }
+  if (under && l < R && row0 + l < a.rows && ((under >> l) & 1)) a.rowflag[row0 + l] = 1;
   if (q0 >= jp) return;
   core_store<CT, R, QB>(a, row0, h, q0, o, inv);
 }
@@ -732,16 +737,17 @@ __global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<C
   }
   if (!any_flagged) return;
   const int h = blockIdx.z;
-  const int q0 = blockIdx.x * (16 * QB);
   const int jp = a.jp, n = a.n;
   const float* B = a.bias + ((size_t)(row0 / a.rows_per_bias) * a.heads + h) * jp * jp;
 
   // Rows that keep no key: every logit carries the same -inf*log2e term, which
   // absorbs q.k + bias in f32, so the softmax is uniform over the n keys and
-  // the output is mean_k v (the reference's f32 result for such rows).
+  // the output is mean_k v (the reference's f32 result for such rows),
+  // computed once and written to every query.
   bool all_masked = true;
 #pragma unroll
-  for (int r = 0; r < R; ++r) all_masked = all_masked && (row0 + r >= a.rows || a.anykeep[rr[r]] == 0);
+  for (int r = 0; r < R; ++r)
+    all_masked = all_masked && (row0 + r >= a.rows || a.anykeep[rr[r]] == 0);
   if (all_masked) {
     f32x4 o[R][2][QB];
     float inv[R][QB];
@@ -778,113 +784,118 @@ __global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<C
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) inv[r][qb] = 1.0f / (float)n;
     }
-    core_store<CT, R, QB>(a, row0, h, q0, o, inv);
+    for (int q0 = blockIdx.x * (16 * QB); q0 < jp; q0 += gridDim.x * (16 * QB))
+      core_store<CT, R, QB>(a, row0, h, q0, o, inv);
     return;
   }
 
-  const CT* Qp[R];
-  const CT* Kp[R];
-  const CT* Vp[R];
-  const float* MBp[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const size_t rh = (size_t)rr[r] * a.heads + h;
-    Qp[r] = a.q + rh * jp * 32;
-    Kp[r] = a.k + rh * jp * 32;
-    Vp[r] = a.v + rh * jp * 32;
-    MBp[r] = a.mb + (size_t)rr[r] * jp;
-  }
-  Frag<CT> qf[R][QB];
-  const float* brow[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qq = q0 + 16 * qb + r16;
-    brow[qb] = B + (size_t)min(qq, n - 1) * jp + 4 * g;
-#pragma unroll
-    for (int r = 0; r < R; ++r) qf[r][qb].load(Qp[r] + (size_t)qq * 32 + 8 * g);
-  }
-  const Frag<CT> ones = ones_frag(CT());
+  // query blocks of the row, gridDim.x apart
+  for (int q0 = blockIdx.x * (16 * QB); q0 < jp; q0 += gridDim.x * (16 * QB)) {
 
-  f32x4 o[R][2][QB];
-  float m[R][QB], lsum[R][QB];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      o[r][0][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      o[r][1][qb] = o[r][0][qb];
-      m[r][qb] = -1e30f;
-      lsum[r][qb] = 0.f;
-    }
-
-  for (int k0 = 0; k0 < jp; k0 += 32) {
-    f32x4 bfr[2][QB];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-        bfr[kb][qb] = *reinterpret_cast<const f32x4*>(brow[qb] + k0 + 16 * kb);
+    const CT* Qp[R];
+    const CT* Kp[R];
+    const CT* Vp[R];
+    const float* MBp[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      Frag<CT> kf[2], vf[2];
-      f32x4 mbv[2];
+      const size_t rh = (size_t)rr[r] * a.heads + h;
+      Qp[r] = a.q + rh * jp * 32;
+      Kp[r] = a.k + rh * jp * 32;
+      Vp[r] = a.v + rh * jp * 32;
+      MBp[r] = a.mb + (size_t)rr[r] * jp;
+    }
+    Frag<CT> qf[R][QB];
+    const float* brow[QB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        kf[kb].load(Kp[r] + (size_t)(k0 + 16 * kb + r16) * 32 + 8 * g);
-        vf[kb].load(Vp[r] + (size_t)(k0 >> 5) * 1024 + (kb * 64 + l) * 8);
-        mbv[kb] = *reinterpret_cast<const f32x4*>(MBp[r] + k0 + 16 * kb + 4 * g);
-      }
-      f32x4 s[2][QB];
-      if (a.mflag[(size_t)rr[r] * (jp >> 5) + (k0 >> 5)]) {
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qq = q0 + 16 * qb + r16;
+      brow[qb] = B + (size_t)min(qq, n - 1) * jp + 4 * g;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int r = 0; r < R; ++r) qf[r][qb].load(Qp[r] + (size_t)qq * 32 + 8 * g);
+    }
+    const Frag<CT> ones = ones_frag(CT());
+
+    f32x4 o[R][2][QB];
+    float m[R][QB], lsum[R][QB];
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            s[kb][qb] = bfr[kb][qb] + mbv[kb];
-            mma(s[kb][qb], kf[kb], qf[r][qb]);
-          }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            s[kb][qb] = bfr[kb][qb];
-            mma(s[kb][qb], kf[kb], qf[r][qb]);
-          }
-      }
-      Frag<CT> pf[QB];
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        float mx = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
-                         fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3])));
-        mx = group_max_fast(mx);
-        if (__any(mx > m[r][qb])) {
-          const float mnew = fmaxf(m[r][qb], mx);
-          const float sc = __builtin_amdgcn_exp2f(m[r][qb] - mnew);
-          m[r][qb] = mnew;
-          lsum[r][qb] *= sc;
-          o[r][0][qb] *= sc;
-          o[r][1][qb] *= sc;
-        }
-        const float mm = m[r][qb];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e] - mm));
-        lsum[r][qb] = psum8(pf[qb], ones, lsum[r][qb]);
+        o[r][0][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        o[r][1][qb] = o[r][0][qb];
+        m[r][qb] = -1e30f;
+        lsum[r][qb] = 0.f;
       }
+
+    for (int k0 = 0; k0 < jp; k0 += 32) {
+      f32x4 bfr[2][QB];
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+        for (int qb = 0; qb < QB; ++qb)
+          bfr[kb][qb] = *reinterpret_cast<const f32x4*>(brow[qb] + k0 + 16 * kb);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        Frag<CT> kf[2], vf[2];
+        f32x4 mbv[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          kf[kb].load(Kp[r] + (size_t)(k0 + 16 * kb + r16) * 32 + 8 * g);
+          vf[kb].load(Vp[r] + (size_t)(k0 >> 5) * 1024 + (kb * 64 + l) * 8);
+          mbv[kb] = *reinterpret_cast<const f32x4*>(MBp[r] + k0 + 16 * kb + 4 * g);
+        }
+        f32x4 s[2][QB];
+        if (a.mflag[(size_t)rr[r] * (jp >> 5) + (k0 >> 5)]) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              s[kb][qb] = bfr[kb][qb] + mbv[kb];
+              mma(s[kb][qb], kf[kb], qf[r][qb]);
+            }
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              s[kb][qb] = bfr[kb][qb];
+              mma(s[kb][qb], kf[kb], qf[r][qb]);
+            }
+        }
+        Frag<CT> pf[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          float mx = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
+                           fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3])));
+          mx = group_max_fast(mx);
+          if (__any(mx > m[r][qb])) {
+            const float mnew = fmaxf(m[r][qb], mx);
+            const float sc = __builtin_amdgcn_exp2f(m[r][qb] - mnew);
+            m[r][qb] = mnew;
+            lsum[r][qb] *= sc;
+            o[r][0][qb] *= sc;
+            o[r][1][qb] *= sc;
+          }
+          const float mm = m[r][qb];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e] - mm));
+          lsum[r][qb] = psum8(pf[qb], ones, lsum[r][qb]);
+        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+      }
     }
+    float inv[R][QB];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) inv[r][qb] = 1.0f / group_sum_fast(lsum[r][qb]);
+    core_store<CT, R, QB>(a, row0, h, q0, o, inv);
   }
-  float inv[R][QB];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) inv[r][qb] = 1.0f / group_sum_fast(lsum[r][qb]);
-  core_store<CT, R, QB>(a, row0, h, q0, o, inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -1235,8 +1246,9 @@ void launch_core_t(const TriattCoreArgs<CT>& p, hipStream_t st) {
   const int nx = (p.jp + Q_WG - 1) / Q_WG, ny = (p.rows + R_WG - 1) / R_WG;
   hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>),
                      dim3((unsigned)(nx * ny * p.heads)), dim3(64 * RG * QS), 0, st, p, nx, ny);
-  // the exact core keeps a modest tile: it only runs for flagged rows
-  dim3 grid2(p.jp / 32, (p.rows + 3) / 4, p.heads);
+  // the exact core keeps a modest tile; each wave loops over up to 8 query
+  // blocks of one row (it does work only for rows the fast core flagged)
+  dim3 grid2((p.jp + 255) / 256, (p.rows + 3) / 4, p.heads);
   hipLaunchKernelGGL((triatt_core_exact_kernel<CT, 1, 2>), grid2, dim3(256), 0, st, p);
 }
 
