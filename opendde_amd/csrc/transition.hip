@@ -213,6 +213,152 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
   }
 }
 
+// Pipelined form for C = 128, n = 4 (the pair transition): 8 waves own 256
+// rows; the hidden dimension is walked in chunks of 32 whose W_a / W_b rows
+// and W_o columns (24 KiB) stream into three LDS stages by direct global ->
+// LDS loads, two chunks ahead, continuing across row tiles (every tile walks
+// the same chunks).  One fence-free barrier per chunk: each wave waits for
+// its own loads of the chunk (vmcnt) and its LDS reads of the previous one
+// (lgkmcnt) first; the stage refilled at chunk q was last read at chunk q-1.
+// LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
+// bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
+// (4 slots; slot t of row r holds chunk t ^ ((r >> 1) & 3)).
+constexpr int kTpRows = 256;
+constexpr int kTpStages = 3;
+constexpr int kTpChunkElems = 3 * 4096;  // W_a, W_b: 32 x 128; W_o: 128 x 32
+
+template <typename ZT>
+__global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<ZT, bf16> a,
+                                                                 int64_t ntiles) {
+  constexpr int C = 128, kC = 4, HID = 512, NCB = C / 16, NCHUNK = HID / kTrHid;
+  constexpr int LDX = TileLD<bf16, C>::value;
+  __shared__ __attribute__((aligned(16))) bf16 xs[kTpRows * LDX];
+  __shared__ __attribute__((aligned(16))) bf16 ws[kTpStages][kTpChunkElems];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+
+  // this workgroup's tiles and chunk loads (only loads that will be consumed
+  // are issued, so none is in flight when the workgroup ends)
+  const int my_tiles =
+      blockIdx.x < ntiles ? (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0;
+  const int Q = my_tiles * NCHUNK;
+  auto issue = [&](int q) {
+    const int h0 = (q % NCHUNK) * kTrHid;
+    bf16* base = ws[q % kTpStages];
+#pragma unroll 1
+    for (int op = 0; op < 3; ++op) {  // one address live at a time
+      const int b = w * 3 + op, region = b >> 3, bi = b & 7;  // 24 KiB = 24 blocks
+      const bf16* src;
+      if (region < 2) {  // W_a / W_b rows h0 + row, 4 rows per block
+        const int row = bi * 4 + (l >> 4), chunk = (l & 15) ^ (row & 15);
+        src = (region ? a.wb : a.wa) + (size_t)(h0 + row) * C + chunk * 8;
+      } else {           // W_o columns h0.., 16 rows (channels) per block
+        const int row = bi * 16 + (l >> 2), chunk = (l & 3) ^ ((row >> 1) & 3);
+        src = a.wo + (size_t)row * HID + h0 + chunk * 8;
+      }
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(base + region * 4096 + bi * 512), 16, 0, 0);
+    }
+  };
+  if (Q > 0) issue(0);
+  if (Q > 1) issue(1);
+
+  const int sa_off = r16 * C;                  // + hb*16*C + slot*8
+  const int so_sw = (r16 >> 1) & 3;
+  int q = 0;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r0 = tile * kTpRows;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    barrier_nofence();  // every wave is done with the previous tile's xs
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      stage_ln_tile<ZT, bf16, C>(
+          [&](int r) -> const ZT* {
+            const int64_t row = r0 + half * 128 + r;
+            return row < a.rows ? a.x + row * C : nullptr;
+          },
+          a.ln_w, a.ln_b, a.eps, xs + half * 128 * LDX);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    barrier_nofence();
+    Frag<bf16> xf[2][kC];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) tile_frags<bf16, C>(xs, 2 * w + rb, xf[rb]);
+    f32x4 acc[2][NCB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int hc = 0; hc < NCHUNK; ++hc, ++q) {
+      // this wave's loads of chunk q landed (the next chunk may be in flight;
+      // at a tile's first chunk the previous tile's stores are drained too)
+      if (hc > 0 && q + 1 < Q) {
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      }
+      barrier_nofence();
+      if (q + 2 < Q) issue(q + 2);
+      const bf16* wa = ws[q % kTpStages];
+      const bf16* wb = wa + 4096;
+      const bf16* wo = wa + 8192;
+      Frag<bf16> fa[2][kC], fb[2][kC];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+          const int off = sa_off + hb * 16 * C + ((4 * t + g) ^ r16) * 8;
+          fa[hb][t].load(wa + off);
+          fb[hb][t].load(wb + off);
+        }
+      Frag<bf16> fo[NCB];  // W_o[c][h0 + slot]: hidden 4g..4g+3 and 16+4g..16+4g+3
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const bf16* row = wo + (cb * 16 + r16) * kTrHid + 4 * (g & 1);
+        float v[8];
+        load4(row + (((g >> 1)) ^ so_sw) * 8, v);
+        load4(row + ((2 + (g >> 1)) ^ so_sw) * 8, v + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fo[cb].set(e, v[e]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        Frag<bf16> hf;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+          for (int t = 0; t < kC; ++t) {
+            mma(sa, fa[hb][t], xf[rb][t]);
+            mma(sb, fb[hb][t], xf[rb][t]);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) mma(acc[rb][cb], fo[cb], hf);
+      }
+    }
+    // epilogue: lane holds row (2w+rb)*16 + r16, channels cb*16 + 4g + e
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int64_t row = r0 + (2 * w + rb) * 16 + r16;
+      const bool valid = row < a.rows;
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const int c0 = cb * 16 + 4 * g;
+        float base[4] = {0.f, 0.f, 0.f, 0.f};
+        if (valid && a.add) load4(a.x + row * C + c0, base);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[rb][cb][e] += base[e];
+        if (valid) store4(a.out + row * C + c0, acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2],
+                          acc[rb][cb][3]);
+      }
+      if (a.pb_out) pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, valid);
+    }
+  }
+}
+
 }  // namespace odde
 
 using namespace odde;
@@ -241,7 +387,11 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
   p.pb_out = a->pb_heads ? a->pb_out : nullptr;
   p.pb_eps = a->pb_eps;
   LaunchScope ls(ODDE_K_TRANSITION, st);
-  if (a->c == 128 && a->n_factor == 4) launch_tr<ZT, CT, 4, 4>(p, st);
+  if (a->c == 128 && a->n_factor == 4) {
+    const int64_t ntiles = (p.rows + kTpRows - 1) / kTpRows;
+    const int grid = (int)std::min<int64_t>(ntiles, 256);
+    hipLaunchKernelGGL((transition_pipe_kernel<ZT>), dim3(grid), dim3(512), 0, st, p, ntiles);
+  }
   else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
   else if (a->c == 256 && a->n_factor == 4) launch_tr<ZT, CT, 8, 4>(p, st);
   else return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256} with n = 4");
