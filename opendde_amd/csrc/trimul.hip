@@ -515,6 +515,26 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
                (v[e + 2] - mean) * rstd * wv[2] + bv[2], (v[e + 3] - mean) * rstd * wv[3] + bv[3]);
       }
     }
+    // residual z values of this lane's outputs, taken from the raw tile before
+    // the next tile's rows overwrite it (row r, 16-byte chunk c in slot c ^ (r & 7))
+    float res[kTileRows / 16][NBO][4];
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < NBO; ++cb) {
+        const int r = rb * 16 + r16;
+        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        constexpr int EPC = 16 / (int)sizeof(ZT);
+        const ZT* rowp = reinterpret_cast<const ZT*>(raw + r * RawTile<ZT, C>::ROW_BYTES);
+        const int chunk = c0 / EPC;
+        const ZT* src = rowp + ((chunk ^ (r & 7)) * EPC) + (c0 % EPC);
+        if (a.add) {
+          load4(src, res[rb][cb]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) res[rb][cb][e] = 0.f;
+        }
+      }
     __syncthreads();
     if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
 #pragma unroll
@@ -532,11 +552,9 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         for (int t = 0; t < kC; ++t) mma(ag, wgf[cb][t], zf[t]);
         if (yr >= n) continue;
         const int c0 = w * (C / 4) + cb * 16 + 4 * g;
-        float base[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.add) load4(a.z + (int64_t)x * a.z_s0 + (int64_t)yr * a.z_s1 + c0, base);
         float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[e] * sigmoidf_(ag[e]);
+        for (int e = 0; e < 4; ++e) r[e] = res[rb][cb][e] + ay[e] * sigmoidf_(ag[e]);
         store4(a.out + (int64_t)x * a.o_s0 + (int64_t)yr * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
       }
     }
