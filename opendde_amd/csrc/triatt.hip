@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
         a.mflag[(size_t)i * (jp >> 5) + (j0 >> 5) + l] =
             ((l == 0 ? bal : bal >> 32) & 0xffffffffull) != 0;
     }
-    __syncthreads();
+    lds_barrier();  // xs and keep_s ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
     if (threadIdx.x < kTileRows) {
       const int t = threadIdx.x, kb = t >> 5, sl = t & 31;
@@ -968,7 +968,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
             *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
       }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> xf[kHD];
@@ -987,7 +987,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
                base[1] + acc[1], base[2] + acc[2], base[3] + acc[3]);
       }
     }
-    __syncthreads();
+    lds_barrier();  // xo is rewritten for the next tile
   }
 }
 

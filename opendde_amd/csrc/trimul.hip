@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
                     ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
                     : 0.f;
     }
-    __syncthreads();
+    lds_barrier();  // xs and mk_s ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
@@ -535,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
           for (int e = 0; e < 4; ++e) res[rb][cb][e] = 0.f;
         }
       }
-    __syncthreads();
+    lds_barrier();  // xp and xz ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
@@ -558,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         store4(a.out + (int64_t)x * a.o_s0 + (int64_t)yr * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
       }
     }
-    __syncthreads();
+    lds_barrier();  // xp and xz are rewritten for the next tile
   }
 }
 
