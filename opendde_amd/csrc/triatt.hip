@@ -949,28 +949,64 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
 // staged in LDS.
 template <typename ZT, typename CT, int kHD, int kC>
 __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT, CT> a, int ntiles) {
-  constexpr int HD = kHD * 32, C = kC * 32, NBO = C / 64;
+  constexpr int HD = kHD * 32, C = kC * 32, NBO = C / 64, RB = kTileRows / 16;
   constexpr int LD = TileLD<CT, HD>::value;
+  constexpr int VEC = 16 / sizeof(CT), PER_ROW = HD / VEC;
+  constexpr int OCH = kTileRows * PER_ROW / 256;  // 16-byte chunks of o per thread
+  static_assert(kTileRows * PER_ROW % 256 == 0, "o tile chunks");
   __shared__ __attribute__((aligned(16))) CT xo[kTileRows * LD];
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
   Frag<CT> wof[NBO][kHD];
   load_w_slice<CT, NBO, kHD>(a.wo, HD, w * (C / 4), C, wof);
   const int jp = a.jp, n = a.n, tiles_per_row = jp / kTileRows;
+
+  // The next tile's o rows and this lane's residual values are loaded into
+  // registers while the current tile is computed.
+  f32x4 opre[OCH];
+  float rpre[RB][NBO][4];
+  auto fetch = [&](int tl) {
+    const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
+    const CT* src = a.o + ((size_t)ti * jp + tj0) * HD;
+#pragma unroll
+    for (int k = 0; k < OCH; ++k) {
+      const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
+      opre[k] = *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int jr = tj0 + rb * 16 + r16;
+#pragma unroll
+      for (int cb = 0; cb < NBO; ++cb) {
+        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        if (a.add && jr < n) {
+          load4(a.res + (int64_t)ti * a.r_s0 + (int64_t)jr * a.r_s1 + c0, rpre[rb][cb]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rpre[rb][cb][e] = 0.f;
+        }
+      }
+    }
+  };
+  if ((int)blockIdx.x < ntiles) fetch(blockIdx.x);
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int i = tile / tiles_per_row;
     const int j0 = (tile % tiles_per_row) * kTileRows;
-    {
-      constexpr int VEC = 16 / sizeof(CT), PER_ROW = HD / VEC;
-      const CT* src = a.o + ((size_t)i * jp + j0) * HD;
-      for (int ci = threadIdx.x; ci < kTileRows * PER_ROW; ci += 256) {
-        const int r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
-        *reinterpret_cast<f32x4*>(xo + r * LD + cc) =
-            *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
-      }
-    }
-    lds_barrier();
 #pragma unroll
-    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+    for (int k = 0; k < OCH; ++k) {
+      const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
+      *reinterpret_cast<f32x4*>(xo + r * LD + cc) = opre[k];
+    }
+    float res[RB][NBO][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < NBO; ++cb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) res[rb][cb][e] = rpre[rb][cb][e];
+    lds_barrier();
+    if (tile + (int)gridDim.x < ntiles) fetch(tile + gridDim.x);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
       Frag<CT> xf[kHD];
       tile_frags<CT, HD>(xo, rb, xf);
       const int jr = j0 + rb * 16 + r16;
@@ -981,10 +1017,8 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
         for (int t = 0; t < kHD; ++t) mma(acc, wof[cb][t], xf[t]);
         if (jr >= n) continue;
         const int c0 = w * (C / 4) + cb * 16 + 4 * g;
-        float base[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.add) load4(a.res + (int64_t)i * a.r_s0 + (int64_t)jr * a.r_s1 + c0, base);
-        store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jr * a.o_s1 + c0, base[0] + acc[0],
-               base[1] + acc[1], base[2] + acc[2], base[3] + acc[3]);
+        store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jr * a.o_s1 + c0, res[rb][cb][0] + acc[0],
+               res[rb][cb][1] + acc[1], res[rb][cb][2] + acc[2], res[rb][cb][3] + acc[3]);
       }
     }
     lds_barrier();  // xo is rewritten for the next tile
@@ -1196,7 +1230,7 @@ bool launch_proj_ws(const TriattProjArgs<ZT, CT>& p, int C, int HD, int n, int j
 template <typename ZT, typename CT, int kHD, int kC>
 void launch_out_ws_t(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   const int ntiles = n * (jp / kTileRows);
-  hipLaunchKernelGGL((triatt_out_ws_kernel<ZT, CT, kHD, kC>), dim3(min(ntiles, 2 * 256)),
+  hipLaunchKernelGGL((triatt_out_ws_kernel<ZT, CT, kHD, kC>), dim3(min(ntiles, 3 * 256)),
                      dim3(256), 0, st, p, ntiles);
 }
 template <typename ZT, typename CT>

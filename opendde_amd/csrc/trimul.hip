@@ -468,20 +468,43 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         },
         raw);
   };
-  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
+  // P[:, x, y0:y0+64] of the next tile is loaded into registers while the
+  // current tile is computed, then written transposed to xp[y][c]: thread t
+  // holds channels PCH*(t/8) .. +PCH-1 at rows 8*(t%8) .. +7 and writes
+  // them as eight PCH-channel row pieces.
+  static_assert(sizeof(CT) == 2 && kTileRows == 64, "bf16 P, 64-row tiles");
+  constexpr int PCH = CH / 32;  // channels per thread (16-byte loads of 8 rows each)
+  f32x4 ppre[PCH];
+  const int pcg = threadIdx.x >> 3, pyb = threadIdx.x & 7;
+  auto pfetch = [&](int tl) {
+    const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;
+    const CT* src = a.P + (size_t)tx * np + ty0 + 8 * pyb;
+#pragma unroll
+    for (int k = 0; k < PCH; ++k)
+      ppre[k] = *reinterpret_cast<const f32x4*>(src + (size_t)(PCH * pcg + k) * np * np);
+  };
+  if ((int)blockIdx.x < ntiles) {
+    issue(blockIdx.x);
+    pfetch(blockIdx.x);
+  }
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
-    {  // P[:, x, y0:y0+64] -> xp[y][c]
-      constexpr int VEC = 16 / sizeof(CT), PER_C = kTileRows / VEC;
-      const CT* src = a.P + (size_t)x * np + y0;
-      for (int ci = threadIdx.x; ci < CH * PER_C; ci += 256) {
-        const int c = ci / PER_C, yy = (ci % PER_C) * VEC;
-        CT v[VEC];
-        *reinterpret_cast<f32x4*>(v) =
-            *reinterpret_cast<const f32x4*>(src + (size_t)c * np * np + yy);
+    {
+      CT v[PCH][8];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) xp[(yy + e) * LDP + c] = v[e];
+      for (int k = 0; k < PCH; ++k) *reinterpret_cast<f32x4*>(v[k]) = ppre[k];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        CT rowv[PCH];
+#pragma unroll
+        for (int k = 0; k < PCH; ++k) rowv[k] = v[k][e];
+        CT* dst = xp + (8 * pyb + e) * LDP + PCH * pcg;
+        if constexpr (PCH == 4) {
+          *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(rowv);
+        } else {
+          *reinterpret_cast<unsigned*>(dst) = *reinterpret_cast<const unsigned*>(rowv);
+        }
       }
     }
     raw_tile_wait();  // z rows landed; every wave is done with the previous tile
@@ -536,7 +559,10 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         }
       }
     lds_barrier();  // xp and xz ready; raw consumed
-    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
+    if (tile + (int)gridDim.x < ntiles) {
+      issue(tile + gridDim.x);  // raw is free again
+      pfetch(tile + gridDim.x);
+    }
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> pf[kCH], zf[kC];
