@@ -266,8 +266,13 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
   __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float keep_s[kTileRows];
+  __shared__ float lnp[2 * C];  // LayerNorm weight, bias
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int H = a.heads, jp = a.jp, n = a.n;
+  for (int t = threadIdx.x; t < C; t += 256) {
+    lnp[t] = a.ln_w[t];
+    lnp[C + t] = a.ln_b[t];
+  }
   const CT* W = w == 0 ? a.wq : w == 1 ? a.wk : w == 2 ? a.wv : a.wg;
   Frag<CT> wf[NB][kC];
   load_w_slice<CT, NB, kC>(W, C, 0, HD, wf);
@@ -287,17 +292,31 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
         },
         raw);
   };
-  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
+  // the next tile's mask value (wave 0, lane = key) and row flag are loaded
+  // with its z rows, so no global load latency sits inside a tile
+  float mnext = 1.f;
+  int aknext = 0;
+  auto mfetch = [&](int tl) {
+    const int ti = tl / tiles_per_row, j = (tl % tiles_per_row) * kTileRows + l;
+    if (w == 0 && a.mask && j < n) mnext = a.mask[(int64_t)ti * a.m_s0 + (int64_t)j * a.m_s1];
+    aknext = a.anykeep[ti];
+  };
+  if ((int)blockIdx.x < ntiles) {
+    issue(blockIdx.x);
+    mfetch(blockIdx.x);
+  }
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int i = tile / tiles_per_row;
     const int j0 = (tile % tiles_per_row) * kTileRows;
+    const float mcur = mnext;
+    const bool zero_v = aknext != 0;
     raw_tile_wait();  // also: every wave is done with the previous tile's xs
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, a.ln_w, a.ln_b, a.eps, xs);
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, lnp, lnp + C, a.eps, xs);
     if (w == 0) {  // mask row of the tile's 64 keys (lane l = key j0 + l)
       const int j = j0 + l;
       float mv = -INFINITY, kp = 0.f;
       if (j < n) {
-        const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)j * a.m_s1] : 1.0f;
+        const float m = mcur;
         mv = (m - 1.0f) * a.mask_inf;
         kp = m == 1.0f ? 1.f : 0.f;
       }
@@ -309,13 +328,15 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
             ((l == 0 ? bal : bal >> 32) & 0xffffffffull) != 0;
     }
     lds_barrier();  // xs and keep_s ready; raw consumed
-    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
+    if (tile + (int)gridDim.x < ntiles) {
+      issue(tile + gridDim.x);  // raw is free again
+      mfetch(tile + gridDim.x);
+    }
     if (threadIdx.x < kTileRows) {
       const int t = threadIdx.x, kb = t >> 5, sl = t & 31;
       a.keep[((size_t)i * (jp >> 5) + (j0 >> 5) + kb) * 32 + sl] =
           from_f32<CT>(keep_s[kb * 32 + slot_key(sl >> 3, sl & 7)]);
     }
-    const bool zero_v = a.anykeep[i] != 0;
     float knm[kHD];
 #pragma unroll
     for (int h = 0; h < kHD; ++h) knm[h] = 0.f;

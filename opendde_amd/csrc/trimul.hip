@@ -385,7 +385,12 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float mk_s[kTileRows];
+  __shared__ float lnp[2 * C];  // LayerNorm weight, bias
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  for (int t = threadIdx.x; t < C; t += 256) {
+    lnp[t] = a.ln_w[t];
+    lnp[C + t] = a.ln_b[t];
+  }
   const int which = w >> 1, half = w & 1;
   const int o0 = which * CH + half * (CH / 2);
   Frag<CT> wpf[NB][kC], wgf[NB][kC];
@@ -403,21 +408,32 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
         },
         raw);
   };
-  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
+  // wave 0 loads the next tile's mask values (lane = column) with its z rows
+  float mnext = 0.f;
+  auto mfetch = [&](int tl) {
+    const int tx = tl / tiles_per_row, y = (tl % tiles_per_row) * kTileRows + l;
+    if (w == 0)
+      mnext = (tx < n && y < n)
+                  ? (a.mask ? a.mask[(int64_t)tx * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
+                  : 0.f;
+  };
+  if ((int)blockIdx.x < ntiles) {
+    issue(blockIdx.x);
+    mfetch(blockIdx.x);
+  }
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
+    const float mcur = mnext;
     raw_tile_wait();  // also: every wave is done with the previous tile
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, a.ln_w, a.ln_b,
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, lnp, lnp + C,
                            a.eps, xs);
-    if (w == 0) {
-      const int y = y0 + l;
-      mk_s[l] = (x < n && y < n)
-                    ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
-                    : 0.f;
-    }
+    if (w == 0) mk_s[l] = mcur;
     lds_barrier();  // xs and mk_s ready; raw consumed
-    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);  // raw is free again
+    if (tile + (int)gridDim.x < ntiles) {
+      issue(tile + gridDim.x);  // raw is free again
+      mfetch(tile + gridDim.x);
+    }
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> xf[kC];
@@ -455,7 +471,16 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   __shared__ __attribute__((aligned(16))) CT xp[kTileRows * LDP];
   __shared__ __attribute__((aligned(16))) CT xz[kTileRows * TileLD<CT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
+  __shared__ float lnp[2 * C + 2 * CH];  // LN_in weight, bias; LN_out weight, bias
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  for (int t = threadIdx.x; t < C; t += 256) {
+    lnp[t] = a.ln_in_w[t];
+    lnp[C + t] = a.ln_in_b[t];
+  }
+  for (int t = threadIdx.x; t < CH; t += 256) {
+    lnp[2 * C + t] = a.ln_out_w[t];
+    lnp[2 * C + CH + t] = a.ln_out_b[t];
+  }
   Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
   load_w_slice<CT, NBO, kCH>(a.wz, CH, w * (C / 4), C, wzf);
   load_w_slice<CT, NBO, kC>(a.wg, C, w * (C / 4), C, wgf);
@@ -508,8 +533,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       }
     }
     raw_tile_wait();  // z rows landed; every wave is done with the previous tile
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return y0 + r < n; }, a.ln_in_w, a.ln_in_b, a.eps,
-                           xz);
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return y0 + r < n; }, lnp, lnp + C, a.eps, xz);
     {  // LN_out over the channels of each staged P row, in place
       constexpr int Q = CH / 4;
       const int r = threadIdx.x >> 2, quarter = threadIdx.x & 3;
@@ -532,8 +556,8 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
 #pragma unroll
       for (int e = 0; e < Q; e += 4) {
         float wv[4], bv[4];
-        load4(a.ln_out_w + quarter * Q + e, wv);
-        load4(a.ln_out_b + quarter * Q + e, bv);
+        load4(lnp + 2 * C + quarter * Q + e, wv);
+        load4(lnp + 2 * C + CH + quarter * Q + e, bv);
         store4(row + e, (v[e] - mean) * rstd * wv[0] + bv[0], (v[e + 1] - mean) * rstd * wv[1] + bv[1],
                (v[e + 2] - mean) * rstd * wv[2] + bv[2], (v[e + 3] - mean) * rstd * wv[3] + bv[3]);
       }
