@@ -50,7 +50,8 @@ constexpr int kTrHid = 32;    // hidden units per chunk
 template <typename ZT, typename CT, int kC>
 __device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>& a,
                                                    const f32x4 (&zacc)[kC * 2], int64_t row,
-                                                   bool valid) {
+                                                   bool valid, const float* pb_ln_w,
+                                                   const float* pb_ln_b, const CT* pb_w) {
   constexpr int C = kC * 32, NCB = C / 16;
   const int l = lane_id(), g = l >> 4, r16 = l & 15;
   float zv[NCB][4];
@@ -80,14 +81,14 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>&
 #pragma unroll
   for (int t = 0; t < kC; ++t) {
     float lw[8], lb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, wv[8];
-    load4(a.pb_ln_w + 32 * t + 4 * g, lw);
-    load4(a.pb_ln_w + 32 * t + 16 + 4 * g, lw + 4);
-    if (a.pb_ln_b) {
-      load4(a.pb_ln_b + 32 * t + 4 * g, lb);
-      load4(a.pb_ln_b + 32 * t + 16 + 4 * g, lb + 4);
+    load4(pb_ln_w + 32 * t + 4 * g, lw);
+    load4(pb_ln_w + 32 * t + 16 + 4 * g, lw + 4);
+    if (pb_ln_b) {
+      load4(pb_ln_b + 32 * t + 4 * g, lb);
+      load4(pb_ln_b + 32 * t + 16 + 4 * g, lb + 4);
     }
-    load4(a.pb_w + r16 * C + 32 * t + 4 * g, wv);
-    load4(a.pb_w + r16 * C + 32 * t + 16 + 4 * g, wv + 4);
+    load4(pb_w + r16 * C + 32 * t + 4 * g, wv);
+    load4(pb_w + r16 * C + 32 * t + 16 + 4 * g, wv + 4);
     Frag<CT> yf, wf;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -207,7 +208,8 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
         if (valid) store4(a.out + row * C + c0, acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2],
                           acc[rb][cb][3]);
       }
-      if (a.pb_out) pair_bias_epilogue<ZT, CT, kC>(a, acc[rb], row, valid);
+      if (a.pb_out)
+        pair_bias_epilogue<ZT, CT, kC>(a, acc[rb], row, valid, a.pb_ln_w, a.pb_ln_b, a.pb_w);
     }
     __syncthreads();  // xs reused by the next tile
   }
@@ -234,7 +236,19 @@ __global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<
   constexpr int LDX = TileLD<bf16, C>::value;
   __shared__ __attribute__((aligned(16))) bf16 xs[kTpRows * LDX];
   __shared__ __attribute__((aligned(16))) bf16 ws[kTpStages][kTpChunkElems];
+  // parameters read every tile, kept in LDS: LN weight, bias; and for the
+  // pair-bias epilogue its LN weight, bias and the 16 x C projection
+  __shared__ __attribute__((aligned(16))) float lnp[4 * C];
+  __shared__ __attribute__((aligned(16))) bf16 pbw[16 * C];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  for (int t = threadIdx.x; t < C; t += 512) {
+    lnp[t] = a.ln_w[t];
+    lnp[C + t] = a.ln_b[t];
+    lnp[2 * C + t] = a.pb_out ? a.pb_ln_w[t] : 0.f;
+    lnp[3 * C + t] = (a.pb_out && a.pb_ln_b) ? a.pb_ln_b[t] : 0.f;
+  }
+  if (a.pb_out)
+    for (int t = threadIdx.x; t < 16 * C; t += 512) pbw[t] = a.pb_w[t];
 
   // this workgroup's tiles and chunk loads (only loads that will be consumed
   // are issued, so none is in flight when the workgroup ends)
@@ -277,7 +291,7 @@ __global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<
             const int64_t row = r0 + half * 128 + r;
             return row < a.rows ? a.x + row * C : nullptr;
           },
-          a.ln_w, a.ln_b, a.eps, xs + half * 128 * LDX);
+          lnp, lnp + C, a.eps, xs + half * 128 * LDX);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     barrier_nofence();
     Frag<bf16> xf[2][kC];
@@ -354,7 +368,8 @@ __global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<
         if (valid) store4(a.out + row * C + c0, acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2],
                           acc[rb][cb][3]);
       }
-      if (a.pb_out) pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, valid);
+      if (a.pb_out)
+        pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, valid, lnp + 2 * C, lnp + 3 * C, pbw);
     }
   }
 }
