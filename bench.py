@@ -16,7 +16,9 @@ stream it runs on.  ``roofline.traffic`` is the dominant kernel's HBM bytes
 per launch from the committed rocprofv3 --pmc summary of this workload
 (profiles/pmc_traffic_trunk_n<N>.json, made with ``--pmc-probe``), or null.
 ``cpu_baseline`` times the CPU oracle (fp32) on one block of the same
-workload on this host.
+workload on this host.  ``layer_norm`` times the standalone fast LayerNorm
+(forward and backward) on the workload's pair tensor shape, N*N x 128 bf16,
+outside the trunk step.
 """
 
 from __future__ import annotations
@@ -133,6 +135,57 @@ def load_traffic(n: int):
         return json.load(f).get("bytes_per_launch", {})
 
 
+def layer_norm_measure(n: int, dev, reps: int = 20):
+    """Standalone pair LayerNorm of the workload (N*N rows x 128, bf16, with
+    weight and bias) through the fast-LayerNorm entry points: forward and
+    backward average launch time from the library's HIP events, algorithmic
+    HBM bytes per launch (forward: read x, write out, write mean and invvar;
+    backward: read x, dout, mean and invvar, write grad_input), and torch's
+    own F.layer_norm forward on the same tensor for comparison."""
+    from opendde_amd import fast_layer_norm as fln
+    rows, c = n * n, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(rows, c, generator=g, device=dev).to(torch.bfloat16)
+    dout = torch.randn(rows, c, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(c, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(c, generator=g, device=dev).to(torch.bfloat16)
+    _, mean, invvar = fln.forward_with_both_affine(x, (c,), w, b, 1e-5)
+    fln.backward_with_both_affine(dout, mean, invvar, x, (c,), w, b, 1e-5)
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    for _ in range(reps):
+        fln.forward_with_both_affine(x, (c,), w, b, 1e-5)
+        fln.backward_with_both_affine(dout, mean, invvar, x, (c,), w, b, 1e-5)
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    f_tot, f_cnt = _lib.timing_query(_lib.K_LAYER_NORM)
+    b_tot, b_cnt = _lib.timing_query(_lib.K_LAYER_NORM_BWD)
+    _lib.timing_reset()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.nn.functional.layer_norm(x, (c,), w, b, 1e-5)
+    e0.record()
+    for _ in range(reps):
+        torch.nn.functional.layer_norm(x, (c,), w, b, 1e-5)
+    e1.record()
+    torch.cuda.synchronize()
+    torch_ms = e0.elapsed_time(e1) / reps
+    fwd_bytes = rows * c * 2 * 2 + rows * 8
+    bwd_bytes = rows * c * 2 * 3 + rows * 8
+    f_ms, b_ms = f_tot / f_cnt, b_tot / b_cnt
+    res = {"rows": rows, "n2": c, "dtype": "bf16", "affine": "both",
+           "fwd_avg_ms": round(f_ms, 4), "fwd_bytes": fwd_bytes,
+           "fwd_gbs": round(fwd_bytes / (f_ms * 1e-3) / 1e9, 1),
+           "bwd_avg_ms": round(b_ms, 4), "bwd_bytes": bwd_bytes,
+           "bwd_gbs": round(bwd_bytes / (b_ms * 1e-3) / 1e9, 1),
+           "torch_fwd_ms": round(torch_ms, 4)}
+    res["fwd_pct_hbm_peak"] = round(100 * res["fwd_gbs"] / PEAK_HBM_GBS, 2)
+    res["bwd_pct_hbm_peak"] = round(100 * res["bwd_gbs"] / PEAK_HBM_GBS, 2)
+    del x, dout, mean, invvar
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +195,8 @@ def main():
     ap.add_argument("--blocks", type=int, default=48)
     ap.add_argument("--cpu-sample-n", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-layer-norm", action="store_true",
+                    help="skip the standalone fast-LayerNorm measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "
                          "size, then one trunk step over a single block; prints nothing else")
@@ -258,6 +313,7 @@ def main():
         "kernels": kernels,
         "roofline": roof,
         "cpu_baseline": None,
+        "layer_norm": None if args.no_layer_norm else layer_norm_measure(n, dev),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_n, chunk=128)

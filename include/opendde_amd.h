@@ -29,6 +29,7 @@ extern "C" {
 /* element types */
 #define ODDE_F32 0
 #define ODDE_BF16 1
+#define ODDE_F16 2 /* LayerNorm entry points only */
 
 /* status codes */
 #define ODDE_OK 0
@@ -46,7 +47,9 @@ extern "C" {
 #define ODDE_K_TRIMUL_OUT 5
 #define ODDE_K_TRIATT_RELAYOUT 6
 #define ODDE_K_TRANSITION 7
-#define ODDE_K_COUNT 8
+#define ODDE_K_LAYER_NORM 8
+#define ODDE_K_LAYER_NORM_BWD 9
+#define ODDE_K_COUNT 10
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -206,6 +209,62 @@ typedef struct odde_transition_args {
 } odde_transition_args;
 
 int odde_transition_fwd(const odde_transition_args* args, void* hip_stream);
+
+/*
+ * LayerNorm over the last n2 elements of n1 contiguous rows, forward and
+ * backward: the contract of the reference's optional fast LayerNorm
+ * extension (its 8 entry points forward_{none,with_bias,with_weight,
+ * with_both}_affine / backward_*, opendde/model/layer_norm/layer_norm.py:
+ * 31-40, bound in kernel/layer_norm_cuda.cpp:143-180), selected there by
+ * LAYERNORM_TYPE=fast_layernorm (opendde/model/triangular/layers.py:24-29).
+ *   forward:  mean[r], invvar[r] = 1/sqrt(var[r] + eps) (f32, biased var);
+ *             out = (x - mean) * invvar * gamma + beta
+ *   backward: xhat = (x - mean) * invvar, g = dout * gamma,
+ *             grad_input = invvar * (g - (sum g + xhat * sum g*xhat) / n2)
+ *             grad_gamma = sum_rows dout * xhat, grad_beta = sum_rows dout
+ * x, out, dout, grad_input, gamma, beta, grad_gamma, grad_beta share dtype
+ * (ODDE_F32, ODDE_BF16 or ODDE_F16; statistics and sums are f32), all
+ * contiguous [n1][n2] / [n2].  gamma / beta (and their gradients) may be
+ * NULL; a NULL grad_gamma / grad_beta skips that sum.  When either is
+ * requested the backward needs a workspace (16-byte aligned) for partial
+ * column sums, of the size odde_layer_norm_bwd_workspace_bytes returns (a
+ * function of n1, n2 and dtype only).  Results are deterministic.  n1 == 0
+ * writes zero parameter gradients.
+ */
+typedef struct odde_layer_norm_args {
+  uint32_t struct_size;
+  int32_t dtype;
+  int64_t n1;
+  int32_t n2;
+  float eps;
+  const void* x;
+  const void* gamma; /* may be NULL */
+  const void* beta;  /* may be NULL */
+  void* out;
+  float* mean;
+  float* invvar;
+} odde_layer_norm_args;
+
+typedef struct odde_layer_norm_bwd_args {
+  uint32_t struct_size;
+  int32_t dtype;
+  int64_t n1;
+  int32_t n2;
+  const void* dout;
+  const float* mean;
+  const float* invvar;
+  const void* x;
+  const void* gamma;   /* may be NULL (then g = dout) */
+  void* grad_input;
+  void* grad_gamma;    /* may be NULL */
+  void* grad_beta;     /* may be NULL */
+  void* workspace;
+  uint64_t workspace_bytes;
+} odde_layer_norm_bwd_args;
+
+int odde_layer_norm_fwd(const odde_layer_norm_args* args, void* hip_stream);
+int odde_layer_norm_bwd_workspace_bytes(const odde_layer_norm_bwd_args* args, uint64_t* bytes);
+int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* args, void* hip_stream);
 
 /* Instrumentation (no counterpart in the reference): per-kernel launch
  * counters (always on), and optional HIP-event timing of every launch on the

@@ -20,16 +20,17 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("OPENDDE_AMD_LIB", os.path.join(HERE, "lib", "libopendde_amd.so"))
 ABI_VERSION = 1
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 K_TRIATT_PROJ, K_TRIATT_CORE, K_TRIATT_OUT = 0, 1, 2
 K_TRIMUL_PROJ, K_TRIMUL_CONTRACT, K_TRIMUL_OUT = 3, 4, 5
 K_TRIATT_RELAYOUT = 6
 K_TRANSITION = 7
+K_LAYER_NORM, K_LAYER_NORM_BWD = 8, 9
 KERNEL_NAMES = {
     K_TRIATT_PROJ: "triatt_proj", K_TRIATT_CORE: "triatt_core", K_TRIATT_OUT: "triatt_out",
     K_TRIMUL_PROJ: "trimul_proj", K_TRIMUL_CONTRACT: "trimul_contract",
     K_TRIMUL_OUT: "trimul_out", K_TRIATT_RELAYOUT: "triatt_relayout",
-    K_TRANSITION: "transition",
+    K_TRANSITION: "transition", K_LAYER_NORM: "layer_norm", K_LAYER_NORM_BWD: "layer_norm_bwd",
 }
 
 _i32, _i64, _u32, _u64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
@@ -91,6 +92,22 @@ class TransitionArgs(ctypes.Structure):
     ]
 
 
+class LayerNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", _u32), ("dtype", _i32), ("n1", _i64), ("n2", _i32), ("eps", _f32),
+        ("x", _vp), ("gamma", _vp), ("beta", _vp), ("out", _vp), ("mean", _vp), ("invvar", _vp),
+    ]
+
+
+class LayerNormBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", _u32), ("dtype", _i32), ("n1", _i64), ("n2", _i32),
+        ("dout", _vp), ("mean", _vp), ("invvar", _vp), ("x", _vp), ("gamma", _vp),
+        ("grad_input", _vp), ("grad_gamma", _vp), ("grad_beta", _vp),
+        ("workspace", _vp), ("workspace_bytes", _u64),
+    ]
+
+
 # Every symbol include/opendde_amd.h declares, with its ctypes signature.
 SYMBOLS = {
     "odde_abi_version": (_i32, []),
@@ -102,6 +119,10 @@ SYMBOLS = {
     "odde_trimul_workspace_bytes": (_i32, [ctypes.POINTER(TrimulArgs), ctypes.POINTER(_u64)]),
     "odde_trimul_fwd": (_i32, [ctypes.POINTER(TrimulArgs), _vp]),
     "odde_transition_fwd": (_i32, [ctypes.POINTER(TransitionArgs), _vp]),
+    "odde_layer_norm_fwd": (_i32, [ctypes.POINTER(LayerNormArgs), _vp]),
+    "odde_layer_norm_bwd_workspace_bytes": (_i32, [ctypes.POINTER(LayerNormBwdArgs),
+                                                   ctypes.POINTER(_u64)]),
+    "odde_layer_norm_bwd": (_i32, [ctypes.POINTER(LayerNormBwdArgs), _vp]),
     "odde_launch_count": (_i64, [_i32]),
     "odde_timing_enable": (_i32, [_i32]),
     "odde_timing_reset": (_i32, []),

@@ -9,12 +9,22 @@ parameters directly.
 from __future__ import annotations
 
 import math
+import os
 from functools import partial
 from typing import Optional
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+
+# LayerNorm selection, read once at import as the reference does
+# (layers.py:24-29).
+_use_fast_layer_norm = os.getenv("LAYERNORM_TYPE", "torch") == "fast_layernorm"
+if _use_fast_layer_norm:
+    try:
+        from .layer_norm import FusedLayerNorm
+    except (ImportError, OSError, RuntimeError):
+        _use_fast_layer_norm = False
 
 # std of a standard normal truncated to [-2, 2]:
 # var = 1 - 2*2*phi(2) / (Phi(2) - Phi(-2))
@@ -105,7 +115,12 @@ class OpenFoldLayerNorm(nn.Module):
 
 def LayerNorm(c_in: int, create_scale: bool = True, create_offset: bool = True,
               eps: float = 1e-5) -> nn.Module:
-    """Factory of the reference (layers.py:272-282)."""
+    """Factory of the reference (layers.py:272-282): the HIP ``FusedLayerNorm``
+    when ``LAYERNORM_TYPE=fast_layernorm`` was set at import, else
+    ``OpenFoldLayerNorm``.  Both carry ``weight`` / ``bias`` / ``eps``."""
+    if _use_fast_layer_norm:
+        return FusedLayerNorm(c_in, create_scale=create_scale, create_offset=create_offset,
+                              eps=eps)
     return OpenFoldLayerNorm(c_in, create_scale, create_offset, eps)
 
 

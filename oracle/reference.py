@@ -37,6 +37,10 @@ LN_EPS = 1e-5
 PINNED_BY = {
     "layer_norm": "torch.nn.functional.layer_norm (library) + float64 brute force",
     "linear": "float64 brute force",
+    "layer_norm_fwd": "torch.nn.functional.layer_norm (library) + float64 brute force; "
+    "statistics == torch.var_mean",
+    "layer_norm_bwd": "torch autograd of F.layer_norm (library) + float64 brute force "
+    "(loops over the derivative definition); sum_c grad_input == 0",
     "attention_core": "float64 brute force; SDPA library routine with zero bias; "
     "key-permutation invariance; fully-masked row == mean(V)",
     "triangle_attention": "float64 brute force (start and end); "
@@ -80,6 +84,48 @@ def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor],
     if bias is not None:
         y = y + bias.to(x.dtype)
     return y
+
+
+def layer_norm_fwd(x: torch.Tensor, n2: int, gamma: Optional[torch.Tensor],
+                   beta: Optional[torch.Tensor], eps: float = LN_EPS):
+    """Fast LayerNorm forward contract: ``(out, mean, invvar)`` over the last
+    ``n2`` elements of each row, ``mean`` / ``invvar`` of shape ``[n1]``
+    (layer_norm/kernel/layer_norm_cuda.cpp:73-90; row statistics in
+    layer_norm_cuda_kernel.cu:145-229: biased variance,
+    invvar = 1/sqrt(var + eps), out = (x - mean) * invvar * gamma + beta).
+    Statistics are computed in float64 when ``x`` is float64, else float32."""
+    sd = torch.float64 if x.dtype == torch.float64 else torch.float32
+    xf = x.reshape(-1, n2).to(sd)
+    mu = xf.mean(dim=1)
+    xc = xf - mu[:, None]
+    invvar = torch.rsqrt((xc * xc).mean(dim=1) + eps)
+    y = xc * invvar[:, None]
+    if gamma is not None:
+        y = y * gamma.reshape(n2).to(sd)
+    if beta is not None:
+        y = y + beta.reshape(n2).to(sd)
+    return y.to(x.dtype).reshape(x.shape), mu, invvar
+
+
+def layer_norm_bwd(dout: torch.Tensor, mean: torch.Tensor, invvar: torch.Tensor,
+                   x: torch.Tensor, n2: int, gamma: Optional[torch.Tensor]):
+    """Fast LayerNorm backward contract: ``(grad_input, grad_gamma,
+    grad_beta)`` (layer_norm_cuda.cpp:99-139; layer_norm_cuda_kernel.cu:
+    412-836).  With xhat = (x - mean) * invvar and g = dout * gamma (dout when
+    gamma is absent):
+        grad_input = invvar * (g - mean_c(g) - xhat * mean_c(g * xhat))
+        grad_gamma = sum_rows dout * xhat,  grad_beta = sum_rows dout.
+    Computed in float64 when ``x`` is float64, else float32; the parameter
+    gradients are returned in that precision."""
+    sd = torch.float64 if x.dtype == torch.float64 else torch.float32
+    xf = x.reshape(-1, n2).to(sd)
+    df = dout.reshape(-1, n2).to(sd)
+    mu = mean.reshape(-1, 1).to(sd)
+    iv = invvar.reshape(-1, 1).to(sd)
+    xhat = (xf - mu) * iv
+    g = df * gamma.reshape(n2).to(sd) if gamma is not None else df
+    dx = iv * (g - g.mean(dim=1, keepdim=True) - xhat * (g * xhat).mean(dim=1, keepdim=True))
+    return dx.to(x.dtype).reshape(x.shape), (df * xhat).sum(dim=0), df.sum(dim=0)
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor,

@@ -50,6 +50,36 @@ def layer_norm_rows(x, w, b):
     return out
 
 
+def layer_norm_backward_rows(x, w, dout):
+    """grad_input[r][c] = sum_o dout[r][o] * d ln(x[r])[o] / d x[r][c] and
+    grad_w[c] = sum_r dout[r][c] * xhat[r][c], grad_b[c] = sum_r dout[r][c],
+    from the derivative of LN written out element by element:
+        xhat_o = (x_o - mu) r,   r = (var + eps)^(-1/2)
+        d xhat_o / d x_c = r (delta_oc - 1/n) - xhat_o xhat_c r / n."""
+    x, dout = _np(x), _np(dout)
+    n = x.shape[-1]
+    xf, df = x.reshape(-1, n), dout.reshape(-1, n)
+    wv = [1.0] * n if w is None else list(_np(w))
+    gi = np.zeros_like(xf)
+    gw = np.zeros(n)
+    gb = np.zeros(n)
+    for r in range(xf.shape[0]):
+        row = list(xf[r])
+        mu = sum(row) / n
+        var = sum((v - mu) ** 2 for v in row) / n
+        rs = 1.0 / math.sqrt(var + EPS)
+        xh = [(v - mu) * rs for v in row]
+        for c in range(n):
+            acc = 0.0
+            for o in range(n):
+                dxh = rs * ((1.0 if o == c else 0.0) - 1.0 / n) - xh[o] * xh[c] * rs / n
+                acc += df[r][o] * wv[o] * dxh
+            gi[r][c] = acc
+            gw[c] += df[r][c] * xh[c]
+            gb[c] += df[r][c]
+    return gi.reshape(x.shape), gw, gb
+
+
 def triangle_attention(z, mask, p, H, starting=True):
     """Alg. 13 (starting node), for every (i, j) and head h:
         a[k] = softmax_k( q_h[i,j].k_h[i,k]/sqrt(D) + b_h[j,k] + INF*(mask[i,k]-1) )

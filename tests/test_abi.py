@@ -36,7 +36,9 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.parametrize("cname,pyty", [("odde_triatt_args", _lib.TriattArgs),
                                         ("odde_triatt_core_args", _lib.TriattCoreArgs),
                                         ("odde_trimul_args", _lib.TrimulArgs),
-                                        ("odde_transition_args", _lib.TransitionArgs)])
+                                        ("odde_transition_args", _lib.TransitionArgs),
+                                        ("odde_layer_norm_args", _lib.LayerNormArgs),
+                                        ("odde_layer_norm_bwd_args", _lib.LayerNormBwdArgs)])
 def test_struct_layout_matches_header(cname, pyty):
     fields = [f for f, _ in pyty._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",

@@ -53,6 +53,40 @@ def test_layer_norm_matches_library_and_loops():
     np.testing.assert_allclose(y.numpy(), bf.layer_norm_rows(x, w, b), rtol=1e-10, atol=1e-10)
 
 
+@pytest.mark.parametrize("affine", ["none", "bias", "weight", "both"])
+def test_fast_layer_norm_contract_matches_library_and_loops(affine):
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 5, 12, generator=g, dtype=D64) * 2 - 0.5
+    w = torch.randn(12, generator=g, dtype=D64) if affine in ("weight", "both") else None
+    b = torch.randn(12, generator=g, dtype=D64) if affine in ("bias", "both") else None
+    dout = torch.randn(3, 5, 12, generator=g, dtype=D64)
+    out, mean, invvar = ref.layer_norm_fwd(x, 12, w, b)
+    torch.testing.assert_close(out, F.layer_norm(x, (12,), w, b, 1e-5), rtol=1e-12, atol=1e-12)
+    var, mu = torch.var_mean(x.reshape(-1, 12), dim=1, unbiased=False)
+    torch.testing.assert_close(mean, mu, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(invvar, 1 / torch.sqrt(var + 1e-5), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(out.numpy(), bf.layer_norm_rows(x, w, b), rtol=1e-10, atol=1e-10)
+
+    dx, dw, db = ref.layer_norm_bwd(dout, mean, invvar, x, 12, w)
+    # library: autograd of F.layer_norm
+    xa = x.clone().requires_grad_(True)
+    wa = w.clone().requires_grad_(True) if w is not None else None
+    ba = b.clone().requires_grad_(True) if b is not None else None
+    F.layer_norm(xa, (12,), wa, ba, 1e-5).backward(dout)
+    torch.testing.assert_close(dx, xa.grad, rtol=1e-10, atol=1e-12)
+    if wa is not None:
+        torch.testing.assert_close(dw, wa.grad, rtol=1e-10, atol=1e-12)
+    if ba is not None:
+        torch.testing.assert_close(db, ba.grad, rtol=1e-10, atol=1e-12)
+    # loops over the derivative definition
+    gi, gw, gb = bf.layer_norm_backward_rows(x, w, dout)
+    np.testing.assert_allclose(dx.numpy(), gi, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(dw.numpy(), gw, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(db.numpy(), gb, rtol=1e-9, atol=1e-12)
+    # invariant: LN is shift-invariant, so the input gradient sums to zero per row
+    assert float(dx.sum(dim=-1).abs().max()) < 1e-12
+
+
 def test_attention_core_is_sdpa_without_bias():
     g = torch.Generator().manual_seed(1)
     q, k, v = (torch.randn(3, 2, 9, 4, generator=g, dtype=D64) for _ in range(3))
