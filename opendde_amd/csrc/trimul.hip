@@ -421,11 +421,17 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
     issue(blockIdx.x);
     mfetch(blockIdx.x);
   }
+  raw_tile_wait();
+  // Per tile: LN the raw tile, start the next tile's loads, compute, then wait
+  // for this wave's loads and only then issue the tile's stores (kept in
+  // registers until then), so a wave never waits for its own stores to drain:
+  // they complete while the next tile is normalised and computed.  The
+  // closing barrier makes the next raw tile complete for every wave and
+  // releases xs / mk_s.
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
     const float mcur = mnext;
-    raw_tile_wait();  // also: every wave is done with the previous tile
     raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, lnp, lnp + C,
                            a.eps, xs);
     if (w == 0) mk_s[l] = mcur;
@@ -434,11 +440,11 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
       issue(tile + gridDim.x);  // raw is free again
       mfetch(tile + gridDim.x);
     }
+    bf16x4 ov[kTileRows / 16][NB];
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       Frag<CT> xf[kC];
       tile_frags<CT, C>(xs, rb, xf);
-      const int yb = y0 + rb * 16 + 4 * g;
       float mk[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) mk[e] = mk_s[rb * 16 + 4 * g + e];
@@ -450,14 +456,21 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
           mma(ap, xf[t], wpf[cb][t]);
           mma(ag, xf[t], wgf[cb][t]);
         }
-        const int c = half * (CH / 2) + cb * 16 + r16;
-        float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = mk[e] * sigmoidf_(ag[e]) * ap[e];
-        store4(dst + ((size_t)c * np + x) * np + yb, v[0], v[1], v[2], v[3]);
+        for (int e = 0; e < 4; ++e) ov[rb][cb][e] = (bf16)(mk[e] * sigmoidf_(ag[e]) * ap[e]);
       }
     }
-    // xs and mk_s are rewritten only after the barrier in raw_tile_wait()
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next raw tile (own part) landed
+#pragma unroll
+    for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      const int yb = y0 + rb * 16 + 4 * g;
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        const int c = half * (CH / 2) + cb * 16 + r16;
+        *reinterpret_cast<bf16x4*>(dst + ((size_t)c * np + x) * np + yb) = ov[rb][cb];
+      }
+    }
+    lds_barrier();  // every wave's part of the next raw tile landed; xs, mk_s free
   }
 }
 
