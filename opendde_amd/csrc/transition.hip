@@ -215,52 +215,99 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
   }
 }
 
-// Pipelined form for C = 128, n = 4 (the pair transition): 8 waves own 256
-// rows; the hidden dimension is walked in chunks of 32 whose W_a / W_b rows
-// and W_o columns (24 KiB) stream into three LDS stages by direct global ->
-// LDS loads, two chunks ahead, continuing across row tiles (every tile walks
-// the same chunks).  One fence-free barrier per chunk: each wave waits for
-// its own loads of the chunk (vmcnt) and its LDS reads of the previous one
-// (lgkmcnt) first; the stage refilled at chunk q was last read at chunk q-1.
+// Pipelined form for C = 128, n = 4 (the pair transition).  Two workgroups
+// of 4 waves per CU; a workgroup owns 128 rows at a time, wave w rows
+// 32w..32w+31 (two 16-row blocks).  The rows never go through LDS: each wave
+// loads its rows' K32 fragment slots straight into registers and applies the
+// LayerNorm there (the four lanes of a row reduce by shuffles).  The hidden
+// dimension is walked in chunks of 32 whose W_a / W_b rows and W_o columns
+// (24 KiB) stream into three LDS stages by direct global -> LDS loads, two
+// chunks ahead, continuing across row tiles (every tile walks the same
+// chunks).  At a tile boundary the next tile's rows and this tile's residual
+// rows are loaded together, then the outputs are stored; so the loads of one
+// workgroup overlap the other workgroup's MFMA work.
 // LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
 // bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
 // (4 slots; slot t of row r holds chunk t ^ ((r >> 1) & 3)).
-constexpr int kTpRows = 256;
+constexpr int kTpRows = 128;
 constexpr int kTpStages = 3;
 constexpr int kTpChunkElems = 3 * 4096;  // W_a, W_b: 32 x 128; W_o: 128 x 32
+constexpr int kTpOps = 6;                // 1 KiB direct loads per wave per chunk
+
+// A lane's K32 fragment slots of one C = 128 row (channels 32t + 8g .. +7 for
+// t = 0..3) held as raw 16-byte chunks until they are normalised.
+template <typename ZT>
+struct RowSlots {
+  static constexpr int PER_T = 8 * (int)sizeof(ZT) / 16;  // chunks per K32 block
+  f32x4 c[4 * PER_T];
+  __device__ __forceinline__ void load(const ZT* row, int g) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int k = 0; k < PER_T; ++k)
+        c[t * PER_T + k] =
+            *reinterpret_cast<const f32x4*>(row + 32 * t + 8 * g + k * (16 / (int)sizeof(ZT)));
+  }
+  __device__ __forceinline__ void get(int t, float (&x)[8]) const {
+    if constexpr (sizeof(ZT) == 4) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = c[2 * t][e];
+        x[4 + e] = c[2 * t + 1][e];
+      }
+    } else {
+      const bf16x8 v = __builtin_bit_cast(bf16x8, c[t]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
+    }
+  }
+};
+
+// A lane's four output channels of one row (acc layout) as stored in ZT.
+template <typename ZT> struct Quad;
+template <> struct Quad<float> {
+  f32x4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ float get(int e) const { return v[e]; }
+};
+template <> struct Quad<bf16> {
+  bf16x4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x4*>(p); }
+  __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
+};
 
 template <typename ZT>
-__global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<ZT, bf16> a,
+__global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<ZT, bf16> a,
                                                                  int64_t ntiles) {
   constexpr int C = 128, kC = 4, HID = 512, NCB = C / 16, NCHUNK = HID / kTrHid;
-  constexpr int LDX = TileLD<bf16, C>::value;
-  __shared__ __attribute__((aligned(16))) bf16 xs[kTpRows * LDX];
   __shared__ __attribute__((aligned(16))) bf16 ws[kTpStages][kTpChunkElems];
   // parameters read every tile, kept in LDS: LN weight, bias; and for the
   // pair-bias epilogue its LN weight, bias and the 16 x C projection
   __shared__ __attribute__((aligned(16))) float lnp[4 * C];
   __shared__ __attribute__((aligned(16))) bf16 pbw[16 * C];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
-  for (int t = threadIdx.x; t < C; t += 512) {
+  for (int t = threadIdx.x; t < C; t += 256) {
     lnp[t] = a.ln_w[t];
     lnp[C + t] = a.ln_b[t];
     lnp[2 * C + t] = a.pb_out ? a.pb_ln_w[t] : 0.f;
     lnp[3 * C + t] = (a.pb_out && a.pb_ln_b) ? a.pb_ln_b[t] : 0.f;
   }
   if (a.pb_out)
-    for (int t = threadIdx.x; t < 16 * C; t += 512) pbw[t] = a.pb_w[t];
+    for (int t = threadIdx.x; t < 16 * C; t += 256) pbw[t] = a.pb_w[t];
+  __syncthreads();  // lnp / pbw are read before the first chunk barrier
 
   // this workgroup's tiles and chunk loads (only loads that will be consumed
   // are issued, so none is in flight when the workgroup ends)
   const int my_tiles =
       blockIdx.x < ntiles ? (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0;
+  if (my_tiles == 0) return;
   const int Q = my_tiles * NCHUNK;
   auto issue = [&](int q) {
     const int h0 = (q % NCHUNK) * kTrHid;
     bf16* base = ws[q % kTpStages];
 #pragma unroll 1
-    for (int op = 0; op < 3; ++op) {  // one address live at a time
-      const int b = w * 3 + op, region = b >> 3, bi = b & 7;  // 24 KiB = 24 blocks
+    for (int op = 0; op < kTpOps; ++op) {  // one address live at a time
+      const int b = w * kTpOps + op, region = b >> 3, bi = b & 7;  // 24 KiB = 24 blocks
       const bf16* src;
       if (region < 2) {  // W_a / W_b rows h0 + row, 4 rows per block
         const int row = bi * 4 + (l >> 4), chunk = (l & 15) ^ (row & 15);
@@ -274,29 +321,68 @@ __global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<
           (__attribute__((address_space(3))) void*)(base + region * 4096 + bi * 512), 16, 0, 0);
     }
   };
-  if (Q > 0) issue(0);
+  issue(0);
   if (Q > 1) issue(1);
+
+  auto row_of = [&](int64_t tile, int rb) -> int64_t {
+    return tile * kTpRows + (2 * w + rb) * 16 + r16;
+  };
+  RowSlots<ZT> xr[2];  // the rows of the tile about to start
+  auto load_rows = [&](int64_t tile) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int64_t row = min(row_of(tile, rb), a.rows - 1);  // pad rows read a real row
+      xr[rb].load(a.x + row * C, g);
+    }
+  };
+  load_rows(blockIdx.x);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const int sa_off = r16 * C;                  // + hb*16*C + slot*8
   const int so_sw = (r16 >> 1) & 3;
+  const float* ln_w = lnp;
+  const float* ln_b = lnp + C;
   int q = 0;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t r0 = tile * kTpRows;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    barrier_nofence();  // every wave is done with the previous tile's xs
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-      stage_ln_tile<ZT, bf16, C>(
-          [&](int r) -> const ZT* {
-            const int64_t row = r0 + half * 128 + r;
-            return row < a.rows ? a.x + row * C : nullptr;
-          },
-          lnp, lnp + C, a.eps, xs + half * 128 * LDX);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    barrier_nofence();
+    // LayerNorm of the wave's rows (already in registers) into B fragments
     Frag<bf16> xf[2][kC];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) tile_frags<bf16, C>(xs, 2 * w + rb, xf[rb]);
+    for (int rb = 0; rb < 2; ++rb) {
+      const bool valid = row_of(tile, rb) < a.rows;
+      float x[kC][8];
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < kC; ++t) {
+        xr[rb].get(t, x[t]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += x[t][e];
+      }
+      s += __shfl_xor(s, 16, 64);
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float v = 0.f;
+#pragma unroll
+      for (int t = 0; t < kC; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = x[t][e] - mean;
+          v += d * d;
+        }
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      const float rstd = rsqrtf(v * (1.0f / C) + a.eps);
+#pragma unroll
+      for (int t = 0; t < kC; ++t) {
+        float lw[8], lb[8];
+        load4(ln_w + 32 * t + 8 * g, lw);
+        load4(ln_w + 32 * t + 8 * g + 4, lw + 4);
+        load4(ln_b + 32 * t + 8 * g, lb);
+        load4(ln_b + 32 * t + 8 * g + 4, lb + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          xf[rb][t].set(e, valid ? (x[t][e] - mean) * rstd * lw[e] + lb[e] : 0.f);
+      }
+    }
     f32x4 acc[2][NCB];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
@@ -304,73 +390,102 @@ __global__ __launch_bounds__(512, 1) void transition_pipe_kernel(TransitionArgs<
       for (int cb = 0; cb < NCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int hc = 0; hc < NCHUNK; ++hc, ++q) {
-      // this wave's loads of chunk q landed (the next chunk may be in flight;
-      // at a tile's first chunk the previous tile's stores are drained too)
-      if (hc > 0 && q + 1 < Q) {
-        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+      // This wave's loads of chunk q have landed: the loads of a tile's
+      // chunks 0 and 1 (issued during the previous tile's last two chunks, or
+      // before the first tile) were awaited at the tile boundary; from
+      // hc == 2 on, only the loads of chunk q + 1 (kTpOps of them) were
+      // issued after chunk q's.
+      if (hc < 2) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      } else if (q + 1 < Q) {
+        asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
       } else {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       }
+      static_assert(kTpOps == 6, "the vmcnt above counts one chunk's loads");
       barrier_nofence();
       if (q + 2 < Q) issue(q + 2);
       const bf16* wa = ws[q % kTpStages];
       const bf16* wb = wa + 4096;
       const bf16* wo = wa + 8192;
-      Frag<bf16> fa[2][kC], fb[2][kC];
+      // GEMM1 per 16 hidden units (hb): gate and value fragments of hb, both
+      // row blocks; silu(a) * b lands in slots 4hb..4hb+3 of each row block's
+      // hidden fragment
+      Frag<bf16> hf[2];
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb)
+      for (int hb = 0; hb < 2; ++hb) {
+        Frag<bf16> fa[kC], fb[kC];
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
           const int off = sa_off + hb * 16 * C + ((4 * t + g) ^ r16) * 8;
-          fa[hb][t].load(wa + off);
-          fb[hb][t].load(wb + off);
+          fa[t].load(wa + off);
+          fb[t].load(wb + off);
         }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+          for (int t = 0; t < kC; ++t) {
+            mma(sa, fa[t], xf[rb][t]);
+            mma(sb, fb[t], xf[rb][t]);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hf[rb].set(4 * hb + e, siluf_(sa[e]) * sb[e]);
+        }
+      }
       Frag<bf16> fo[NCB];  // W_o[c][h0 + slot]: hidden 4g..4g+3 and 16+4g..16+4g+3
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         const bf16* row = wo + (cb * 16 + r16) * kTrHid + 4 * (g & 1);
-        float v[8];
-        load4(row + (((g >> 1)) ^ so_sw) * 8, v);
-        load4(row + ((2 + (g >> 1)) ^ so_sw) * 8, v + 4);
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + (((g >> 1)) ^ so_sw) * 8);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + ((2 + (g >> 1)) ^ so_sw) * 8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) fo[cb].set(e, v[e]);
+        for (int e = 0; e < 4; ++e) {
+          fo[cb].v[e] = lo[e];
+          fo[cb].v[4 + e] = hi[e];
+        }
       }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) mma(acc[rb][cb], fo[cb], hf[rb]);
+    }
+    // tile boundary: the next tile's rows and this tile's residual rows are
+    // loaded together (this wave's pending chunk loads are older, so they
+    // complete first), then the outputs are stored.  With float32 rows the
+    // registers do not hold both sets at once: the next rows are loaded after
+    // the stores.
+    constexpr bool kEarlyRows = sizeof(ZT) == 2;
+    Quad<ZT> res[2][NCB];
+    if (a.add) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        Frag<bf16> hf;
+        const int64_t row = min(row_of(tile, rb), a.rows - 1);
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
-#pragma unroll
-          for (int t = 0; t < kC; ++t) {
-            mma(sa, fa[hb][t], xf[rb][t]);
-            mma(sb, fb[hb][t], xf[rb][t]);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
-        }
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) mma(acc[rb][cb], fo[cb], hf);
+        for (int cb = 0; cb < NCB; ++cb) res[rb][cb].load(a.x + row * C + cb * 16 + 4 * g);
       }
     }
+    const int64_t next = tile + gridDim.x;
+    if (kEarlyRows && next < ntiles) load_rows(next);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // epilogue: lane holds row (2w+rb)*16 + r16, channels cb*16 + 4g + e
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int64_t row = r0 + (2 * w + rb) * 16 + r16;
+      const int64_t row = row_of(tile, rb);
       const bool valid = row < a.rows;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const int c0 = cb * 16 + 4 * g;
-        float base[4] = {0.f, 0.f, 0.f, 0.f};
-        if (valid && a.add) load4(a.x + row * C + c0, base);
+        if (a.add)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[rb][cb][e] += base[e];
-        if (valid) store4(a.out + row * C + c0, acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2],
-                          acc[rb][cb][3]);
+          for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[rb][cb].get(e);
+        if (valid)
+          store4(a.out + row * C + cb * 16 + 4 * g, acc[rb][cb][0], acc[rb][cb][1],
+                 acc[rb][cb][2], acc[rb][cb][3]);
       }
       if (a.pb_out)
         pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, valid, lnp + 2 * C, lnp + 3 * C, pbw);
     }
+    if (!kEarlyRows && next < ntiles) load_rows(next);
   }
 }
 
@@ -404,8 +519,8 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
   LaunchScope ls(ODDE_K_TRANSITION, st);
   if (a->c == 128 && a->n_factor == 4) {
     const int64_t ntiles = (p.rows + kTpRows - 1) / kTpRows;
-    const int grid = (int)std::min<int64_t>(ntiles, 256);
-    hipLaunchKernelGGL((transition_pipe_kernel<ZT>), dim3(grid), dim3(512), 0, st, p, ntiles);
+    const int grid = (int)std::min<int64_t>(ntiles, 2 * 256);
+    hipLaunchKernelGGL((transition_pipe_kernel<ZT>), dim3(grid), dim3(256), 0, st, p, ntiles);
   }
   else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
   else if (a->c == 256 && a->n_factor == 4) launch_tr<ZT, CT, 8, 4>(p, st);
