@@ -65,7 +65,7 @@ def kernel_bytes(n, c_z=128, h=4, ch=128, z_bytes=4, ct_bytes=2):
     hd = h * 32
     zrw = n * n * c_z * z_bytes
     return {
-        "triatt_proj": zrw + 4 * n * jp * hd * ct_bytes + h * jp * jp * ct_bytes + n * jp * 4,
+        "triatt_proj": zrw + 4 * n * jp * hd * ct_bytes + h * jp * jp * 4 + n * jp * 4,
         "triatt_out": n * jp * hd * ct_bytes + 2 * zrw,
         "trimul_proj": zrw + 2 * ch * np_ * np_ * ct_bytes,
         "trimul_out": ch * np_ * np_ * ct_bytes + 2 * zrw,
@@ -197,6 +197,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-layer-norm", action="store_true",
                     help="skip the standalone fast-LayerNorm measurement")
+    ap.add_argument("--preset", choices=["trunk", "opendde_v1"], default="trunk",
+                    help="trunk: c_z 128, 4 triangle heads, hidden 128 (the benchmark "
+                         "configuration); opendde_v1: the shipped model's pair width, c_z 384 "
+                         "with hidden_scale_up (12 heads, hidden 384)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "
                          "size, then one trunk step over a single block; prints nothing else")
@@ -208,10 +212,12 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
-    cfg = wl.PairConfig("trunk", args.n, n_blocks=args.blocks, n_pad=args.n * 5 // 100,
-                        random_pad=True, seed=3)
+    v1 = args.preset == "opendde_v1"
+    c_z, heads, ch = (384, 12, 384) if v1 else (128, 4, 128)
+    cfg = wl.PairConfig("trunk", args.n, c_z=c_z, n_blocks=args.blocks,
+                        n_pad=args.n * 5 // 100, random_pad=True, seed=3)
     z0, s0, mask, gen = wl.make_inputs(cfg)
-    stack = PairformerStack(n_blocks=args.blocks, c_z=128, c_s=384)
+    stack = PairformerStack(n_blocks=args.blocks, c_z=c_z, c_s=384, hidden_scale_up=v1)
     wl.init_module_(stack, gen)
     stack = stack.to(dev).eval()
     z0, s0, mask = z0.to(dev), s0.to(dev), mask.to(dev)
@@ -246,12 +252,12 @@ def main():
     _lib.timing_enable(False)
 
     n = args.n
-    f = flops(n)
+    f = flops(n, c_z=c_z, h=heads, ch=ch)
     ms_step = dt * 1e3 / args.steps
     trunk_flops = f["block"] * args.blocks
     value = trunk_flops / (ms_step * 1e-3) / 1e12
 
-    kb = kernel_bytes(n)
+    kb = kernel_bytes(n, c_z=c_z, h=heads, ch=ch)
     kernels = {}
     for kid, name in _lib.KERNEL_NAMES.items():
         tot, cnt = _lib.timing_query(kid)
@@ -271,7 +277,7 @@ def main():
         kernels[name] = ent
     dom = max(kernels, key=lambda k: kernels[k]["total_ms_per_step"])
     d = kernels[dom]
-    traffic = load_traffic(n).get(dom)
+    traffic = None if v1 else load_traffic(n).get(dom)
     if "tflops" in d:
         achieved = d["tflops"]
         roof = {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
@@ -297,9 +303,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"pairformer_trunk_{args.blocks}x_n{n}", "n_tokens": n,
-                   "n_blocks": args.blocks, "c_z": 128, "c_s": 384, "tri_heads": 4,
-                   "head_dim": 32, "c_hidden_mul": 128, "pad_tokens": n * 5 // 100,
+        "config": {"workload": f"pairformer_{'opendde_v1_' if v1 else ''}trunk_"
+                               f"{args.blocks}x_n{n}", "n_tokens": n,
+                   "n_blocks": args.blocks, "c_z": c_z, "c_s": 384, "tri_heads": heads,
+                   "head_dim": 32, "c_hidden_mul": ch, "pad_tokens": n * 5 // 100,
                    "residual_dtype": "fp32", "compute_dtype": "bf16", "seed": 3},
         "block_ms": round(ms_step / args.blocks, 3),
         "tri_attn_core_tflops": kernels.get("triatt_core", {}).get("tflops"),
@@ -315,7 +322,7 @@ def main():
         "cpu_baseline": None,
         "layer_norm": None if args.no_layer_norm else layer_norm_measure(n, dev),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not v1:
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_n, chunk=128)
     print(json.dumps(out), flush=True)
 

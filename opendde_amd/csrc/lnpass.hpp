@@ -1,0 +1,147 @@
+// LayerNorm passes that feed the wide-channel GEMM kernels (gemm.hpp) with
+// normalised bf16 rows: the A operand of an NT GEMM is then a plain
+// row-major [rows][C] matrix that the mainloop streams into LDS by direct
+// loads.  Statistics are f32, two-pass, over the C channels of a row.
+#pragma once
+
+#include "common.hpp"
+
+namespace odde {
+
+// out[m][:] = LN(z[x][y][:]) for m = x * R + y, x < X, y < R, where
+// z[x][y][c] = z + x * s0 + y * s1 + c; rows with x >= n or y >= n (padding)
+// are written as zeros.  16 lanes per row, C / 16 contiguous channels per
+// lane (16-byte loads and stores); grid-stride over rows.
+template <typename ZT, int C>
+__global__ __launch_bounds__(256) void ln_view_bf16_kernel(const ZT* __restrict__ z, int64_t s0,
+                                                           int64_t s1, int n, int X, int R,
+                                                           const float* __restrict__ ln_w,
+                                                           const float* __restrict__ ln_b,
+                                                           float eps, bf16* __restrict__ out) {
+  constexpr int E = C / 16;                      // channels per lane
+  constexpr int LV = E * (int)sizeof(ZT) / 16;   // 16-byte loads per lane
+  constexpr int SV = E * 2 / 16;                 // 16-byte stores per lane
+  static_assert(E % 8 == 0, "C a multiple of 128");
+  const int sub = threadIdx.x & 15;
+  const int64_t rows = (int64_t)X * R;
+  const int64_t r0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 4;
+  const int64_t nr = (int64_t(gridDim.x) * 256) >> 4;
+  float lw[E], lb[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    lw[e] = ln_w[sub * E + e];
+    lb[e] = ln_b[sub * E + e];
+  }
+  for (int64_t r = r0; r < rows; r += nr) {  // uniform over the 16 lanes of a row
+    const int x = (int)(r / R), y = (int)(r % R);
+    const bool valid = x < n && y < n;
+    float v[E];
+    if (valid) {
+      const ZT* src = z + (int64_t)x * s0 + (int64_t)y * s1 + sub * E;
+#pragma unroll
+      for (int k = 0; k < LV; ++k) {
+        const f32x4 c = reinterpret_cast<const f32x4*>(src)[k];
+        if constexpr (sizeof(ZT) == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * k + e] = c[e];
+        } else {
+          const bf16x8 h = __builtin_bit_cast(bf16x8, c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[8 * k + e] = (float)h[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = 0.f;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += v[e];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o, 64);
+    const float mean = s * (1.0f / C);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float d = v[e] - mean;
+      q += d * d;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o, 64);
+    const float rstd = rsqrtf(q * (1.0f / C) + eps);
+    bf16* dst = out + r * C + sub * E;
+#pragma unroll
+    for (int k = 0; k < SV; ++k) {
+      bf16x8 h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 8 * k + e;
+        h[e] = (bf16)(valid ? (v[c] - mean) * rstd * lw[c] + lb[c] : 0.f);
+      }
+      reinterpret_cast<bf16x8*>(dst)[k] = h;
+    }
+  }
+}
+
+// out[x * np + y][:] = LN(P[:][x][y]) for the channel-major P[CH][np][np]
+// (bf16): a workgroup transposes the 64-column block P[:, x, y0..y0+63]
+// through LDS, then 4 threads per column normalise its CH channels.  Grid
+// (np / 64, np).  Columns with x >= n or y >= n are written as zeros.
+template <int CH>
+__global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __restrict__ P, int np,
+                                                                int n,
+                                                                const float* __restrict__ ln_w,
+                                                                const float* __restrict__ ln_b,
+                                                                float eps, bf16* __restrict__ out) {
+  constexpr int LD = CH + 8;     // LDS row stride (elements) of the transposed tile
+  constexpr int Q = CH / 4;      // channels per thread in the LayerNorm pass
+  __shared__ __attribute__((aligned(16))) bf16 t[64 * LD];
+  const int x = blockIdx.y, y0 = blockIdx.x * 64;
+  const bf16* src = P + (size_t)x * np + y0;
+  for (int ci = threadIdx.x; ci < CH * 8; ci += 256) {  // 8 16-byte chunks per channel row
+    const int c = ci >> 3, yy = (ci & 7) * 8;
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)c * np * np + yy);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[(yy + e) * LD + c] = v[e];
+  }
+  __syncthreads();
+  const int yl = threadIdx.x >> 2, part = threadIdx.x & 3;
+  const int y = y0 + yl;
+  const bool valid = x < n && y < n;
+  const bf16* row = t + yl * LD + part * Q;
+  float v[Q];
+#pragma unroll
+  for (int k = 0; k < Q / 8; ++k) {
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(row + 8 * k);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[8 * k + e] = (float)h[e];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < Q; ++e) s += v[e];
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  const float mean = s * (1.0f / CH);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < Q; ++e) {
+    const float d = v[e] - mean;
+    q += d * d;
+  }
+  q += __shfl_xor(q, 1, 64);
+  q += __shfl_xor(q, 2, 64);
+  const float rstd = rsqrtf(q * (1.0f / CH) + eps);
+  bf16* dst = out + ((size_t)x * np + y) * CH + part * Q;
+#pragma unroll
+  for (int k = 0; k < Q / 8; ++k) {
+    bf16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = part * Q + 8 * k + e;
+      h[e] = (bf16)(valid ? (v[8 * k + e] - mean) * rstd * ln_w[c] + ln_b[c] : 0.f);
+    }
+    reinterpret_cast<bf16x8*>(dst)[k] = h;
+  }
+}
+
+}  // namespace odde

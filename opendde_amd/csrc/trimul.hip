@@ -19,6 +19,8 @@
 // Workspace (CT = compute type, Np = N rounded up to 128):
 //   A, B, P : [Ch][Np][Np]
 #include "common.hpp"
+#include "gemm.hpp"
+#include "lnpass.hpp"
 #include "rowtile.hpp"
 #include "runtime.hpp"
 
@@ -181,24 +183,11 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(ContractArgs<CT> a
 }
 
 // Large-tile form (bf16, Np a multiple of 256): TX x TY tiles per workgroup
-// of 8 waves (WX along x, 8/WX along y).  K advances in stages of 32 staged
-// by direct global -> LDS loads into NS buffers: stage s+NS-1 streams in
-// while stage s is multiplied.  One fence-free barrier per stage suffices:
-// each wave first waits for its own loads of stage s (vmcnt) and its own LDS
-// reads of stage s-1 (lgkmcnt), and the buffer refilled at stage s was last
-// read at stage s-1.  LDS rows are 64 bytes (4 chunks of 16); slot t of row r
-// holds chunk t ^ ((r >> 1) & 3), which spreads the K32 fragment reads of 16
-// consecutive rows over all banks.
-constexpr int kCk = 32;  // k per stage
-
-__device__ __forceinline__ int ct_swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
-
+// of 8 waves, the shared NT mainloop (gemm.hpp) over k = 0..Np.
 template <int TX, int TY, int WX, int NS>
 __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<bf16> a) {
-  constexpr int WY = 8 / WX, MX = TX / WX / 16, MY = TY / WY / 16;  // fragments per wave
-  constexpr int OPS_A = TX / 16 / 8, OPS_B = TY / 16 / 8;          // 1 KiB loads per wave
-  constexpr int OPS = OPS_A + OPS_B;
-  __shared__ __attribute__((aligned(16))) bf16 sm[NS][(TX + TY) * kCk];  // [stage][A rows | B rows][k]
+  using S = GemmShape<TX, TY, WX>;
+  __shared__ __attribute__((aligned(16))) bf16 sm[NS * S::STAGE_ELEMS];
   const int TXn = a.np / TX, TYn = a.np / TY;
   const int tiles = TXn * TYn;
   int bid = blockIdx.x, c, tile;
@@ -211,84 +200,23 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
     tile = bid % tiles;
   }
   const int x0 = (tile / TYn) * TX, y0 = (tile % TYn) * TY;
-  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
-  const int wx = w % WX, wy = w / WX;
   const size_t plane = (size_t)a.np * a.np;
+  f32x4 acc[S::MX][S::MY];
   const bf16* Ab = a.A + c * plane + (size_t)x0 * a.np;
   const bf16* Bb = a.B + c * plane + (size_t)y0 * a.np;
-
-  // Stage loads: 1 KiB (16 rows of 64 bytes) per wave instruction; wave w
-  // loads A blocks w*OPS_A.. and B blocks w*OPS_B..; source offsets are fixed
-  // per lane, only k advances.
-  int soff[OPS];
-#pragma unroll
-  for (int op = 0; op < OPS; ++op) {
-    const bool isb = op >= OPS_A;
-    const int blk = isb ? w * OPS_B + (op - OPS_A) : w * OPS_A + op;
-    const int row = blk * 16 + (l >> 2);
-    soff[op] = row * a.np + ct_swz(row, l & 3) * 8;
-  }
-  auto issue = [&](int st) {
-    const int k0 = st * kCk;
-    bf16* base = sm[st % NS];
-#pragma unroll
-    for (int op = 0; op < OPS; ++op) {
-      const bool isb = op >= OPS_A;
-      const int blk = isb ? w * OPS_B + (op - OPS_A) : w * OPS_A + op;
-      const bf16* src = (isb ? Bb : Ab) + soff[op] + k0;
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)src,
-          (__attribute__((address_space(3))) void*)(base + (isb ? TX * kCk : 0) + blk * 512),
-          16, 0, 0);
-    }
-  };
-
-  f32x4 acc[MX][MY];
-#pragma unroll
-  for (int i = 0; i < MX; ++i)
-#pragma unroll
-    for (int j = 0; j < MY; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // fragment offsets: the swizzle depends on r16 only (rows step by 16)
-  const int fsw = ct_swz(r16, g) * 8;
-  const int aoff = (wx * (TX / WX) + r16) * kCk + fsw;
-  const int boff = TX * kCk + (wy * (TY / WY) + r16) * kCk + fsw;
-
-  const int S = a.np / kCk;  // >= 8
-#pragma unroll
-  for (int st = 0; st < NS - 1; ++st) issue(st);
-  for (int st = 0; st < S; ++st) {
-    // this wave's loads of stage st landed (up to NS-2 later stages in flight)
-    const int ahead = min(S - 1 - st, NS - 2);
-    if (ahead >= 2) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * OPS) : "memory");
-    } else if (ahead == 1) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // own reads of stage st-1 done
-    barrier_nofence();
-    if (st + NS - 1 < S) issue(st + NS - 1);
-    const bf16* base = sm[st % NS];
-    Frag<bf16> af[MX], bfr[MY];
-#pragma unroll
-    for (int j = 0; j < MY; ++j) bfr[j].load(base + boff + j * 16 * kCk);
-#pragma unroll
-    for (int i = 0; i < MX; ++i) af[i].load(base + aoff + i * 16 * kCk);
-#pragma unroll
-    for (int i = 0; i < MX; ++i)
-#pragma unroll
-      for (int j = 0; j < MY; ++j) mma(acc[i][j], bfr[j], af[i]);
-  }
+  gemm_nt_mainloop<TX, TY, WX, NS, true>([&](int r) { return Ab + (size_t)r * a.np; },
+                                         [&](int r) { return Bb + (size_t)r * a.np; }, a.np, sm,
+                                         acc);
   // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16), rows y = y0 + wy*TY/WY + 16j + 4g + r
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % WX, wy = w / WX;
   bf16* Pb = a.P + c * plane;
 #pragma unroll
-  for (int i = 0; i < MX; ++i)
+  for (int i = 0; i < S::MX; ++i)
 #pragma unroll
-    for (int j = 0; j < MY; ++j) {
+    for (int j = 0; j < S::MY; ++j) {
       const int xx = x0 + wx * (TX / WX) + i * 16 + r16;
-      const int yy = y0 + wy * (TY / WY) + j * 16 + 4 * g;
+      const int yy = y0 + wy * (TY / S::WY) + j * 16 + 4 * g;
       store4(Pb + (size_t)xx * a.np + yy, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
     }
 }
@@ -625,6 +553,135 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   }
 }
 
+// ---------------------------------------------------------------------------
+// 4. wide channels (bf16; C or Ch of 256 and more): LayerNorm passes
+//    (lnpass.hpp) into bf16 rows, then NT GEMMs on the shared mainloop
+//    (gemm.hpp) with the gating / residual epilogues.  Rows are the pairs of
+//    the padded grid, m = x * Np + y (Np^2 rows, a multiple of 2048).
+// ---------------------------------------------------------------------------
+constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3;
+using WideShape = GemmShape<kWTX, kWTY, kWWX>;
+
+// Linear workgroup id -> (row tile, column tile) such that all column tiles
+// of a row tile run on one XCD (workgroups are dealt to the 8 XCDs
+// round-robin), so the tile's A rows are fetched into one L2.  The row tile
+// count must be a multiple of 8.
+__device__ __forceinline__ void wide_tile_map(int L, int ncol, int& rt, int& ct) {
+  const int xcd = L & 7, s = L >> 3;
+  rt = xcd + 8 * (s / ncol);
+  ct = s % ncol;
+}
+
+struct TrimulWideProjArgs {
+  const bf16* zn;   // [Np^2][C] LN_in rows in the projection's view order
+  const bf16* wp;   // [2*Ch][C] (a_p rows, then b_p rows)
+  const bf16* wg;   // [2*Ch][C]
+  const float* mask;
+  int64_t m_s0, m_s1;
+  bf16* A;          // [Ch][Np][Np]
+  bf16* B;
+  int n, np, c, ch;
+};
+
+// Output rows of the GEMM are the 4*Ch projections interleaved in 16-row
+// blocks [a_p | a_g | a_p | a_g ... | b_p | b_g ...] (read in place through
+// the row functor, no copy), so a wave's fragments j (value) and j + 1
+// (gate) hold the same 16 channels.  Accumulator: one channel, four
+// consecutive pairs per lane -> 8-byte stores into the channel-major planes.
+__global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArgs a, int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kWNS * WideShape::STAGE_ELEMS];
+  int rt, ct;
+  wide_tile_map(blockIdx.x, ncol, rt, ct);
+  const int64_t x0 = (int64_t)rt * kWTX;
+  const int y0 = ct * kWTY;
+  const int C = a.c, CH = a.ch, np = a.np;
+  f32x4 acc[WideShape::MX][WideShape::MY];
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false>(
+      [&](int r) { return a.zn + (x0 + r) * C; },
+      [&](int r) {
+        const int R = y0 + r, side = R / (2 * CH), within = R % (2 * CH), t = within & 31;
+        const int chan = side * CH + (within >> 5) * 16 + (t & 15);
+        return (t < 16 ? a.wp : a.wg) + (size_t)chan * C;
+      },
+      C, sm, acc);
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kWWX, wy = w / kWWX;
+#pragma unroll
+  for (int i = 0; i < WideShape::MX; ++i) {
+    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3, one row x
+    const int x = (int)(m / np), y = (int)(m % np);
+    float mk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      mk[e] = (x < a.n && y + e < a.n)
+                  ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)(y + e) * a.m_s1] : 1.0f)
+                  : 0.f;
+#pragma unroll
+    for (int j = 0; j < WideShape::MY; j += 2) {
+      const int R = y0 + wy * (kWTY / WideShape::WY) + 16 * j;  // first row of the value block
+      const int side = R / (2 * CH), chan = ((R % (2 * CH)) >> 5) * 16 + r16;
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)(mk[e] * sigmoidf_(acc[i][j + 1][e]) * acc[i][j][e]);
+      *reinterpret_cast<bf16x4*>((side ? a.B : a.A) + ((size_t)chan * np + x) * np + y) = v;
+    }
+  }
+}
+
+template <typename ZT>
+struct TrimulWideOutArgs {
+  const bf16* pn;   // [Np^2][Ch] LN_out(P) rows, natural order
+  const bf16* zn;   // [Np^2][C] LN_in(z) rows in the projection's view order
+  const bf16* wz;   // [C][Ch]
+  const bf16* wg;   // [C][C]
+  const ZT* z;
+  int64_t z_s0, z_s1;
+  ZT* out;
+  int64_t o_s0, o_s1;
+  int n, np, c, ch, add, zn_transposed;
+};
+
+// out[x][y][c] = (add ? z : 0) + sigmoid(LN_in(z) W_g^T) * (LN_out(P) W_z^T):
+// two NT GEMMs over the same tile (K = Ch, then K = C), then the epilogue.
+// Accumulator: one pair, four consecutive channels per lane.
+template <typename ZT>
+__global__ __launch_bounds__(512) void trimul_out_wide_kernel(TrimulWideOutArgs<ZT> a, int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kWNS * WideShape::STAGE_ELEMS];
+  int rt, ct;
+  wide_tile_map(blockIdx.x, ncol, rt, ct);
+  const int64_t x0 = (int64_t)rt * kWTX;
+  const int y0 = ct * kWTY;
+  const int C = a.c, CH = a.ch, np = a.np;
+  f32x4 accy[WideShape::MX][WideShape::MY], accg[WideShape::MX][WideShape::MY];
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+      [&](int r) { return a.pn + (x0 + r) * CH; },
+      [&](int r) { return a.wz + (size_t)(y0 + r) * CH; }, CH, sm, accy);
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+      [&](int r) {
+        const int64_t m = x0 + r;  // the incoming form's z rows were normalised transposed
+        const int64_t zr = a.zn_transposed ? (m % np) * np + m / np : m;
+        return a.zn + zr * C;
+      },
+      [&](int r) { return a.wg + (size_t)(y0 + r) * C; }, C, sm, accg);
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kWWX, wy = w / kWWX;
+#pragma unroll
+  for (int i = 0; i < WideShape::MX; ++i) {
+    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + r16;
+    const int x = (int)(m / np), y = (int)(m % np);
+    if (x >= a.n || y >= a.n) continue;
+#pragma unroll
+    for (int j = 0; j < WideShape::MY; ++j) {
+      const int c0 = y0 + wy * (kWTY / WideShape::WY) + 16 * j + 4 * g;
+      float r[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.add) load4(a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 + c0, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += sigmoidf_(accg[i][j][e]) * accy[i][j][e];
+      store4(a.out + (int64_t)x * a.o_s0 + (int64_t)y * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+    }
+  }
+}
+
 }  // namespace odde
 
 // ===========================================================================
@@ -634,18 +691,109 @@ using namespace odde;
 
 namespace {
 
-struct TrimulWs { void* A; void* B; void* P; uint64_t bytes; };
+// Wide-channel path: bf16 compute, C in {128, 256, 384} and C or Ch of 256
+// and more (the weight slices of the register-resident kernels no longer fit).
+bool trimul_wide(int c, int ch, int dt) {
+  return dt == ODDE_BF16 && (c == 128 || c == 256 || c == 384) && (c >= 256 || ch >= 256);
+}
 
-TrimulWs carve_trimul(void* base, uint64_t size, int n, int ch, int dt) {
+struct TrimulWs { void* A; void* B; void* P; void* zn; uint64_t bytes; };
+
+TrimulWs carve_trimul(void* base, uint64_t size, int n, int c, int ch, int dt) {
   const int np = round_up(n, 128);
   const uint64_t plane = (uint64_t)ch * np * np * dtype_size(dt);
-  Carver c(base, size);
+  Carver cv(base, size);
   TrimulWs w;
-  w.A = c.take<char>(plane);
-  w.B = c.take<char>(plane);
-  w.P = c.take<char>(plane);
-  w.bytes = (c.used + 255) & ~uint64_t(255);
+  w.A = cv.take<char>(plane);
+  w.B = cv.take<char>(plane);
+  w.P = cv.take<char>(plane);
+  // the wide path's LN_in(z) rows (its LN_out(P) rows reuse A after the
+  // contraction)
+  w.zn = trimul_wide(c, ch, dt) ? cv.take<char>((uint64_t)np * np * c * 2) : nullptr;
+  w.bytes = (cv.used + 255) & ~uint64_t(255);
   return w;
+}
+
+template <typename ZT>
+int run_trimul_wide(const odde_trimul_args* a, const TrimulWs& ws, hipStream_t st) {
+  const int n = a->n, C = a->c, ch = a->c_hidden, np = round_up(n, 128);
+  const bool outgoing = a->outgoing != 0;
+  const int64_t vs0 = outgoing ? a->z_s0 : a->z_s1, vs1 = outgoing ? a->z_s1 : a->z_s0;
+  const int64_t rows = (int64_t)np * np;             // a multiple of 16384
+  const int row_tiles = (int)(rows / kWTX);          // a multiple of 8
+  bf16* zn = static_cast<bf16*>(ws.zn);
+  {
+    LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
+    const int lg = (int)std::min<int64_t>(rows / 16, 4096);
+    const ZT* z = static_cast<const ZT*>(a->z);
+    if (C == 128)
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 128>), dim3(lg), dim3(256), 0, st, z, vs0, vs1, n,
+                         np, np, a->norm_in_weight, a->norm_in_bias, a->eps, zn);
+    else if (C == 256)
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 256>), dim3(lg), dim3(256), 0, st, z, vs0, vs1, n,
+                         np, np, a->norm_in_weight, a->norm_in_bias, a->eps, zn);
+    else
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 384>), dim3(lg), dim3(256), 0, st, z, vs0, vs1, n,
+                         np, np, a->norm_in_weight, a->norm_in_bias, a->eps, zn);
+    TrimulWideProjArgs p;
+    p.zn = zn;
+    p.wp = static_cast<const bf16*>(a->p_in_weight);
+    p.wg = static_cast<const bf16*>(a->g_in_weight);
+    p.mask = a->mask;
+    p.m_s0 = outgoing ? a->mask_s0 : a->mask_s1;
+    p.m_s1 = outgoing ? a->mask_s1 : a->mask_s0;
+    p.A = static_cast<bf16*>(ws.A);
+    p.B = static_cast<bf16*>(ws.B);
+    p.n = n; p.np = np; p.c = C; p.ch = ch;
+    const int ncol = 4 * ch / kWTY;
+    hipLaunchKernelGGL(trimul_proj_wide_kernel, dim3(row_tiles * ncol), dim3(512), 0, st, p, ncol);
+    int rc = check_launch("trimul_proj (wide)");
+    if (rc) return rc;
+  }
+  ContractArgs<bf16> k;
+  k.A = static_cast<bf16*>(ws.A); k.B = static_cast<bf16*>(ws.B); k.P = static_cast<bf16*>(ws.P);
+  k.np = np; k.ch = ch;
+  {
+    LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
+    if (np % 256 == 0) {
+      const int tiles = (np / 256) * (np / 128);
+      hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3>), dim3(tiles * ch), dim3(512),
+                         0, st, k);
+    } else {
+      const int tiles = (np / 128) * (np / 128);
+      hipLaunchKernelGGL((trimul_contract_kernel<bf16>), dim3(tiles * ch), dim3(256), 0, st, k);
+    }
+    int rc = check_launch("trimul_contract");
+    if (rc) return rc;
+  }
+  {
+    LaunchScope ls(ODDE_K_TRIMUL_OUT, st);
+    bf16* pn = static_cast<bf16*>(ws.A);  // A is dead after the contraction
+    const dim3 tg(np / 64, np);
+    switch (ch) {
+      case 64: hipLaunchKernelGGL((ln_transpose_bf16_kernel<64>), tg, dim3(256), 0, st, k.P, np, n,
+                                  a->norm_out_weight, a->norm_out_bias, a->eps, pn); break;
+      case 128: hipLaunchKernelGGL((ln_transpose_bf16_kernel<128>), tg, dim3(256), 0, st, k.P, np,
+                                   n, a->norm_out_weight, a->norm_out_bias, a->eps, pn); break;
+      case 256: hipLaunchKernelGGL((ln_transpose_bf16_kernel<256>), tg, dim3(256), 0, st, k.P, np,
+                                   n, a->norm_out_weight, a->norm_out_bias, a->eps, pn); break;
+      case 384: hipLaunchKernelGGL((ln_transpose_bf16_kernel<384>), tg, dim3(256), 0, st, k.P, np,
+                                   n, a->norm_out_weight, a->norm_out_bias, a->eps, pn); break;
+      default: return set_error(ODDE_EUNSUPPORTED, "trimul: unsupported c_hidden");
+    }
+    TrimulWideOutArgs<ZT> o;
+    o.pn = pn; o.zn = zn;
+    o.wz = static_cast<const bf16*>(a->p_out_weight);
+    o.wg = static_cast<const bf16*>(a->g_out_weight);
+    o.z = static_cast<const ZT*>(a->z); o.z_s0 = a->z_s0; o.z_s1 = a->z_s1;
+    o.out = static_cast<ZT*>(a->out); o.o_s0 = a->out_s0; o.o_s1 = a->out_s1;
+    o.n = n; o.np = np; o.c = C; o.ch = ch; o.add = a->add_residual;
+    o.zn_transposed = outgoing ? 0 : 1;
+    const int ncol = C / kWTY;
+    hipLaunchKernelGGL((trimul_out_wide_kernel<ZT>), dim3(row_tiles * ncol), dim3(512), 0, st, o,
+                       ncol);
+    return check_launch("trimul_out (wide)");
+  }
 }
 
 int kdim(int c) {
@@ -737,7 +885,10 @@ template <typename ZT, typename CT>
 int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   const int n = a->n, C = a->c, ch = a->c_hidden;
   const int np = round_up(n, 128);
-  TrimulWs ws = carve_trimul(a->workspace, a->workspace_bytes, n, ch, a->compute_dtype);
+  TrimulWs ws = carve_trimul(a->workspace, a->workspace_bytes, n, C, ch, a->compute_dtype);
+  if constexpr (sizeof(CT) == 2) {
+    if (trimul_wide(C, ch, a->compute_dtype)) return run_trimul_wide<ZT>(a, ws, st);
+  }
   const bool out = a->outgoing != 0;
 
   TrimulProjArgs<ZT, CT> p;
@@ -819,7 +970,7 @@ int odde_trimul_workspace_bytes(const odde_trimul_args* a, uint64_t* bytes) {
   int rc = check_trimul(a);
   if (rc) return rc;
   if (!bytes) return set_error(ODDE_EINVAL, "trimul: null bytes");
-  *bytes = carve_trimul(nullptr, 0, a->n, a->c_hidden, a->compute_dtype).bytes;
+  *bytes = carve_trimul(nullptr, 0, a->n, a->c, a->c_hidden, a->compute_dtype).bytes;
   return ODDE_OK;
 }
 
@@ -830,7 +981,7 @@ int odde_trimul_fwd(const odde_trimul_args* a, void* stream) {
       !a->norm_out_bias || !a->p_in_weight || !a->g_in_weight || !a->p_out_weight ||
       !a->g_out_weight)
     return set_error(ODDE_EINVAL, "trimul: null tensor pointer");
-  const uint64_t need = carve_trimul(nullptr, 0, a->n, a->c_hidden, a->compute_dtype).bytes;
+  const uint64_t need = carve_trimul(nullptr, 0, a->n, a->c, a->c_hidden, a->compute_dtype).bytes;
   if (!a->workspace || a->workspace_bytes < need ||
       (reinterpret_cast<uintptr_t>(a->workspace) & 255))
     return set_error(ODDE_EWORKSPACE, "trimul: workspace missing, too small or not 256-byte aligned");

@@ -147,6 +147,31 @@ def test_triangle_multiplication_channel_shapes(c, ch):
     assert_fp32(got, exp, f"trimul c={c} ch={ch}")
 
 
+@pytest.mark.parametrize("c,ch", [(384, 384), (256, 256), (128, 256), (384, 64)])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("n", [40, 130])
+def test_triangle_multiplication_wide_bf16(c, ch, outgoing, n):
+    """Wide channels (C or Ch >= 256) take the LayerNorm-pass + NT GEMM path;
+    z in bf16, and z in fp32 under bf16 autocast with an in-place residual
+    add."""
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(c, ch), 700 + c + ch + n, STD * 0.5)
+    z = _z(n, c, c + 3 * ch + n)
+    mask = token_pair_mask(n, max(1, n // 10), seed=n + 1, random=True)
+    zb = z.to(torch.bfloat16)
+    exp = ref.triangle_multiplication(zb.float(), mask, params_of(mod), outgoing)
+    mod = mod.to(DEV)
+    got = mod(zb.to(DEV), mask.to(DEV), triangle_multiplicative="hip")
+    assert got.dtype == torch.bfloat16
+    assert_bf16(got, exp, f"trimul wide bf16 c={c} ch={ch} n={n} out={outgoing}")
+    exp32 = ref.triangle_multiplication(z, mask, params_of(mod), outgoing)
+    z2 = z.to(DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        got = mod.hip_apply(z2, mask.to(DEV), out=z2, add_residual=True)
+    assert got.data_ptr() == z2.data_ptr()
+    assert_bf16(z2 - z.to(DEV), exp32, f"trimul wide fp32-z c={c} ch={ch} n={n} out={outgoing}")
+
+
 def test_triangle_multiplication_in_place_add():
     n = 70
     mod = seeded(TriangleMultiplicationOutgoing(128, 128), 9, STD).to(DEV)
