@@ -45,6 +45,8 @@
 #include <stdlib.h>
 
 #include "common.hpp"
+#include "gemm.hpp"
+#include "lnpass.hpp"
 #include "rowtile.hpp"
 #include "runtime.hpp"
 
@@ -1158,6 +1160,204 @@ __global__ __launch_bounds__(256) void triatt_mflag_kernel(const float* mb, int*
   mflag[tid] = any;
 }
 
+// ---------------------------------------------------------------------------
+// 5. wide channels (bf16; C or H*32 of 256 and more): a LayerNorm pass into
+//    bf16 rows (lnpass.hpp), then NT GEMMs on the shared mainloop
+//    (gemm.hpp).  Rows are the pairs m = i * Jp + j, padded to a multiple of
+//    2048 (rows past n * Jp are never stored).
+// ---------------------------------------------------------------------------
+constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3;
+using WideShape = GemmShape<kWTX, kWTY, kWWX>;
+
+__device__ __forceinline__ void wide_tile_map(int L, int ncol, int& rt, int& ct) {
+  const int xcd = L & 7, s = L >> 3;  // all column tiles of a row tile on one XCD
+  rt = xcd + 8 * (s / ncol);
+  ct = s % ncol;
+}
+
+// Mask outputs (mb, mflag, keep) and the triangle bias of 64 pairs (i, j0..)
+// from the normalised rows, as in the register projection kernel: a
+// workgroup of 4 waves, 16 pairs per wave.
+template <typename ZT, int kC>
+__global__ __launch_bounds__(256) void triatt_bias_mask_wide_kernel(TriattProjArgs<ZT, bf16> a,
+                                                                    const bf16* zn) {
+  constexpr int C = kC * 32;
+  const int i = blockIdx.y;
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int H = a.heads, jp = a.jp;
+  const int j0 = blockIdx.x * 64 + w * 16;
+  const int jl = j0 + r16;
+  const bool valid = jl < a.n;
+  Frag<bf16> x[kC];
+  const bf16* row = zn + ((size_t)i * jp + jl) * C + 8 * g;
+#pragma unroll
+  for (int t = 0; t < kC; ++t) x[t].load(row + 32 * t);
+
+  __shared__ float keep_s[64];
+  __shared__ int wmasked[4];
+  float mv = -INFINITY, kp = 0.f;
+  if (valid) {
+    const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
+    mv = (m - 1.0f) * a.mask_inf;
+    kp = m == 1.0f ? 1.f : 0.f;
+  }
+  if (g == 0) {
+    a.mb[(size_t)i * jp + jl] = mv;
+    keep_s[w * 16 + r16] = kp;
+  }
+  const bool any_masked = __any(mv != 0.f);
+  if (l == 0) wmasked[w] = any_masked ? 1 : 0;
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const int b = threadIdx.x;  // 32-key block b of this 64-key tile = waves 2b, 2b+1
+    a.mflag[(size_t)i * (jp >> 5) + blockIdx.x * 2 + b] = wmasked[2 * b] | wmasked[2 * b + 1];
+  }
+  if (threadIdx.x < 64) {
+    const int t = threadIdx.x, kb = t >> 5, s = t & 31;
+    a.keep[((size_t)i * (jp >> 5) + blockIdx.x * 2 + kb) * 32 + s] =
+        (bf16)keep_s[kb * 32 + slot_key(s >> 3, s & 7)];
+  }
+  // triangle bias: channel h = r16 (< H), rows j0+4g .. +3 -> bias[h][i][..]
+  f32x4 ab = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    Frag<bf16> f;
+    load_w_frag(a.wb, C, 0, H, t, f);
+    mma(ab, x[t], f);
+  }
+  const float sc = kLog2e;
+  const int jb = j0 + 4 * g;
+  const float bm = group_max_fast(fmaxf(fmaxf(ab[0], ab[1]), fmaxf(ab[2], ab[3])) * sc);
+  if (r16 < H) {
+    store4(a.bias + ((size_t)r16 * jp + i) * jp + jb, ab[0] * sc, ab[1] * sc, ab[2] * sc,
+           ab[3] * sc);
+    if (g == 0) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
+  }
+}
+
+// q, k, v, gate as one NT GEMM of the normalised rows with the weight rows
+// [W_q | W_k | W_v | W_g] (H*32 each, a multiple of the 128-row column tile,
+// so a tile is one of the four).  q, k, gate: one pair and four consecutive
+// channels per lane (8-byte stores into [I][H][Jp][32]); v: one channel and
+// four consecutive pairs per lane (8-byte stores into the fragment-ordered
+// V layout), zeroed on masked keys of rows that keep a key.  k also yields
+// the per-(row, head) maximum key norm for the fast core's bound.
+template <typename ZT>
+__global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT, bf16> a,
+                                                               const bf16* zn, int C, int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kWNS * WideShape::STAGE_ELEMS];
+  int rt, ct;
+  wide_tile_map(blockIdx.x, ncol, rt, ct);
+  const int H = a.heads, HD = H * 32, jp = a.jp, n = a.n;
+  const int64_t x0 = (int64_t)rt * kWTX;
+  const int per = HD / kWTY, type = ct / per, o0 = (ct % per) * kWTY;
+  const bf16* W = type == 0 ? a.wq : type == 1 ? a.wk : type == 2 ? a.wv : a.wg;
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kWWX, wy = w / kWWX;
+  auto arow = [&](int r) { return zn + (x0 + r) * C; };
+  auto brow = [&](int r) { return W + (size_t)(o0 + r) * C; };
+  f32x4 acc[WideShape::MX][WideShape::MY];
+  if (type == 2) {  // v: channel-per-lane orientation
+    gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false>(arow, brow, C, sm, acc);
+#pragma unroll
+    for (int i = 0; i < WideShape::MX; ++i) {
+      const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3
+      const int row = (int)(m / jp), jj = (int)(m % jp);
+      if (row >= n) continue;
+      float vk[4] = {1.f, 1.f, 1.f, 1.f};
+      if (a.anykeep[row] != 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float mv = jj + e < n ? (a.mask ? a.mask[(int64_t)row * a.m_s0 +
+                                                         (int64_t)(jj + e) * a.m_s1]
+                                                : 1.0f)
+                                      : 0.f;
+          vk[e] = mv == 1.0f ? 1.f : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < WideShape::MY; ++j) {
+        const int o = o0 + wy * (kWTY / WideShape::WY) + 16 * j + r16;
+        store4(a.v + vperm_offset(row, o >> 5, H, jp, jj, o & 31), acc[i][j][0] * vk[0],
+               acc[i][j][1] * vk[1], acc[i][j][2] * vk[2], acc[i][j][3] * vk[3]);
+      }
+    }
+    return;
+  }
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(arow, brow, C, sm, acc);
+  // the wave's 64 pairs lie in one row (Jp and the offsets are multiples of 64)
+  const int64_t mw = x0 + wx * (kWTX / kWWX);
+  const int row = (int)(mw / jp);
+  if (row >= n) return;
+  const int ob = o0 + wy * (kWTY / WideShape::WY);  // the wave's 64 channels = heads ob/32, +1
+  float knm[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < WideShape::MX; ++i) {
+    const int jj = (int)((mw + 16 * i + r16) % jp);
+    float ss[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < WideShape::MY; ++j) {
+      const int o = ob + 16 * j + 4 * g;
+      const size_t off = (((size_t)row * H + (o >> 5)) * jp + jj) * 32 + (o & 31);
+      const f32x4 v = acc[i][j];
+      if (type == 0) {
+        const float sc = a.q_scale;
+        store4(a.q + off, v[0] * sc, v[1] * sc, v[2] * sc, v[3] * sc);
+      } else if (type == 1) {
+        store4(a.k + off, v[0], v[1], v[2], v[3]);
+        ss[j >> 1] += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      } else {
+        store4(a.gate + off, sigmoidf_(v[0]), sigmoidf_(v[1]), sigmoidf_(v[2]), sigmoidf_(v[3]));
+      }
+    }
+    if (type == 1) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) knm[hh] = fmaxf(knm[hh], sqrtf(group_sum_fast(ss[hh])));
+    }
+  }
+  if (type == 1) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float v = lanes16_max(knm[hh]);
+      if (l == 0) atomicMax(&a.kmax[row * H + (ob >> 5) + hh], __float_as_uint(v));
+    }
+  }
+}
+
+// out[i][j][c] = (add ? res : 0) + o W_o^T: NT GEMM of the gated attention
+// rows o [I*Jp][H*32] with W_o [C][H*32]; one pair and four consecutive
+// channels per lane.
+template <typename ZT>
+__global__ __launch_bounds__(512) void triatt_out_wide_kernel(TriattOutArgs<ZT, bf16> a, int HD,
+                                                              int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kWNS * WideShape::STAGE_ELEMS];
+  int rt, ct;
+  wide_tile_map(blockIdx.x, ncol, rt, ct);
+  const int64_t x0 = (int64_t)rt * kWTX;
+  const int y0 = ct * kWTY;
+  f32x4 acc[WideShape::MX][WideShape::MY];
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+      [&](int r) { return a.o + (x0 + r) * HD; },
+      [&](int r) { return a.wo + (size_t)(y0 + r) * HD; }, HD, sm, acc);
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kWWX, wy = w / kWWX;
+#pragma unroll
+  for (int i = 0; i < WideShape::MX; ++i) {
+    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + r16;
+    const int row = (int)(m / a.jp), jj = (int)(m % a.jp);
+    if (row >= a.n || jj >= a.n) continue;
+#pragma unroll
+    for (int j = 0; j < WideShape::MY; ++j) {
+      const int c0 = y0 + wy * (kWTY / WideShape::WY) + 16 * j + 4 * g;
+      float r[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.add) load4(a.res + (int64_t)row * a.r_s0 + (int64_t)jj * a.r_s1 + c0, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += acc[i][j][e];
+      store4(a.out + (int64_t)row * a.o_s0 + (int64_t)jj * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+    }
+  }
+}
+
 }  // namespace odde
 
 // ===========================================================================
@@ -1190,16 +1390,31 @@ void carve_core_bufs(Carver& c, CoreBufs& w, int rows, int heads, int jp, int bi
   w.anykeep = c.take<int>((uint64_t)rows);
 }
 
-struct TriattWs { CoreBufs c; void* gate; void* o; uint64_t bytes; };
+// Wide-channel path: bf16 compute, C and H*32 in {128, 256, 384}, one of them
+// 256 or more (the weight slices of the register-resident kernels no longer
+// fit).
+bool triatt_wide(int c, int heads, int dt) {
+  const int hd = heads * 32;
+  return dt == ODDE_BF16 && (c == 128 || c == 256 || c == 384) &&
+         (hd == 128 || hd == 256 || hd == 384) && (c >= 256 || hd >= 256);
+}
+// rows of the wide path's GEMMs: the n * Jp pairs padded to whole groups of
+// 8 row tiles
+int64_t triatt_wide_rows(int n) { return (int64_t)round_up(n * round_up(n, 64), 2048); }
 
-TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int dt) {
+struct TriattWs { CoreBufs c; void* gate; void* o; void* zn; uint64_t bytes; };
+
+TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int cz, int dt) {
   const int jp = round_up(n, 64);
+  const bool wide = triatt_wide(cz, heads, dt);
   const uint64_t per = (uint64_t)n * heads * jp * 32 * dtype_size(dt);
   Carver c(base, size);
   TriattWs w;
   carve_core_bufs(c, w.c, n, heads, jp, 1, dt);
   w.gate = c.take<char>(per);
-  w.o = c.take<char>(per);
+  // the wide path reads o as GEMM rows, whole 256-row tiles
+  w.o = c.take<char>(wide ? (uint64_t)triatt_wide_rows(n) * heads * 32 * 2 : per);
+  w.zn = wide ? c.take<char>((uint64_t)triatt_wide_rows(n) * cz * 2) : nullptr;
   w.bytes = (c.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -1343,11 +1558,48 @@ void fill_core_args(TriattCoreArgs<CT>& c, const CoreBufs& b) {
   c.rowflag = b.rowflag; c.anykeep = b.anykeep;
 }
 
+// Wide-channel projection: LayerNorm pass into bf16 rows, mask outputs and
+// triangle bias, then q, k, v, gate as one NT GEMM.
+template <typename ZT>
+int run_triatt_proj_wide(const TriattProjArgs<ZT, bf16>& p, const odde_triatt_args* a, bf16* zn,
+                         hipStream_t st) {
+  const int n = p.n, jp = p.jp, C = a->c, HD = p.heads * 32;
+  const int64_t rows = (int64_t)n * jp;
+  const int lg = (int)std::min<int64_t>((rows + 15) / 16, 4096);
+  switch (C) {
+    case 128:
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 128>), dim3(lg), dim3(256), 0, st, p.z, p.z_s0,
+                         p.z_s1, n, n, jp, p.ln_w, p.ln_b, p.eps, zn);
+      hipLaunchKernelGGL((triatt_bias_mask_wide_kernel<ZT, 4>), dim3(jp / 64, n), dim3(256), 0,
+                         st, p, zn);
+      break;
+    case 256:
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 256>), dim3(lg), dim3(256), 0, st, p.z, p.z_s0,
+                         p.z_s1, n, n, jp, p.ln_w, p.ln_b, p.eps, zn);
+      hipLaunchKernelGGL((triatt_bias_mask_wide_kernel<ZT, 8>), dim3(jp / 64, n), dim3(256), 0,
+                         st, p, zn);
+      break;
+    case 384:
+      hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 384>), dim3(lg), dim3(256), 0, st, p.z, p.z_s0,
+                         p.z_s1, n, n, jp, p.ln_w, p.ln_b, p.eps, zn);
+      hipLaunchKernelGGL((triatt_bias_mask_wide_kernel<ZT, 12>), dim3(jp / 64, n), dim3(256), 0,
+                         st, p, zn);
+      break;
+    default: return set_error(ODDE_EUNSUPPORTED, "triatt: c must be 128, 256 or 384 here");
+  }
+  const int row_tiles = (int)(triatt_wide_rows(n) / kWTX), ncol = 4 * HD / kWTY;
+  hipLaunchKernelGGL((triatt_qkvg_wide_kernel<ZT>), dim3(row_tiles * ncol), dim3(512), 0, st, p,
+                     zn, C, ncol);
+  return ODDE_OK;
+}
+
 template <typename ZT, typename CT>
 int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   const int n = a->n, H = a->heads, C = a->c, HD = H * 32;
   const int jp = round_up(n, 64);
-  TriattWs ws = carve_triatt(a->workspace, a->workspace_bytes, n, H, a->compute_dtype);
+  TriattWs ws = carve_triatt(a->workspace, a->workspace_bytes, n, H, C, a->compute_dtype);
+  bool wide = false;
+  if constexpr (sizeof(CT) == 2) wide = triatt_wide(C, H, a->compute_dtype);
 
   TriattProjArgs<ZT, CT> p;
   p.z = static_cast<const ZT*>(a->z);
@@ -1372,7 +1624,13 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
     PrepArgs pa{a->mask, a->mask_s0, a->mask_s1, ws.c.anykeep, ws.c.rowflag, ws.c.kmax,
                 ws.c.bmax, n, jp, H};
     hipLaunchKernelGGL(triatt_prep_kernel, dim3(n), dim3(256), 0, st, pa);
-    if (!launch_proj_ws<ZT, CT>(p, C, HD, n, jp, st)) {
+    if constexpr (sizeof(CT) == 2) {
+      if (wide) {
+        int rc = run_triatt_proj_wide<ZT>(p, a, static_cast<bf16*>(ws.zn), st);
+        if (rc) return rc;
+      }
+    }
+    if (!wide && !launch_proj_ws<ZT, CT>(p, C, HD, n, jp, st)) {
       switch (C) {
         case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
         case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
@@ -1402,6 +1660,14 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   o.n = n; o.jp = jp; o.c = C; o.add = a->add_residual;
   {
     LaunchScope ls(ODDE_K_TRIATT_OUT, st);
+    if constexpr (sizeof(CT) == 2) {
+      if (wide) {
+        const int row_tiles = (int)(triatt_wide_rows(n) / kWTX), ncol = C / kWTY;
+        hipLaunchKernelGGL((triatt_out_wide_kernel<ZT>), dim3(row_tiles * ncol), dim3(512), 0, st,
+                           o, HD, ncol);
+        return check_launch("triatt_out (wide)");
+      }
+    }
     if (launch_out_ws<ZT, CT>(o, HD, C, n, jp, st)) return check_launch("triatt_out");
     switch (HD) {
       case 64: launch_out<ZT, CT, 2>(o, n, jp, st); break;
@@ -1422,7 +1688,7 @@ int odde_triatt_workspace_bytes(const odde_triatt_args* a, uint64_t* bytes) {
   int rc = check_triatt(a);
   if (rc) return rc;
   if (!bytes) return set_error(ODDE_EINVAL, "triatt: null bytes");
-  *bytes = carve_triatt(nullptr, 0, a->n, a->heads, a->compute_dtype).bytes;
+  *bytes = carve_triatt(nullptr, 0, a->n, a->heads, a->c, a->compute_dtype).bytes;
   return ODDE_OK;
 }
 
@@ -1432,7 +1698,7 @@ int odde_triatt_fwd(const odde_triatt_args* a, void* stream) {
   if (!a->z || !a->out || !a->ln_w || !a->ln_b || !a->w_bias || !a->w_q || !a->w_k ||
       !a->w_v || !a->w_g || !a->w_o)
     return set_error(ODDE_EINVAL, "triatt: null tensor pointer");
-  const uint64_t need = carve_triatt(nullptr, 0, a->n, a->heads, a->compute_dtype).bytes;
+  const uint64_t need = carve_triatt(nullptr, 0, a->n, a->heads, a->c, a->compute_dtype).bytes;
   if (!a->workspace || a->workspace_bytes < need ||
       (reinterpret_cast<uintptr_t>(a->workspace) & 255))
     return set_error(ODDE_EWORKSPACE, "triatt: workspace missing, too small or not 256-byte aligned");
