@@ -183,6 +183,10 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  *   pb_out[h][r] = sum_c LN'(out[r])[c] * pb_w[h][c]     (f32, [16][rows])
  * with LN' = LayerNorm(pb_ln_w, pb_ln_b (may be NULL), pb_eps); pb_w is
  * [16][c] in compute_dtype.  This saves the separate pass over all of z.
+ * The pair-bias projection is available for c <= 256 (fused kernels).
+ * Wide rows (c = 384) run as a LayerNorm pass and two GEMMs whose hidden
+ * activations live in the workspace (odde_transition_workspace_bytes; 0 for
+ * the fused kernels, which need none).
  */
 typedef struct odde_transition_args {
   uint32_t struct_size;
@@ -206,8 +210,11 @@ typedef struct odde_transition_args {
   const void* pb_w;
   float* pb_out;
   float pb_eps;
+  void* workspace;
+  uint64_t workspace_bytes;
 } odde_transition_args;
 
+int odde_transition_workspace_bytes(const odde_transition_args* args, uint64_t* bytes);
 int odde_transition_fwd(const odde_transition_args* args, void* hip_stream);
 
 /*

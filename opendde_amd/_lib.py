@@ -88,7 +88,7 @@ class TransitionArgs(ctypes.Structure):
         ("x", _vp), ("out", _vp), ("ln_w", _vp), ("ln_b", _vp),
         ("w_a", _vp), ("w_b", _vp), ("w_o", _vp), ("eps", _f32),
         ("pb_heads", _i32), ("pb_ln_w", _vp), ("pb_ln_b", _vp), ("pb_w", _vp), ("pb_out", _vp),
-        ("pb_eps", _f32),
+        ("pb_eps", _f32), ("workspace", _vp), ("workspace_bytes", _u64),
     ]
 
 
@@ -118,6 +118,8 @@ SYMBOLS = {
     "odde_triatt_core_fwd": (_i32, [ctypes.POINTER(TriattCoreArgs), _vp]),
     "odde_trimul_workspace_bytes": (_i32, [ctypes.POINTER(TrimulArgs), ctypes.POINTER(_u64)]),
     "odde_trimul_fwd": (_i32, [ctypes.POINTER(TrimulArgs), _vp]),
+    "odde_transition_workspace_bytes": (_i32, [ctypes.POINTER(TransitionArgs),
+                                               ctypes.POINTER(_u64)]),
     "odde_transition_fwd": (_i32, [ctypes.POINTER(TransitionArgs), _vp]),
     "odde_layer_norm_fwd": (_i32, [ctypes.POINTER(LayerNormArgs), _vp]),
     "odde_layer_norm_bwd_workspace_bytes": (_i32, [ctypes.POINTER(LayerNormBwdArgs),

@@ -12,6 +12,8 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "gemm.hpp"
+#include "lnpass.hpp"
 #include "rowtile.hpp"
 #include "runtime.hpp"
 
@@ -489,6 +491,89 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   }
 }
 
+// Wide form (C = 384): a LayerNorm pass into bf16 rows, then two NT GEMMs on
+// the shared mainloop (gemm.hpp) with the hidden activations in the
+// workspace:  h = silu(y W_a^T) * (y W_b^T)  ([Mp][4C] bf16), then
+// out = (add ? x : 0) + h W_o^T.  GEMM1 reads W_a / W_b rows interleaved in
+// 16-row blocks, so a wave's fragments j (gate) and j + 1 (value) hold the
+// same 16 hidden units.  Rows are padded to whole groups of 8 row tiles;
+// rows past `rows` are never stored.
+constexpr int kTwTX = 256, kTwTY = 128, kTwWX = 4, kTwNS = 3;
+using TwShape = GemmShape<kTwTX, kTwTY, kTwWX>;
+
+__device__ __forceinline__ void tw_tile_map(int L, int ncol, int& rt, int& ct) {
+  const int xcd = L & 7, s = L >> 3;  // all column tiles of a row tile on one XCD
+  rt = xcd + 8 * (s / ncol);
+  ct = s % ncol;
+}
+
+__global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* __restrict__ yn,
+                                                                   const bf16* __restrict__ wa,
+                                                                   const bf16* __restrict__ wb,
+                                                                   bf16* __restrict__ h, int C,
+                                                                   int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kTwNS * TwShape::STAGE_ELEMS];
+  int rt, ct;
+  tw_tile_map(blockIdx.x, ncol, rt, ct);
+  const int64_t x0 = (int64_t)rt * kTwTX;
+  const int y0 = ct * kTwTY, HID = 4 * C;
+  f32x4 acc[TwShape::MX][TwShape::MY];
+  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true>(
+      [&](int r) { return yn + (x0 + r) * C; },
+      [&](int r) {
+        const int R = y0 + r, t = R & 31;
+        return (t < 16 ? wa : wb) + (size_t)((R >> 5) * 16 + (t & 15)) * C;
+      },
+      C, sm, acc);
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kTwWX, wy = w / kTwWX;
+#pragma unroll
+  for (int i = 0; i < TwShape::MX; ++i) {
+    const int64_t m = x0 + wx * (kTwTX / kTwWX) + 16 * i + r16;
+#pragma unroll
+    for (int j = 0; j < TwShape::MY; j += 2) {
+      const int hid = ((y0 + wy * (kTwTY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)(siluf_(acc[i][j][e]) * acc[i][j + 1][e]);
+      *reinterpret_cast<bf16x4*>(h + m * HID + hid) = v;
+    }
+  }
+}
+
+template <typename ZT>
+__global__ __launch_bounds__(512) void transition_wide_out_kernel(const bf16* __restrict__ h,
+                                                                  const bf16* __restrict__ wo,
+                                                                  const ZT* x, ZT* out,
+                                                                  int64_t rows, int C, int add,
+                                                                  int ncol) {
+  __shared__ __attribute__((aligned(16))) bf16 sm[kTwNS * TwShape::STAGE_ELEMS];
+  int rt, ct;
+  tw_tile_map(blockIdx.x, ncol, rt, ct);
+  const int64_t x0 = (int64_t)rt * kTwTX;
+  const int y0 = ct * kTwTY, HID = 4 * C;
+  f32x4 acc[TwShape::MX][TwShape::MY];
+  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true>(
+      [&](int r) { return h + (x0 + r) * HID; },
+      [&](int r) { return wo + (size_t)(y0 + r) * HID; }, HID, sm, acc);
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % kTwWX, wy = w / kTwWX;
+#pragma unroll
+  for (int i = 0; i < TwShape::MX; ++i) {
+    const int64_t m = x0 + wx * (kTwTX / kTwWX) + 16 * i + r16;
+    if (m >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < TwShape::MY; ++j) {
+      const int c0 = y0 + wy * (kTwTY / TwShape::WY) + 16 * j + 4 * g;
+      float r[4] = {0.f, 0.f, 0.f, 0.f};
+      if (add) load4(x + m * C + c0, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += acc[i][j][e];
+      store4(out + m * C + c0, r[0], r[1], r[2], r[3]);
+    }
+  }
+}
+
 }  // namespace odde
 
 using namespace odde;
@@ -502,8 +587,40 @@ void launch_tr(const TransitionArgs<ZT, CT>& p, hipStream_t st) {
   hipLaunchKernelGGL((transition_kernel<ZT, CT, kC, NF>), dim3(grid), dim3(256), 0, st, p, ntiles);
 }
 
+bool transition_wide(int c, int nf, int dt) { return dt == ODDE_BF16 && c == 384 && nf == 4; }
+int64_t transition_wide_rows(int64_t rows) { return (rows + 2047) / 2048 * 2048; }
+uint64_t transition_ws_bytes(const odde_transition_args* a) {
+  if (!transition_wide(a->c, a->n_factor, a->compute_dtype)) return 0;
+  // normalised rows [Mp][C] and hidden activations [Mp][4C], bf16
+  return (uint64_t)transition_wide_rows(a->rows) * 5 * a->c * 2 + 256;
+}
+
+template <typename ZT>
+int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
+  const int C = a->c;
+  const int64_t rows = a->rows, mp = transition_wide_rows(rows);
+  bf16* yn = static_cast<bf16*>(a->workspace);
+  bf16* h = yn + mp * C;
+  LaunchScope ls(ODDE_K_TRANSITION, st);
+  const int lg = (int)std::min<int64_t>((rows + 15) / 16, 4096);
+  // rows as one view row of length `rows` (x = 0, y = row)
+  hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 384>), dim3(lg), dim3(256), 0, st,
+                     static_cast<const ZT*>(a->x), (int64_t)0, (int64_t)C, (int)rows, 1,
+                     (int)rows, a->ln_w, a->ln_b, a->eps, yn);
+  const int row_tiles = (int)(mp / kTwTX);
+  const int ncol1 = 8 * C / kTwTY, ncol2 = C / kTwTY;
+  hipLaunchKernelGGL(transition_wide_gate_kernel, dim3(row_tiles * ncol1), dim3(512), 0, st, yn,
+                     static_cast<const bf16*>(a->w_a), static_cast<const bf16*>(a->w_b), h, C,
+                     ncol1);
+  hipLaunchKernelGGL((transition_wide_out_kernel<ZT>), dim3(row_tiles * ncol2), dim3(512), 0, st,
+                     h, static_cast<const bf16*>(a->w_o), static_cast<const ZT*>(a->x),
+                     static_cast<ZT*>(a->out), rows, C, a->add_residual, ncol2);
+  return check_launch("transition (wide)");
+}
+
 template <typename ZT, typename CT>
 int run_transition(const odde_transition_args* a, hipStream_t st) {
+  if (transition_wide(a->c, a->n_factor, a->compute_dtype)) return run_transition_wide<ZT>(a, st);
   TransitionArgs<ZT, CT> p;
   p.x = static_cast<const ZT*>(a->x);
   p.out = static_cast<ZT*>(a->out);
@@ -524,7 +641,7 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
   }
   else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
   else if (a->c == 256 && a->n_factor == 4) launch_tr<ZT, CT, 8, 4>(p, st);
-  else return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256} with n = 4");
+  else return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256, 384} with n = 4");
   return check_launch("transition");
 }
 
@@ -532,12 +649,24 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
 
 extern "C" {
 
+int odde_transition_workspace_bytes(const odde_transition_args* a, uint64_t* bytes) {
+  if (!a || !bytes) return set_error(ODDE_EINVAL, "transition: null argument");
+  if (a->struct_size != sizeof(odde_transition_args))
+    return set_error(ODDE_EINVAL, "transition: struct_size mismatch (ABI version skew)");
+  if (a->rows < 0 || a->c <= 0 || a->n_factor <= 0)
+    return set_error(ODDE_EINVAL, "transition: bad sizes");
+  *bytes = transition_ws_bytes(a);
+  return ODDE_OK;
+}
+
 int odde_transition_fwd(const odde_transition_args* a, void* stream) {
   if (!a) return set_error(ODDE_EINVAL, "transition: null args");
   if (a->struct_size != sizeof(odde_transition_args))
     return set_error(ODDE_EINVAL, "transition: struct_size mismatch (ABI version skew)");
   if (a->rows < 0 || a->c <= 0 || a->n_factor <= 0)
     return set_error(ODDE_EINVAL, "transition: bad sizes");
+  if (a->rows >= (int64_t(1) << 31))
+    return set_error(ODDE_EUNSUPPORTED, "transition: at most 2^31 - 1 rows per call");
   if (!valid_dtype(a->x_dtype) || !valid_dtype(a->compute_dtype))
     return set_error(ODDE_EINVAL, "transition: bad dtype");
   if (a->compute_dtype != ODDE_BF16)
@@ -546,7 +675,13 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
     return set_error(ODDE_EINVAL, "transition: null tensor pointer");
   if ((reinterpret_cast<uintptr_t>(a->x) | reinterpret_cast<uintptr_t>(a->out)) & 15)
     return set_error(ODDE_EINVAL, "transition: x/out must be 16-byte aligned");
+  const uint64_t need = transition_ws_bytes(a);
+  if (need && a->rows > 0 && (!a->workspace || a->workspace_bytes < need))
+    return set_error(ODDE_EWORKSPACE, "transition: workspace too small");
+  if (need && (reinterpret_cast<uintptr_t>(a->workspace) & 255))
+    return set_error(ODDE_EWORKSPACE, "transition: workspace must be 256-byte aligned");
   if (a->pb_heads != 0) {
+    if (need) return set_error(ODDE_EUNSUPPORTED, "transition: no pair-bias projection at c = 384");
     if (a->pb_heads != 16)
       return set_error(ODDE_EUNSUPPORTED, "transition: pair-bias projection needs 16 heads");
     if (!a->pb_ln_w || !a->pb_w || !a->pb_out)

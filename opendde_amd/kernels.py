@@ -284,7 +284,9 @@ def triangle_attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out[0] if squeeze else out
 
 
-TRANSITION_CHANNELS = (64, 128, 256)
+TRANSITION_CHANNELS = (64, 128, 256, 384)
+# widths whose fused kernel also writes the pair-bias projection
+TRANSITION_PAIR_BIAS_CHANNELS = (64, 128, 256)
 
 
 def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torch.Tensor] = None,
@@ -322,6 +324,9 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     a.ln_w, a.ln_b, a.w_a, a.w_b, a.w_o = (_ptr(t) for t in keep)
     a.eps = float(eps)
     if pair_bias is not None:
+        if c not in TRANSITION_PAIR_BIAS_CHANNELS:
+            raise NotImplementedError(f"fused pair-bias projection needs c in "
+                                      f"{TRANSITION_PAIR_BIAS_CHANNELS}")
         pln_w, pln_b, pw, peps, dest = pair_bias
         rows = a.rows
         if pw.shape != (16, c):
@@ -339,6 +344,14 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
         a.pb_ln_b = _ptr(pkeep[2]) if pln_b is not None else None
         a.pb_out = _ptr(dest)
         a.pb_eps = float(peps)
-    _lib.check(_lib.load().odde_transition_fwd(ctypes.byref(a), _stream(x.device)),
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    _lib.check(lib.odde_transition_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)),
+               "odde_transition_workspace_bytes")
+    ws = None
+    if nb.value:
+        ws = _workspace(nb.value, x.device)
+        a.workspace, a.workspace_bytes = _ptr(ws), ws.numel()
+    _lib.check(lib.odde_transition_fwd(ctypes.byref(a), _stream(x.device)),
                "odde_transition_fwd")
     return out

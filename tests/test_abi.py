@@ -93,6 +93,16 @@ def test_bad_arguments_return_status_and_message():
     tr.pb_heads = 16
     rc, msg = _status("odde_transition_fwd", tr)
     assert rc == -1 and "pair-bias" in msg
+    # c = 384 runs as LN pass + two GEMMs with the hidden rows in a workspace
+    tr.c, tr.pb_heads = 384, 0
+    nb = ctypes.c_uint64(0)
+    assert _lib.load().odde_transition_workspace_bytes(ctypes.byref(tr), ctypes.byref(nb)) == 0
+    assert nb.value >= 2048 * 5 * 384 * 2
+    rc, msg = _status("odde_transition_fwd", tr)
+    assert rc == -3 and "workspace" in msg
+    tr.c = 128
+    assert _lib.load().odde_transition_workspace_bytes(ctypes.byref(tr), ctypes.byref(nb)) == 0
+    assert nb.value == 0
 
 
 def test_workspace_query_and_too_small_workspace():

@@ -9,9 +9,9 @@ multiplication hidden width to c_z, modules/pairformer.py:91-93):
 * the MSA module's pair stack: c_z = 384, c_s = 0 (pairformer.py:804-808);
 * the template embedder's stack: c = 64, c_s = 0, 2 blocks, 2 heads,
   c_hidden_mul = 64 (pairformer.py:1678-1685).
-Each runs through the HIP triangle kernels (the pair transition at c = 384 is
-the torch path: the fused transition kernel takes c in {64, 128, 256}) and is
-compared with the CPU oracle: fp32 to max-abs 1e-4, bf16 autocast to the
+Each runs through the HIP triangle kernels (and, in the bf16 mode, the HIP
+pair transition: fused at c = 64, LayerNorm pass + two GEMMs at c = 384) and
+is compared with the CPU oracle: fp32 to max-abs 1e-4, bf16 autocast to the
 bf16 tier on the block's update.
 """
 
@@ -76,11 +76,14 @@ def test_consumer_stack_matches_oracle(name, autocast):
     p = params_of(stack)
     se, ze = ref.pairformer_stack(s, z, mask, p, n_blocks, no_heads_pair=heads, n_heads=16)
     stack = stack.to(DEV)
-    before = (_lib.launch_count(_lib.K_TRIATT_CORE), _lib.launch_count(_lib.K_TRIMUL_CONTRACT))
+    before = (_lib.launch_count(_lib.K_TRIATT_CORE), _lib.launch_count(_lib.K_TRIMUL_CONTRACT),
+              _lib.launch_count(_lib.K_TRANSITION))
     sg, zg = _run(stack, s, z, mask, autocast)
     torch.cuda.synchronize()
     assert _lib.launch_count(_lib.K_TRIATT_CORE) == before[0] + 2 * n_blocks
     assert _lib.launch_count(_lib.K_TRIMUL_CONTRACT) == before[1] + 2 * n_blocks
+    # the HIP transition computes in bf16: it runs in the bf16 mode only
+    assert _lib.launch_count(_lib.K_TRANSITION) == before[2] + (n_blocks if autocast else 0)
     if autocast:
         assert_bf16(zg - z.to(DEV), ze - z, f"{name} z update")
         if c_s:

@@ -290,12 +290,12 @@ def test_triangle_attention_fully_masked_rows_are_mean_of_v(n_pad):
 # -------------------------------------------------------------- transition
 
 
-@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130)])
+@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 1000), (384, 130)])
 def test_transition_bf16(c, rows):
     from opendde_amd.pairformer import Transition
-    # weights scaled so the output stays O(1) at every width (the absolute
-    # bound of the bf16 tier is scale dependent)
-    mod = seeded(Transition(c, 4), 700 + c, STD * (128 / c) ** 0.5)
+    # weights scaled so the output stays O(1) at every width (std ~0.6, max
+    # ~3; the absolute bound of the bf16 tier is scale dependent)
+    mod = seeded(Transition(c, 4), 700 + c, 0.7 * STD * (128 / c) ** 0.5)
     x = torch.randn(rows, c, generator=torch.Generator().manual_seed(c)).to(torch.bfloat16)
     exp = ref.transition(x.float(), params_of(mod))
     before = _lib.launch_count(_lib.K_TRANSITION)
@@ -305,10 +305,11 @@ def test_transition_bf16(c, rows):
     assert_bf16(got, exp, f"transition c={c} rows={rows}")
 
 
-def test_transition_fp32_residual_under_autocast_in_place():
+@pytest.mark.parametrize("c", [128, 384])
+def test_transition_fp32_residual_under_autocast_in_place(c):
     from opendde_amd.pairformer import Transition
-    mod = seeded(Transition(128, 4), 711, STD).to(DEV)
-    x = torch.randn(64, 64, 128, generator=torch.Generator().manual_seed(3))
+    mod = seeded(Transition(c, 4), 711, STD * (128 / c) ** 0.5).to(DEV)
+    x = torch.randn(64, 64, c, generator=torch.Generator().manual_seed(3))
     exp = x + ref.transition(x, params_of(mod))
     xg = x.to(DEV)
     with torch.autocast("cuda", dtype=torch.bfloat16):
