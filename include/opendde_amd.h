@@ -183,10 +183,10 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  *   pb_out[h][r] = sum_c LN'(out[r])[c] * pb_w[h][c]     (f32, [16][rows])
  * with LN' = LayerNorm(pb_ln_w, pb_ln_b (may be NULL), pb_eps); pb_w is
  * [16][c] in compute_dtype.  This saves the separate pass over all of z.
- * The pair-bias projection is available for c <= 256 (fused kernels).
  * Wide rows (c = 384) run as a LayerNorm pass and two GEMMs whose hidden
  * activations live in the workspace (odde_transition_workspace_bytes; 0 for
- * the fused kernels, which need none).
+ * the fused kernels, which need none), and the pair-bias projection as a pass
+ * over the rows written.
  */
 typedef struct odde_transition_args {
   uint32_t struct_size;

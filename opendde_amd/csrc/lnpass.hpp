@@ -87,6 +87,10 @@ __global__ __launch_bounds__(256) void ln_view_bf16_kernel(const ZT* __restrict_
 // (bf16): a workgroup transposes the 64-column block P[:, x, y0..y0+63]
 // through LDS, then 4 threads per column normalise its CH channels.  Grid
 // (np / 64, np).  Columns with x >= n or y >= n are written as zeros.
+// In the transposed tile, row y keeps channel c at column
+// c ^ (8 * ((y >> 3) & 7)) (8-channel groups permuted by y / 8): the lanes of
+// one transposing store cover 8 channels at 8 rows y0 + 8k + e, which then
+// fall on distinct bank groups instead of one.
 template <int CH>
 __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __restrict__ P, int np,
                                                                 int n,
@@ -95,24 +99,34 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
                                                                 float eps, bf16* __restrict__ out) {
   constexpr int LD = CH + 8;     // LDS row stride (elements) of the transposed tile
   constexpr int Q = CH / 4;      // channels per thread in the LayerNorm pass
+  static_assert(CH % 64 == 0, "the column permutation stays within 64-channel groups");
   __shared__ __attribute__((aligned(16))) bf16 t[64 * LD];
   const int x = blockIdx.y, y0 = blockIdx.x * 64;
   const bf16* src = P + (size_t)x * np + y0;
-  for (int ci = threadIdx.x; ci < CH * 8; ci += 256) {  // 8 16-byte chunks per channel row
-    const int c = ci >> 3, yy = (ci & 7) * 8;
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)c * np * np + yy);
+  constexpr int NL = CH * 8 / 256;  // 16-byte chunks per thread (8 per channel row)
+  bf16x8 ld[NL];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) t[(yy + e) * LD + c] = v[e];
+  for (int k = 0; k < NL; ++k) {  // all loads in flight before the first LDS store
+    const int ci = threadIdx.x + 256 * k, c = ci >> 3, yy = (ci & 7) * 8;
+    ld[k] = *reinterpret_cast<const bf16x8*>(src + (size_t)c * np * np + yy);
+  }
+#pragma unroll
+  for (int k = 0; k < NL; ++k) {
+    const int ci = threadIdx.x + 256 * k, c = ci >> 3, yy = (ci & 7) * 8;
+    const int cs = c ^ (8 * ((yy >> 3) & 7));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[(yy + e) * LD + cs] = ld[k][e];
   }
   __syncthreads();
   const int yl = threadIdx.x >> 2, part = threadIdx.x & 3;
   const int y = y0 + yl;
   const bool valid = x < n && y < n;
-  const bf16* row = t + yl * LD + part * Q;
+  const bf16* row = t + yl * LD;
+  const int sw = 8 * ((yl >> 3) & 7);
   float v[Q];
 #pragma unroll
   for (int k = 0; k < Q / 8; ++k) {
-    const bf16x8 h = *reinterpret_cast<const bf16x8*>(row + 8 * k);
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(row + ((part * Q + 8 * k) ^ sw));
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[8 * k + e] = (float)h[e];
   }

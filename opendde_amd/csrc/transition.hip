@@ -37,6 +37,7 @@ struct TransitionArgs {
   const CT* pb_w;        // [16][C]
   float* pb_out;         // [16][rows]
   float pb_eps;
+  const float* pb_zero;  // C zeros (stand-in for a null pb_ln_b)
 };
 
 constexpr int kTrRows = 128;  // rows per workgroup tile
@@ -498,6 +499,38 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 // 16-row blocks, so a wave's fragments j (gate) and j + 1 (value) hold the
 // same 16 hidden units.  Rows are padded to whole groups of 8 row tiles;
 // rows past `rows` are never stored.
+__global__ void fill_zero_kernel(float* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0.f;
+}
+
+// Pair-bias projection of the rows as written (the fused kernels do this in
+// their epilogue): 16 rows per wave, each lane loads its K32 fragment slots of
+// a row, LayerNorm statistics over the four lanes of the row, then 16 heads
+// by MFMA against pb_w; pb_out[h][r] = sum_c LN'(out[r])[c] pb_w[h][c].
+template <typename ZT, int kC>
+__global__ __launch_bounds__(256) void transition_pair_bias_kernel(TransitionArgs<ZT, bf16> a) {
+  constexpr int C = kC * 32;
+  const int l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int64_t nblk = (a.rows + 15) / 16;
+  Frag<bf16> wf[kC];
+#pragma unroll
+  for (int t = 0; t < kC; ++t) load_w_frag(a.pb_w, C, 0, 16, t, wf[t]);
+  for (int64_t b = int64_t(blockIdx.x) * 4 + wave_id(); b < nblk; b += int64_t(gridDim.x) * 4) {
+    const int64_t row = b * 16 + r16;
+    const bool valid = row < a.rows;
+    Frag<bf16> yf[kC];
+    ln_rows_to_frags<ZT, bf16, C>(a.out + (valid ? row : 0) * C, valid, a.pb_ln_w,
+                                  a.pb_ln_b ? a.pb_ln_b : a.pb_zero, a.pb_eps, yf);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < kC; ++t) mma(acc, wf[t], yf[t]);
+    if (valid) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a.pb_out[(size_t)(4 * g + e) * a.rows + row] = acc[e];
+    }
+  }
+}
+
 constexpr int kTwTX = 256, kTwTY = 128, kTwWX = 4, kTwNS = 3;
 using TwShape = GemmShape<kTwTX, kTwTY, kTwWX>;
 
@@ -615,6 +648,27 @@ int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
   hipLaunchKernelGGL((transition_wide_out_kernel<ZT>), dim3(row_tiles * ncol2), dim3(512), 0, st,
                      h, static_cast<const bf16*>(a->w_o), static_cast<const ZT*>(a->x),
                      static_cast<ZT*>(a->out), rows, C, a->add_residual, ncol2);
+  if (a->pb_heads) {
+    TransitionArgs<ZT, bf16> p;
+    p.out = static_cast<ZT*>(a->out);
+    p.rows = rows;
+    p.pb_ln_w = a->pb_ln_w;
+    p.pb_ln_b = a->pb_ln_b;
+    p.pb_w = static_cast<const bf16*>(a->pb_w);
+    p.pb_out = a->pb_out;
+    p.pb_eps = a->pb_eps;
+    // without an LN bias the kernel reads a row of zeros, written into the
+    // hidden buffer (no longer needed once the output GEMM has run)
+    float* zero = reinterpret_cast<float*>(h);
+    if (!a->pb_ln_b) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(256), 0, st, zero, C);
+      p.pb_zero = zero;
+    } else {
+      p.pb_zero = a->pb_ln_b;
+    }
+    const int grid = (int)std::min<int64_t>((rows + 63) / 64, 4096);
+    hipLaunchKernelGGL((transition_pair_bias_kernel<ZT, 12>), dim3(grid), dim3(256), 0, st, p);
+  }
   return check_launch("transition (wide)");
 }
 
@@ -681,7 +735,6 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
   if (need && (reinterpret_cast<uintptr_t>(a->workspace) & 255))
     return set_error(ODDE_EWORKSPACE, "transition: workspace must be 256-byte aligned");
   if (a->pb_heads != 0) {
-    if (need) return set_error(ODDE_EUNSUPPORTED, "transition: no pair-bias projection at c = 384");
     if (a->pb_heads != 16)
       return set_error(ODDE_EUNSUPPORTED, "transition: pair-bias projection needs 16 heads");
     if (!a->pb_ln_w || !a->pb_w || !a->pb_out)

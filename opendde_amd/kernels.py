@@ -285,8 +285,6 @@ def triangle_attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 
 TRANSITION_CHANNELS = (64, 128, 256, 384)
-# widths whose fused kernel also writes the pair-bias projection
-TRANSITION_PAIR_BIAS_CHANNELS = (64, 128, 256)
 
 
 def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torch.Tensor] = None,
@@ -324,9 +322,6 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     a.ln_w, a.ln_b, a.w_a, a.w_b, a.w_o = (_ptr(t) for t in keep)
     a.eps = float(eps)
     if pair_bias is not None:
-        if c not in TRANSITION_PAIR_BIAS_CHANNELS:
-            raise NotImplementedError(f"fused pair-bias projection needs c in "
-                                      f"{TRANSITION_PAIR_BIAS_CHANNELS}")
         pln_w, pln_b, pw, peps, dest = pair_bias
         rows = a.rows
         if pw.shape != (16, c):

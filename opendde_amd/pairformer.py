@@ -235,8 +235,7 @@ class PairformerBlock(nn.Module):
         z_bias = None
         if (hip_mul or hip_att) and self.pair_transition.hip_supported(z):
             pb = None
-            if (self.c_s > 0 and z.dim() == 3 and self.attention_pair_bias.hip_pair_bias_ok()
-                    and z.shape[-1] in K.TRANSITION_PAIR_BIAS_CHANNELS):
+            if self.c_s > 0 and z.dim() == 3 and self.attention_pair_bias.hip_pair_bias_ok():
                 z_bias = torch.empty((16, z.shape[0], z.shape[1]), dtype=torch.float32,
                                      device=z.device)
                 pb = self.attention_pair_bias.pair_bias_spec(z_bias.view(16, -1))

@@ -320,21 +320,23 @@ def test_transition_fp32_residual_under_autocast_in_place(c):
 
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
-def test_transition_pair_bias_projection(x_dtype):
-    # the single track's pair bias linear_nobias_z(layernorm_z(z)) computed in
-    # the transition kernel's epilogue from the rows it writes
-    from opendde_amd import kernels as K
+@pytest.mark.parametrize("c,ln_offset", [(128, True), (384, True), (384, False)])
+def test_transition_pair_bias_projection(x_dtype, c, ln_offset):
+    # the single track's pair bias linear_nobias_z(layernorm_z(z)) computed
+    # from the rows the transition writes (fused epilogue at c = 128, a pass
+    # after the GEMMs at c = 384)
     from opendde_amd.pairformer import AttentionPairBias, Transition
-    n = 75  # 5625 rows: ragged against the 128-row tiles
+    n = 75  # 5625 rows: ragged against the row tiles
     # smaller transition weights keep z's update O(1): with bf16 storage the
     # written z also carries the rounding of |z| ~ 4 values (ulp 2^-5)
-    tr = seeded(Transition(128, 4), 720, STD / 2)
-    apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=128), 721, 0.1)
-    x = torch.randn(n, n, 128, generator=torch.Generator().manual_seed(5)).to(x_dtype)
+    tr = seeded(Transition(c, 4), 720, STD / 2 * (128 / c) ** 0.5)
+    apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=c, create_offset_ln_z=ln_offset), 721,
+                 0.1 * (128 / c) ** 0.5)
+    x = torch.randn(n, n, c, generator=torch.Generator().manual_seed(5)).to(x_dtype)
     xf = x.float()
     z_new = xf + ref.transition(xf, params_of(tr))
     pz = params_of(apb)
-    exp_bias = ref.linear(ref.layer_norm(z_new, pz["layernorm_z.weight"], pz["layernorm_z.bias"]),
+    exp_bias = ref.linear(ref.layer_norm(z_new, pz["layernorm_z.weight"], pz.get("layernorm_z.bias")),
                           pz["linear_nobias_z.weight"]).permute(2, 0, 1)
     tr, apb = tr.to(DEV), apb.to(DEV)
     xg = x.to(DEV)
@@ -342,8 +344,8 @@ def test_transition_pair_bias_projection(x_dtype):
     with torch.autocast("cuda", dtype=torch.bfloat16):
         out = tr.hip_apply(xg, out=xg, add_residual=True,
                            pair_bias=apb.pair_bias_spec(dest.view(16, -1)))
-    assert_bf16(out.float() - xf.to(DEV), z_new - xf, f"transition update ({x_dtype})")
-    assert_bf16(dest, exp_bias, f"fused pair bias ({x_dtype})")
+    assert_bf16(out.float() - xf.to(DEV), z_new - xf, f"transition update ({x_dtype}, c={c})")
+    assert_bf16(dest, exp_bias, f"pair bias ({x_dtype}, c={c}, offset={ln_offset})")
 
 
 def test_pairformer_block_bf16_autocast():
