@@ -247,7 +247,10 @@ class PairformerBlock(nn.Module):
         if self.c_s > 0:
             s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias,
                                              z_bias=z_bias)
-            s = s + self.single_transition(s)
+            if (hip_mul or hip_att) and self.single_transition.hip_supported(s):
+                s = self.single_transition.hip_apply(s.contiguous(), add_residual=True)
+            else:
+                s = s + self.single_transition(s)
         return s, z
 
 

@@ -366,7 +366,8 @@ def test_pairformer_block_bf16_autocast():
         sg, zg = blk(s.to(DEV), z.to(DEV).clone(), mask.to(DEV), triangle_multiplicative="hip",
                      triangle_attention="hip", inplace_safe=True)
     hook.remove()
-    assert _lib.launch_count(_lib.K_TRANSITION) == before + 1
+    # the pair transition (with the fused pair bias) and the single transition
+    assert _lib.launch_count(_lib.K_TRANSITION) == before + 2
     assert not ln_z_calls, "pair bias should come from the fused transition epilogue"
     assert zg.dtype == torch.float32
     assert_bf16(zg - z.to(DEV), ze - z, "block update z (bf16 arithmetic)")
