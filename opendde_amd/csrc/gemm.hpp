@@ -4,15 +4,21 @@
 // on a workgroup of 8 waves (WX along x, 8/WX along y; each wave owns a
 // (TX/WX) x (TY/WY) block as MX x MY 16x16 fragments).
 //
-// K advances in stages of 32 staged by direct global -> LDS loads
+// K advances in stages of KC (32 or 64) staged by direct global -> LDS loads
 // (global_load_lds_dwordx4) into NS buffers: stage s+NS-1 streams in while
 // stage s is multiplied.  One fence-free barrier per stage suffices: each
 // wave first waits for its own loads of stage s (vmcnt) and its own LDS reads
 // of stage s-1 (lgkmcnt), and the buffer refilled at stage s was last read at
-// stage s-1.  LDS rows are 64 bytes (4 chunks of 16); slot t of row r holds
-// chunk t ^ ((r >> 1) & 3), which spreads the K32 fragment reads of 16
-// consecutive rows over all banks.  Every load issued is consumed before the
-// mainloop returns (no load is in flight afterwards).
+// stage s-1.  An LDS row holds the KC elements of one A or B row (KC/8
+// chunks of 16 bytes); its slot t holds chunk t ^ f(row) with
+// f = (row >> 1) & 3 for KC = 32 and f = row & 7 for KC = 64, which keeps the
+// fragment reads of 8 consecutive rows on distinct bank groups.  Every load
+// issued is consumed before the mainloop returns (no load is in flight
+// afterwards).
+//
+// KC = 64 reads whole 128-byte lines of every row per stage: a direct load
+// that covers 16 rows x 64 bytes moves half as many bytes per cycle from L2
+// as one covering 8 rows x 128 bytes.
 //
 // Orientation (the accumulator layout, see common.hpp):
 //   kPairCols = true : acc[i][j] column (lane % 16) is A row
@@ -26,45 +32,61 @@
 
 namespace odde {
 
-constexpr int kCk = 32;  // k per stage
+constexpr int kCk = 32;  // default k per stage
 
-__device__ __forceinline__ int ct_swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+// LDS slot of chunk `chunk` of row `row` (an involution: also the chunk held
+// by a slot)
+template <int KC>
+__device__ __forceinline__ int gemm_swz(int row, int chunk) {
+  if constexpr (KC == 32) {
+    return chunk ^ ((row >> 1) & 3);
+  } else {
+    return chunk ^ (row & 7);
+  }
+}
+__device__ __forceinline__ int ct_swz(int row, int chunk) { return gemm_swz<32>(row, chunk); }
 
-template <int TX, int TY, int WX>
+template <int TX, int TY, int WX, int KC = kCk>
 struct GemmShape {
+  static_assert(KC == 32 || KC == 64, "32 or 64 k per stage");
   static constexpr int WY = 8 / WX;
   static constexpr int MX = TX / WX / 16, MY = TY / WY / 16;  // fragments per wave
-  static constexpr int OPS_A = TX / 16 / 8, OPS_B = TY / 16 / 8;  // 1 KiB loads per wave
+  static constexpr int CPR = KC / 8;                          // 16-byte chunks per row
+  static constexpr int RPO = 64 / CPR;                        // rows per 1 KiB load
+  static constexpr int OPS_A = TX / RPO / 8, OPS_B = TY / RPO / 8;  // 1 KiB loads per wave
   static constexpr int OPS = OPS_A + OPS_B;
-  static constexpr int STAGE_ELEMS = (TX + TY) * kCk;             // bf16 per stage
+  static constexpr int STAGE_ELEMS = (TX + TY) * KC;          // bf16 per stage
   static_assert(TX % (16 * 8) == 0 && TY % (16 * 8) == 0, "16-row blocks per wave");
 };
 
 // arow(r) / brow(r): pointer to element k = 0 of the tile's A row r
-// (r < TX) / B row r (r < TY), each readable for K elements; K a multiple
-// of 32 and at least 32 * (NS - 1).  sm holds NS stages of STAGE_ELEMS.
-template <int TX, int TY, int WX, int NS, bool kPairCols, typename ARow, typename BRow>
+// (r < TX) / B row r (r < TY), each readable for K elements; K a positive
+// multiple of KC.  sm holds NS stages of STAGE_ELEMS.
+template <int TX, int TY, int WX, int NS, bool kPairCols, int KC = kCk, typename ARow,
+          typename BRow>
 __device__ __forceinline__ void gemm_nt_mainloop(
     ARow arow, BRow brow, int K, bf16* sm,
-    f32x4 (&acc)[GemmShape<TX, TY, WX>::MX][GemmShape<TX, TY, WX>::MY]) {
-  using S = GemmShape<TX, TY, WX>;
+    f32x4 (&acc)[GemmShape<TX, TY, WX, KC>::MX][GemmShape<TX, TY, WX, KC>::MY]) {
+  using S = GemmShape<TX, TY, WX, KC>;
+  static_assert(NS >= 2 && NS <= 4, "2 to 4 stage buffers");
   constexpr int MX = S::MX, MY = S::MY, OPS_A = S::OPS_A, OPS_B = S::OPS_B, OPS = S::OPS;
+  constexpr int CPR = S::CPR, RPO = S::RPO;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % WX, wy = w / WX;
 
-  // 1 KiB (16 rows of 64 bytes) per wave instruction; wave w loads A blocks
-  // w*OPS_A.. and B blocks w*OPS_B..; source pointers are fixed per lane, only
-  // k advances.
+  // 1 KiB (RPO rows of KC elements) per wave instruction; wave w loads A
+  // blocks w*OPS_A.. and B blocks w*OPS_B..; lane l fills slot l % CPR of row
+  // l / CPR of the block.  Source pointers are fixed per lane, only k advances.
   const bf16* src0[OPS];
 #pragma unroll
   for (int op = 0; op < OPS; ++op) {
     const bool isb = op >= OPS_A;
     const int blk = isb ? w * OPS_B + (op - OPS_A) : w * OPS_A + op;
-    const int row = blk * 16 + (l >> 2);
-    src0[op] = (isb ? brow(row) : arow(row)) + ct_swz(row, l & 3) * 8;
+    const int row = blk * RPO + l / CPR;
+    src0[op] = (isb ? brow(row) : arow(row)) + gemm_swz<KC>(row, l % CPR) * 8;
   }
   auto issue = [&](int st) {
-    const int k0 = st * kCk;
+    const int k0 = st * KC;
     bf16* base = sm + (st % NS) * S::STAGE_ELEMS;
 #pragma unroll
     for (int op = 0; op < OPS; ++op) {
@@ -73,7 +95,7 @@ __device__ __forceinline__ void gemm_nt_mainloop(
       const bf16* src = src0[op] + k0;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)src,
-          (__attribute__((address_space(3))) void*)(base + (isb ? TX * kCk : 0) + blk * 512),
+          (__attribute__((address_space(3))) void*)(base + (isb ? TX * KC : 0) + blk * 512),
           16, 0, 0);
     }
   };
@@ -83,20 +105,20 @@ __device__ __forceinline__ void gemm_nt_mainloop(
 #pragma unroll
     for (int j = 0; j < MY; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // fragment offsets: the swizzle depends on r16 only (rows step by 16)
-  const int fsw = ct_swz(r16, g) * 8;
-  const int aoff = (wx * (TX / WX) + r16) * kCk + fsw;
-  const int boff = TX * kCk + (wy * (TY / S::WY) + r16) * kCk + fsw;
+  // fragment rows: the swizzle depends on r16 only (rows step by 16)
+  const int arow0 = (wx * (TX / WX) + r16) * KC;
+  const int brow0 = TX * KC + (wy * (TY / S::WY) + r16) * KC;
 
-  const int nst = K / kCk;
+  const int nst = K / KC;
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st) issue(st);
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < nst) issue(st);
   for (int st = 0; st < nst; ++st) {
     // this wave's loads of stage st landed (up to NS-2 later stages in flight)
-    const int ahead = min(nst - 1 - st, NS - 2);
-    if (ahead >= 2) {
+    const int later = min(nst - 1 - st, NS - 2);
+    if (later >= 2) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * OPS) : "memory");
-    } else if (ahead == 1) {
+    } else if (later == 1) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS) : "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -105,21 +127,30 @@ __device__ __forceinline__ void gemm_nt_mainloop(
     barrier_nofence();
     if (st + NS - 1 < nst) issue(st + NS - 1);
     const bf16* base = sm + (st % NS) * S::STAGE_ELEMS;
-    Frag<bf16> af[MX], bfr[MY];
+    // all fragments of the stage are requested before the first multiply
+    constexpr int KSUB = KC / 32;
+    Frag<bf16> fa[KSUB][MX], fb[KSUB][MY];
 #pragma unroll
-    for (int j = 0; j < MY; ++j) bfr[j].load(base + boff + j * 16 * kCk);
+    for (int kk = 0; kk < KSUB; ++kk) {
+      const int fsw = gemm_swz<KC>(r16, 4 * kk + g) * 8;
 #pragma unroll
-    for (int i = 0; i < MX; ++i) af[i].load(base + aoff + i * 16 * kCk);
+      for (int j = 0; j < MY; ++j) fb[kk][j].load(base + brow0 + j * 16 * KC + fsw);
 #pragma unroll
-    for (int i = 0; i < MX; ++i)
+      for (int i = 0; i < MX; ++i) fa[kk][i].load(base + arow0 + i * 16 * KC + fsw);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < MY; ++j) {
-        if constexpr (kPairCols) {
-          mma(acc[i][j], bfr[j], af[i]);
-        } else {
-          mma(acc[i][j], af[i], bfr[j]);
+    for (int kk = 0; kk < KSUB; ++kk)
+#pragma unroll
+      for (int i = 0; i < MX; ++i)
+#pragma unroll
+        for (int j = 0; j < MY; ++j) {
+          if constexpr (kPairCols) {
+            mma(acc[i][j], fb[kk][j], fa[kk][i]);
+          } else {
+            mma(acc[i][j], fa[kk][i], fb[kk][j]);
+          }
         }
-      }
   }
   // the stage buffers may be refilled by the caller's next mainloop
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

@@ -184,9 +184,9 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(ContractArgs<CT> a
 
 // Large-tile form (bf16, Np a multiple of 256): TX x TY tiles per workgroup
 // of 8 waves, the shared NT mainloop (gemm.hpp) over k = 0..Np.
-template <int TX, int TY, int WX, int NS>
+template <int TX, int TY, int WX, int NS, int KC>
 __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<bf16> a) {
-  using S = GemmShape<TX, TY, WX>;
+  using S = GemmShape<TX, TY, WX, KC>;
   __shared__ __attribute__((aligned(16))) bf16 sm[NS * S::STAGE_ELEMS];
   const int TXn = a.np / TX, TYn = a.np / TY;
   const int tiles = TXn * TYn;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
   f32x4 acc[S::MX][S::MY];
   const bf16* Ab = a.A + c * plane + (size_t)x0 * a.np;
   const bf16* Bb = a.B + c * plane + (size_t)y0 * a.np;
-  gemm_nt_mainloop<TX, TY, WX, NS, true>([&](int r) { return Ab + (size_t)r * a.np; },
+  gemm_nt_mainloop<TX, TY, WX, NS, true, KC>([&](int r) { return Ab + (size_t)r * a.np; },
                                          [&](int r) { return Bb + (size_t)r * a.np; }, a.np, sm,
                                          acc);
   // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16), rows y = y0 + wy*TY/WY + 16j + 4g + r
@@ -219,6 +219,22 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
       const int yy = y0 + wy * (TY / S::WY) + j * 16 + 4 * g;
       store4(Pb + (size_t)xx * a.np + yy, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
     }
+}
+
+// Np >= 1024: 256 x 256 tiles staged 64 k at a time (whole 128-byte lines of
+// each row; 128 KiB of LDS, one workgroup per CU); smaller Np: 256 x 128
+// tiles staged 32 k at a time (two workgroups per CU), which keeps more
+// workgroups per channel.  Both measured on MI355X.
+inline void launch_contract_big(const ContractArgs<bf16>& k, int np, int ch, hipStream_t st) {
+  if (np >= 1024) {
+    const int tiles = (np / 256) * (np / 256);
+    hipLaunchKernelGGL((trimul_contract_big_kernel<256, 256, 2, 2, 64>), dim3(tiles * ch), dim3(512),
+                       0, st, k);
+  } else {
+    const int tiles = (np / 256) * (np / 128);
+    hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3, 32>), dim3(tiles * ch), dim3(512),
+                       0, st, k);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -756,9 +772,7 @@ int run_trimul_wide(const odde_trimul_args* a, const TrimulWs& ws, hipStream_t s
   {
     LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
     if (np % 256 == 0) {
-      const int tiles = (np / 256) * (np / 128);
-      hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3>), dim3(tiles * ch), dim3(512),
-                         0, st, k);
+      launch_contract_big(k, np, ch, st);
     } else {
       const int tiles = (np / 128) * (np / 128);
       hipLaunchKernelGGL((trimul_contract_kernel<bf16>), dim3(tiles * ch), dim3(256), 0, st, k);
@@ -923,10 +937,8 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   {
     LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
     if constexpr (sizeof(CT) == 2) {
-      if (np % 256 == 0) {  // 256 x 128 tiles, two workgroups per CU
-        const int tiles = (np / 256) * (np / 128);
-        hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3>), dim3(tiles * ch),
-                           dim3(512), 0, st, k);
+      if (np % 256 == 0) {
+        launch_contract_big(k, np, ch, st);
       } else {
         const int tiles = (np / 128) * (np / 128);
         hipLaunchKernelGGL((trimul_contract_kernel<CT>), dim3(tiles * ch), dim3(256), 0, st, k);
