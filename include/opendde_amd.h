@@ -49,7 +49,8 @@ extern "C" {
 #define ODDE_K_TRANSITION 7
 #define ODDE_K_LAYER_NORM 8
 #define ODDE_K_LAYER_NORM_BWD 9
-#define ODDE_K_COUNT 10
+#define ODDE_K_OPM 10
+#define ODDE_K_COUNT 11
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -272,6 +273,51 @@ typedef struct odde_layer_norm_bwd_args {
 int odde_layer_norm_fwd(const odde_layer_norm_args* args, void* hip_stream);
 int odde_layer_norm_bwd_workspace_bytes(const odde_layer_norm_bwd_args* args, uint64_t* bytes);
 int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* args, void* hip_stream);
+
+/*
+ * OuterProductMean, the MSA -> pair update of the MSA module (replaces
+ * OuterProductMean._forward / _opm, opendde/model/triangular/layers.py:
+ * 525-616, called by MSABlock.forward, opendde/model/modules/pairformer.py:
+ * 1289-1292; its row chunking is numerically neutral):
+ *   y = LN(m[s][i]); a = mask[s][i] * (y W_1^T); b = mask[s][i] * (y W_2^T)
+ *   upd[i][j][z] = (sum_{c1,c2} W_out[z][c1*32 + c2] sum_s a[s][i][c1] b[s][j][c2]
+ *                   + b_out[z]) / (sum_s mask[s][i] mask[s][j] + eps)
+ *   out = (add_residual ? out : 0) + upd    (upd rounded to bf16 first)
+ * m: [n_seq][n_res][c_m] contiguous (f32 or bf16); mask: f32 [n_seq][n_res]
+ * or NULL (all ones); out: [n_res][n_res][c_z] contiguous (f32 or bf16).
+ * W_12 = [W_1; W_2]: [2*c_hidden][c_m], W_out: [c_z][c_hidden^2] in
+ * compute_dtype (bf16 only); LN params, b_out (may be NULL) f32.  c_hidden =
+ * 32; c_m in {32, 64, 128}; c_z in {64, 128, 256, 384}.  The workspace
+ * (odde_opm_workspace_bytes, 256-byte aligned) holds a and b transposed, MSA
+ * rows innermost.
+ */
+typedef struct odde_opm_args {
+  uint32_t struct_size;
+  int32_t n_seq;
+  int32_t n_res;
+  int32_t c_m;
+  int32_t c_hidden;
+  int32_t c_z;
+  int32_t m_dtype;
+  int32_t out_dtype;
+  int32_t compute_dtype;
+  int32_t add_residual;
+  const void* m;
+  const float* mask;
+  const float* ln_w;
+  const float* ln_b;
+  const void* w_12;
+  const void* w_out;
+  const float* b_out;
+  float ln_eps;
+  float eps;
+  void* out;
+  void* workspace;
+  uint64_t workspace_bytes;
+} odde_opm_args;
+
+int odde_opm_workspace_bytes(const odde_opm_args* args, uint64_t* bytes);
+int odde_opm_fwd(const odde_opm_args* args, void* hip_stream);
 
 /* Instrumentation (no counterpart in the reference): per-kernel launch
  * counters (always on), and optional HIP-event timing of every launch on the

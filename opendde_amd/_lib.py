@@ -26,11 +26,13 @@ K_TRIMUL_PROJ, K_TRIMUL_CONTRACT, K_TRIMUL_OUT = 3, 4, 5
 K_TRIATT_RELAYOUT = 6
 K_TRANSITION = 7
 K_LAYER_NORM, K_LAYER_NORM_BWD = 8, 9
+K_OPM = 10
 KERNEL_NAMES = {
     K_TRIATT_PROJ: "triatt_proj", K_TRIATT_CORE: "triatt_core", K_TRIATT_OUT: "triatt_out",
     K_TRIMUL_PROJ: "trimul_proj", K_TRIMUL_CONTRACT: "trimul_contract",
     K_TRIMUL_OUT: "trimul_out", K_TRIATT_RELAYOUT: "triatt_relayout",
     K_TRANSITION: "transition", K_LAYER_NORM: "layer_norm", K_LAYER_NORM_BWD: "layer_norm_bwd",
+    K_OPM: "outer_product_mean",
 }
 
 _i32, _i64, _u32, _u64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
@@ -108,6 +110,17 @@ class LayerNormBwdArgs(ctypes.Structure):
     ]
 
 
+class OpmArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", _u32), ("n_seq", _i32), ("n_res", _i32), ("c_m", _i32),
+        ("c_hidden", _i32), ("c_z", _i32), ("m_dtype", _i32), ("out_dtype", _i32),
+        ("compute_dtype", _i32), ("add_residual", _i32),
+        ("m", _vp), ("mask", _vp), ("ln_w", _vp), ("ln_b", _vp), ("w_12", _vp), ("w_out", _vp),
+        ("b_out", _vp), ("ln_eps", _f32), ("eps", _f32), ("out", _vp),
+        ("workspace", _vp), ("workspace_bytes", _u64),
+    ]
+
+
 # Every symbol include/opendde_amd.h declares, with its ctypes signature.
 SYMBOLS = {
     "odde_abi_version": (_i32, []),
@@ -125,6 +138,8 @@ SYMBOLS = {
     "odde_layer_norm_bwd_workspace_bytes": (_i32, [ctypes.POINTER(LayerNormBwdArgs),
                                                    ctypes.POINTER(_u64)]),
     "odde_layer_norm_bwd": (_i32, [ctypes.POINTER(LayerNormBwdArgs), _vp]),
+    "odde_opm_workspace_bytes": (_i32, [ctypes.POINTER(OpmArgs), ctypes.POINTER(_u64)]),
+    "odde_opm_fwd": (_i32, [ctypes.POINTER(OpmArgs), _vp]),
     "odde_launch_count": (_i64, [_i32]),
     "odde_timing_enable": (_i32, [_i32]),
     "odde_timing_reset": (_i32, []),

@@ -350,3 +350,59 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     _lib.check(lib.odde_transition_fwd(ctypes.byref(a), _stream(x.device)),
                "odde_transition_fwd")
     return out
+
+
+OPM_C_M = (32, 64, 128)
+OPM_C_Z = (64, 128, 256, 384)
+
+
+def outer_product_mean(m: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, ln_b, w_1, w_2,
+                       w_out, b_out=None, out: Optional[torch.Tensor] = None,
+                       add_residual: bool = False, out_dtype: Optional[torch.dtype] = None,
+                       ln_eps: float = 1e-5, eps: float = 1e-3) -> torch.Tensor:
+    """OuterProductMean update of an MSA ``m`` [S, N, c_m] (bf16 arithmetic):
+    ``(W_out outer(LN(m)) + b_out) / (mask^T mask + eps)`` as [N, N, c_z],
+    rounded to bf16; written to ``out`` (``out += update`` with
+    ``add_residual``, the MSA module's ``z = z + opm_update``).  ``mask``:
+    [S, N] or None (all ones)."""
+    _require_gpu(m, mask)
+    if m.dim() != 3 or not m.is_contiguous():
+        raise ValueError("m must be a contiguous [S, N, c_m] tensor")
+    S, N, c_m = m.shape
+    c, c_z = w_1.shape[0], w_out.shape[0]
+    if c != 32 or c_m not in OPM_C_M or c_z not in OPM_C_Z or w_out.shape[1] != c * c:
+        raise NotImplementedError(
+            f"HIP outer product mean supports c_hidden = 32, c_m in {OPM_C_M}, c_z in {OPM_C_Z}")
+    if out is None:
+        if add_residual:
+            raise ValueError("add_residual needs out (the pair tensor)")
+        out = torch.empty((N, N, c_z), dtype=out_dtype or torch.bfloat16, device=m.device)
+    if not out.is_contiguous() or tuple(out.shape) != (N, N, c_z):
+        raise ValueError(f"out must be a contiguous [{N}, {N}, {c_z}] tensor")
+    mk = None
+    if mask is not None:
+        if tuple(mask.shape) != (S, N):
+            raise ValueError(f"mask must be [S, N] = [{S}, {N}], got {tuple(mask.shape)}")
+        mk = mask.to(torch.float32).contiguous()
+    f32, bf = torch.float32, torch.bfloat16
+    keep = [prepared(ln_w, f32), prepared(ln_b, f32), prepared_cat((w_1, w_2), bf),
+            prepared(w_out, bf)]
+    if b_out is not None:
+        keep.append(prepared(b_out, f32))
+    a = _lib.OpmArgs()
+    a.struct_size = ctypes.sizeof(_lib.OpmArgs)
+    a.n_seq, a.n_res, a.c_m, a.c_hidden, a.c_z = S, N, c_m, c, c_z
+    a.m_dtype, a.out_dtype, a.compute_dtype = dtype_code(m.dtype), dtype_code(out.dtype), _lib.BF16
+    a.add_residual = 1 if add_residual else 0
+    a.m, a.mask, a.out = _ptr(m), _ptr(mk), _ptr(out)
+    a.ln_w, a.ln_b, a.w_12, a.w_out = (_ptr(t) for t in keep[:4])
+    a.b_out = _ptr(keep[4]) if b_out is not None else None
+    a.ln_eps, a.eps = float(ln_eps), float(eps)
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    _lib.check(lib.odde_opm_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)),
+               "odde_opm_workspace_bytes")
+    ws = _workspace(nb.value, m.device)
+    a.workspace, a.workspace_bytes = _ptr(ws), ws.numel()
+    _lib.check(lib.odde_opm_fwd(ctypes.byref(a), _stream(m.device)), "odde_opm_fwd")
+    return out

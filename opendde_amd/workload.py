@@ -104,6 +104,18 @@ def transition_specs(c: int, n: int = 4, prefix: str = ""):
     ]
 
 
+def opm_specs(c_m: int, c: int, c_z: int, prefix: str = ""):
+    """OuterProductMean(c_m, c_z, c_hidden=c) parameters (the reference's
+    OpenfoldLinear defaults: linear_1 / linear_2 built with bias=False,
+    linear_out with a bias; triangular/layers.py:518-521)."""
+    return [
+        (prefix + "layer_norm.weight", (c_m,)), (prefix + "layer_norm.bias", (c_m,)),
+        (prefix + "linear_1.weight", (c, c_m)),
+        (prefix + "linear_2.weight", (c, c_m)),
+        (prefix + "linear_out.weight", (c_z, c * c)), (prefix + "linear_out.bias", (c_z,)),
+    ]
+
+
 def apb_specs(c_s: int, c_z: int, n_heads: int, prefix: str = ""):
     return [
         (prefix + "layernorm_a.weight", (c_s,)), (prefix + "layernorm_a.bias", (c_s,)),

@@ -15,6 +15,7 @@ Reference files followed (paths relative to the reference root):
   opendde/model/modules/primitives.py     Transition, primitives Attention, _attention
   opendde/model/modules/transformer.py    AttentionPairBias
   opendde/model/modules/pairformer.py     PairformerBlock, PairformerStack
+  opendde/model/triangular/layers.py      OuterProductMean (MSA -> pair update)
   opendde/model/utils.py                  chunk_layer (numerically neutral row chunking)
 """
 
@@ -54,6 +55,8 @@ PINNED_BY = {
     "attention_pair_bias": "float64 brute force; SDPA library routine",
     "pairformer_block": "float64 brute force composition; in-place == out-of-place",
     "pairformer_stack": "== sequential pairformer_block",
+    "outer_product_mean": "float64 brute force (loops over s, c1, c2); mask=None -> "
+    "norm S + eps; a fully masked MSA row == that row removed",
 }
 
 
@@ -447,6 +450,43 @@ def pairformer_stack(s, z, mask, p: Params, n_blocks: int, **kw):
     for b in range(n_blocks):
         s, z = pairformer_block(s, z, mask, _sub(p, f"blocks.{b}."), **kw)
     return s, z
+
+
+# ---------------------------------------------------------------------------
+# MSA -> pair: OuterProductMean
+# ---------------------------------------------------------------------------
+
+OPM_EPS = 1e-3  # OuterProductMean(eps=1e-3), triangular/layers.py:512
+
+
+def outer_product_mean(m: torch.Tensor, mask: Optional[torch.Tensor], p: Params,
+                       eps: float = OPM_EPS) -> torch.Tensor:
+    """OuterProductMean update for an MSA ``m`` [S, N, c_m] (mask [S, N] or
+    None = all ones): returns [N, N, c_z].
+
+    Follows OuterProductMean._forward / _opm (triangular/layers.py:525-616):
+    y = LN(m); a = (W_1 y) * mask; b = (W_2 y) * mask;
+    outer[i, j, c1, c2] = sum_s a[s, i, c1] b[s, j, c2], flattened c1-major;
+    out = W_out outer + b_out; out /= (sum_s mask[s, i] mask[s, j] + eps).
+    Its chunking over i (_chunk, :539-566) is numerically neutral and not
+    restated.
+    """
+    if mask is None:
+        mask = m.new_ones(m.shape[:-1])
+    y = _ln(m, p, "layer_norm")
+    mk = mask.to(m.dtype).unsqueeze(-1)
+    a = linear(y, p["linear_1.weight"], p.get("linear_1.bias")) * mk
+    b = linear(y, p["linear_2.weight"], p.get("linear_2.bias")) * mk
+    outer = torch.einsum("sic,sjd->ijcd", a, b)
+    outer = outer.reshape(outer.shape[:-2] + (-1,))
+    out = linear(outer, p["linear_out.weight"], p.get("linear_out.bias"))
+    norm = torch.einsum("si,sj->ij", mask.to(m.dtype), mask.to(m.dtype)) + eps
+    return out / norm.unsqueeze(-1)
+
+
+def flops_outer_product_mean(s: int, n: int, c_m: int, c: int, c_z: int) -> float:
+    """Projections 2*S*N*c_m*2c, outer product 2*S*N^2*c^2, W_out 2*N^2*c^2*c_z."""
+    return 2.0 * s * n * c_m * 2 * c + 2.0 * s * n * n * c * c + 2.0 * n * n * c * c * c_z
 
 
 # ---------------------------------------------------------------------------

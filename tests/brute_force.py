@@ -195,6 +195,43 @@ def transition(x, p):
     return out.reshape(x.shape[:-1] + (out.shape[-1],))
 
 
+def outer_product_mean(m, mask, p, eps=1e-3):
+    """Alg. 9 (AF3) / Alg. 10 (AF2) OuterProductMean, one output element at a
+    time: y[s,i] = LN(m[s,i]); a[s,i,c] = mask[s,i] (W1 y[s,i])[c] (+ b1);
+    b likewise; o[i,j,c1,c2] = sum_s a[s,i,c1] b[s,j,c2];
+    out[i,j,z] = (sum_{c1,c2} Wout[z][c1*C+c2] o[i,j,c1,c2] + bout[z])
+                 / (sum_s mask[s,i] mask[s,j] + eps)."""
+    m = _np(m)
+    S, N, _ = m.shape
+    mk = np.ones((S, N)) if mask is None else _np(mask)
+    P = {k: _np(v) for k, v in p.items()}
+    W1, W2, Wo = P["linear_1.weight"], P["linear_2.weight"], P["linear_out.weight"]
+    C = W1.shape[0]
+    a = np.zeros((S, N, C))
+    b = np.zeros((S, N, C))
+    for s in range(S):
+        for i in range(N):
+            y = ln_vec(list(m[s, i]), P["layer_norm.weight"], P["layer_norm.bias"])
+            av, bv = matvec(W1, y), matvec(W2, y)
+            for c in range(C):
+                a[s, i, c] = mk[s, i] * (av[c] + (P["linear_1.bias"][c] if "linear_1.bias" in P else 0.0))
+                b[s, i, c] = mk[s, i] * (bv[c] + (P["linear_2.bias"][c] if "linear_2.bias" in P else 0.0))
+    out = np.zeros((N, N, Wo.shape[0]))
+    for i in range(N):
+        for j in range(N):
+            norm = sum(mk[s, i] * mk[s, j] for s in range(S)) + eps
+            for zc in range(Wo.shape[0]):
+                acc = 0.0
+                for c1 in range(C):
+                    for c2 in range(C):
+                        o = sum(a[s, i, c1] * b[s, j, c2] for s in range(S))
+                        acc += Wo[zc][c1 * C + c2] * o
+                if "linear_out.bias" in P:
+                    acc += P["linear_out.bias"][zc]
+                out[i, j, zc] = acc / norm
+    return out
+
+
 def attention_pair_bias(s, z, p, n_heads):
     """Alg. 24 (has_s=False): a = LN(s); bias_h[i,j] = Wz LN(z[i,j]);
     out[i] = Wo( concat_h sig(Wg a[i]) * softmax_j(q_h[i].k_h[j]/sqrt(dh) + bias_h[i,j]) v_h[j] ),

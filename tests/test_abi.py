@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol():
                                         ("odde_trimul_args", _lib.TrimulArgs),
                                         ("odde_transition_args", _lib.TransitionArgs),
                                         ("odde_layer_norm_args", _lib.LayerNormArgs),
-                                        ("odde_layer_norm_bwd_args", _lib.LayerNormBwdArgs)])
+                                        ("odde_layer_norm_bwd_args", _lib.LayerNormBwdArgs),
+                                        ("odde_opm_args", _lib.OpmArgs)])
 def test_struct_layout_matches_header(cname, pyty):
     fields = [f for f, _ in pyty._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
@@ -135,3 +136,31 @@ def test_loader_caches_failure(monkeypatch):
         _lib.load()
     _lib.reset_loader_for_tests()
     assert _lib.load() is not None
+
+
+def _opm_args(S=100, N=70, c_m=64, c=32, c_z=128, mask=True):
+    a = _lib.OpmArgs()
+    a.struct_size = ctypes.sizeof(_lib.OpmArgs)
+    a.n_seq, a.n_res, a.c_m, a.c_hidden, a.c_z = S, N, c_m, c, c_z
+    a.m_dtype = a.out_dtype = a.compute_dtype = _lib.BF16
+    a.mask = ctypes.c_void_p(256) if mask else None
+    return a
+
+
+def test_opm_workspace_query_and_limits():
+    """a and b transposed (rows padded to 64 residues, 64 MSA rows) plus the
+    transposed f32 mask when one is given; unsupported sizes return -2."""
+    lib = _lib.load()
+    nb = ctypes.c_uint64(0)
+    assert lib.odde_opm_workspace_bytes(ctypes.byref(_opm_args()), ctypes.byref(nb)) == 0
+    np_, sp = 128, 128
+    assert nb.value >= 2 * np_ * 32 * sp * 2 + np_ * sp * 4
+    nb2 = ctypes.c_uint64(0)
+    assert lib.odde_opm_workspace_bytes(ctypes.byref(_opm_args(mask=False)), ctypes.byref(nb2)) == 0
+    assert nb2.value < nb.value
+    for kw in (dict(c=16), dict(c_m=48), dict(c_z=96)):
+        rc = lib.odde_opm_workspace_bytes(ctypes.byref(_opm_args(**kw)), ctypes.byref(nb))
+        assert rc == -2, kw
+        assert "outer_product_mean" in lib.odde_last_error().decode()
+    rc, msg = _status("odde_opm_fwd", _opm_args())
+    assert rc == -1 and "null tensor pointer" in msg

@@ -206,3 +206,20 @@ def test_module_torch_paths_match_oracle():
         atol=1e-5, rtol=1e-5)
     tr = seeded(Transition(32, 4), 7, 0.1)
     torch.testing.assert_close(tr(z), ref.transition(z, params_of(tr)), atol=1e-5, rtol=1e-5)
+
+
+def test_outer_product_mean_module_torch_path_matches_oracle():
+    """The module's torch path (the reference's math, used on CPU tensors)
+    equals the oracle, with and without a mask and with row chunking."""
+    from opendde_amd.outer_product_mean import OuterProductMean
+    mod = seeded(OuterProductMean(16, 24, 32), 5, 0.1).double()
+    g = torch.Generator().manual_seed(6)
+    m = torch.randn(7, 9, 16, generator=g, dtype=torch.float64)
+    mask = (torch.rand(7, 9, generator=g) > 0.3).double()
+    p = {k: v for k, v in mod.named_parameters()}
+    for mk in (mask, None):
+        exp = ref.outer_product_mean(m, mk, p)
+        torch.testing.assert_close(mod(m, mk), exp, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(mod(m, mk, chunk_size=4), exp, rtol=1e-12, atol=1e-12)
+    with pytest.raises(ValueError):
+        mod(m, mask, kernel="triton")

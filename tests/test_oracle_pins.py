@@ -229,6 +229,45 @@ def test_attention_pair_bias_brute_force():
                                bf.attention_pair_bias(s, z, p, nh), rtol=1e-9, atol=1e-9)
 
 
+def _opm_inputs(S, N, c_m, seed, p_drop=0.3):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.randn(S, N, c_m, generator=g, dtype=D64)
+    mask = (torch.rand((S, N), generator=g) > p_drop).to(D64)
+    return m, mask
+
+
+def test_outer_product_mean_brute_force():
+    S, N, c_m, c, c_z = 4, 5, 8, 3, 5
+    p = _params(wl.opm_specs(c_m, c, c_z), 32)
+    m, mask = _opm_inputs(S, N, c_m, 16)
+    for mk in (mask, None):
+        np.testing.assert_allclose(ref.outer_product_mean(m, mk, p).numpy(),
+                                   bf.outer_product_mean(m, mk, p), rtol=1e-10, atol=1e-10)
+
+
+def test_outer_product_mean_special_cases():
+    S, N, c_m, c, c_z = 6, 4, 8, 3, 4
+    p = _params(wl.opm_specs(c_m, c, c_z), 33)
+    m, mask = _opm_inputs(S, N, c_m, 17)
+    # no mask: every pair's norm is S + eps, so the update is (W_out outer + b) / (S + eps)
+    ones = torch.ones(S, N, dtype=D64)
+    full = ref.outer_product_mean(m, ones, p)
+    torch.testing.assert_close(ref.outer_product_mean(m, None, p), full, rtol=0, atol=0)
+    y = ref.layer_norm(m, p["layer_norm.weight"], p["layer_norm.bias"])
+    a = y @ p["linear_1.weight"].T
+    b = y @ p["linear_2.weight"].T
+    outer = torch.einsum("sic,sjd->ijcd", a, b).reshape(N, N, c * c)
+    expect = (outer @ p["linear_out.weight"].T + p["linear_out.bias"]) / (S + ref.OPM_EPS)
+    torch.testing.assert_close(full, expect, rtol=1e-12, atol=1e-12)
+    # a fully masked MSA row contributes nothing: same as dropping it
+    mask2 = mask.clone()
+    mask2[2] = 0.0
+    keep = [s for s in range(S) if s != 2]
+    torch.testing.assert_close(ref.outer_product_mean(m, mask2, p),
+                               ref.outer_product_mean(m[keep], mask2[keep], p),
+                               rtol=1e-12, atol=1e-12)
+
+
 def _small_block(seed, c_s=8):
     dims = dict(c_z=8, c_s=c_s, h=2, d=4, ch=6, n_heads=2)
     return _params(wl.block_specs(**dims), seed), dims
