@@ -11,7 +11,9 @@
 //    the two projections on MFMA, then the 64 x 64 result goes through LDS so
 //    that a and b are stored transposed, s innermost: At[i * 32 + c][s],
 //    Bt[j * 32 + c][s] (bf16, rows padded to Sp = S rounded up to 64 with
-//    zeros).  The mask is stored transposed as f32 maskT[i][s] when given.
+//    zeros).  The mask is stored transposed as bf16 maskT[i][s] when given,
+//    and opm_norm forms norm[i][j] = sum_s maskT[i][s] maskT[j][s] + eps on
+//    the same GEMM mainloop (exact for 0/1 masks).
 // 2. opm_outer: one workgroup per (8 residues i) x (4 residues j): the NT
 //    GEMM mainloop (gemm.hpp) over k = s gives the 256 x 128 block of
 //    outer products (32 residue pairs, each a 32 x 32 block); the block is
@@ -28,12 +30,26 @@ namespace odde {
 
 constexpr int kOpmC = 32;     // c_hidden
 constexpr int kOpmSB = 64;    // MSA rows per projection workgroup (and the S padding)
-constexpr int kOpmTI = 8;     // residues i per outer workgroup (256 GEMM rows)
-constexpr int kOpmTJ = 4;     // residues j per outer workgroup (128 GEMM rows)
-constexpr int kOpmNS = 3;     // mainloop stages
-constexpr int kOpmPairs = kOpmTI * kOpmTJ;
 constexpr int kOpmPP = kOpmC * kOpmC + 8;  // LDS pitch of one pair's block (bf16)
-using OpmShape = GemmShape<kOpmTI * kOpmC, kOpmTJ * kOpmC, 4>;
+
+// Outer-product workgroup tile: TI residues i x TJ residues j (GEMM rows
+// 32 TI x 32 TJ), WX waves along i, NS stages of KC MSA rows.
+template <int TI_, int TJ_, int WX_, int NS_, int KC_>
+struct OpmTile {
+  static constexpr int TI = TI_, TJ = TJ_, WX = WX_, NS = NS_, KC = KC_;
+  static constexpr int PAIRS = TI * TJ;
+  using Shape = GemmShape<TI * kOpmC, TJ * kOpmC, WX, KC>;
+  static constexpr int MAIN_BYTES = NS * Shape::STAGE_ELEMS * 2;
+  static constexpr int EPI_BYTES = PAIRS * kOpmPP * 2;
+  static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+  static constexpr int PT = PAIRS / 16;  // 16-pair tiles of the projection
+};
+// 256 x 256 GEMM tiles staged 64 MSA rows at a time (whole 128-byte lines),
+// one workgroup per CU; the 64 pairs' blocks reuse the stage buffers.
+using OpmTileBig = OpmTile<8, 8, 2, 2, 64>;
+// 256 x 128 GEMM tiles staged 32 MSA rows at a time, two workgroups per CU.
+using OpmTileSmall = OpmTile<8, 4, 4, 3, 32>;
+using OpmTileUsed = OpmTileSmall;
 
 struct OpmProjArgs {
   const void* m;
@@ -43,7 +59,7 @@ struct OpmProjArgs {
   const bf16* w12;    // [64][c_m]: W_1 rows then W_2 rows
   bf16* at;           // [Np * 32][Sp]
   bf16* bt;
-  float* maskt;       // [Np][Sp] or null
+  bf16* maskt;        // [Np][Sp] or null
   int S, N, Sp;
   float eps;
 };
@@ -87,7 +103,7 @@ __global__ __launch_bounds__(256) void opm_proj_kernel(OpmProjArgs a) {
   if (a.maskt && threadIdx.x < kOpmSB) {
     const int sr = s0 + threadIdx.x;
     a.maskt[(size_t)i * a.Sp + sr] =
-        (sr < a.S && i < a.N) ? (a.mask ? a.mask[(size_t)sr * a.N + i] : 1.f) : 0.f;
+        (bf16)((sr < a.S && i < a.N) ? (a.mask ? a.mask[(size_t)sr * a.N + i] : 1.f) : 0.f);
   }
   __syncthreads();
   // 64 output rows of 64 MSA rows (128 bytes each): 512 chunks of 16 bytes
@@ -100,10 +116,36 @@ __global__ __launch_bounds__(256) void opm_proj_kernel(OpmProjArgs a) {
   }
 }
 
+// norm[i][j] = sum_s maskT[i][s] maskT[j][s] + eps over 128 x 128 tiles
+// (grid (Np / 128)^2, 512 threads).
+__global__ __launch_bounds__(512) void opm_norm_kernel(const bf16* __restrict__ maskt, int Np, int Sp,
+                                                       float eps, float* __restrict__ norm) {
+  using S = GemmShape<128, 128, 2>;
+  __shared__ __attribute__((aligned(16))) bf16 sm[3 * S::STAGE_ELEMS];
+  const int nt = Np / 128, ti = blockIdx.x / nt, tj = blockIdx.x % nt;
+  const bf16* A = maskt + (size_t)ti * 128 * Sp;
+  const bf16* B = maskt + (size_t)tj * 128 * Sp;
+  f32x4 acc[S::MX][S::MY];
+  gemm_nt_mainloop<128, 128, 2, 3, true>([&](int r) { return A + (size_t)r * Sp; },
+                                         [&](int r) { return B + (size_t)r * Sp; }, Sp, sm, acc);
+  // acc[mi][mj]: column (lane % 16) = row i, values = 4 consecutive j
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % 2, wy = w / 2;
+#pragma unroll
+  for (int mi = 0; mi < S::MX; ++mi)
+#pragma unroll
+    for (int mj = 0; mj < S::MY; ++mj) {
+      const int i = ti * 128 + wx * 64 + 16 * mi + r16;
+      const int j = tj * 128 + wy * 32 + 16 * mj + 4 * g;
+      store4(norm + (size_t)i * Np + j, acc[mi][mj][0] + eps, acc[mi][mj][1] + eps,
+             acc[mi][mj][2] + eps, acc[mi][mj][3] + eps);
+    }
+}
+
 struct OpmOuterArgs {
   const bf16* at;
   const bf16* bt;
-  const float* maskt;  // [Np][Sp] or null (all ones: norm = S + eps)
+  const float* norm;   // [Np][Np] or null (all ones: norm = S + eps)
   const bf16* w_out;   // [c_z][1024]
   const float* b_out;  // [c_z] or null
   void* out;           // [N][N][c_z]
@@ -128,100 +170,101 @@ __device__ __forceinline__ void opm_tile_map(int L, int nti, int ntj, int& ti, i
   tj = (band % bpr) * 8 + (w & 7);
 }
 
-template <typename OT, int CZ>
+template <typename OT, int CZ, typename TL>
 __global__ __launch_bounds__(512) void opm_outer_kernel(OpmOuterArgs a) {
-  static_assert(kOpmPairs * kOpmPP * 2 + kOpmPairs * 4 <= kOpmNS * OpmShape::STAGE_ELEMS * 2,
-                "the pair blocks and norms fit in the mainloop's LDS");
-  constexpr int NU = CZ / 64;  // 16-wide z tiles per wave
-  __shared__ __attribute__((aligned(16))) bf16 sm[kOpmNS * OpmShape::STAGE_ELEMS];
+  using S = typename TL::Shape;
+  constexpr int TI = TL::TI, TJ = TL::TJ, PAIRS = TL::PAIRS;
+  constexpr int RI = S::MX / 2, RJ = S::MY / 2;  // residues per wave along i, j
+  // projection split over the 8 waves: WZ along the CZ / 16 z tiles, WP along
+  // the PT 16-pair tiles
+  constexpr int ZT = CZ / 16, PT = TL::PT;
+  constexpr int WZ = ZT < 8 ? ZT : 8, WP = 8 / WZ;
+  constexpr int NU = ZT / WZ, NV = PT / WP;
+  static_assert(ZT % WZ == 0 && PT % WP == 0 && 8 % WZ == 0, "projection tiles split evenly");
+  __shared__ __attribute__((aligned(16))) bf16 sm[TL::LDS_BYTES / 2];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   int ti, tj;
-  opm_tile_map(blockIdx.x, a.Np / kOpmTI, a.Np / kOpmTJ, ti, tj);
-  const bf16* A = a.at + (size_t)ti * kOpmTI * kOpmC * a.Sp;
-  const bf16* B = a.bt + (size_t)tj * kOpmTJ * kOpmC * a.Sp;
-  f32x4 acc[OpmShape::MX][OpmShape::MY];
-  gemm_nt_mainloop<kOpmTI * kOpmC, kOpmTJ * kOpmC, 4, kOpmNS, true>(
+  opm_tile_map(blockIdx.x, a.Np / TI, a.Np / TJ, ti, tj);
+  const bf16* A = a.at + (size_t)ti * TI * kOpmC * a.Sp;
+  const bf16* B = a.bt + (size_t)tj * TJ * kOpmC * a.Sp;
+  f32x4 acc[S::MX][S::MY];
+  gemm_nt_mainloop<TI * kOpmC, TJ * kOpmC, TL::WX, TL::NS, true, TL::KC>(
       [&](int r) { return A + (size_t)r * a.Sp; }, [&](int r) { return B + (size_t)r * a.Sp; },
       a.Sp, sm, acc);
-  // acc[mi][mj]: column (lane % 16) = A row 64 wx + 16 mi + r16 (residue
-  // 2 wx + mi / 2, c1 = 16 (mi % 2) + r16); values e = B rows
-  // 64 wy + 16 mj + 4 g + e (residue 2 wy + mj / 2, c2 = 16 (mj % 2) + 4 g + e)
-  const int wx = w & 3, wy = w >> 2;
+  // acc[mi][mj]: column (lane % 16) = A row 32 RI wx + 16 mi + r16 (residue
+  // RI wx + mi / 2, c1 = 16 (mi % 2) + r16); values e = B rows
+  // 32 RJ wy + 16 mj + 4 g + e (residue RJ wy + mj / 2, c2 = 16 (mj % 2) + 4 g + e)
+  const int wx = w % TL::WX, wy = w / TL::WX;
   bf16* P = sm;
-  float* normv = reinterpret_cast<float*>(sm + kOpmPairs * kOpmPP);
 #pragma unroll
-  for (int mi = 0; mi < OpmShape::MX; ++mi)
+  for (int mi = 0; mi < S::MX; ++mi)
 #pragma unroll
-    for (int mj = 0; mj < OpmShape::MY; ++mj) {
-      const int pair = (2 * wx + mi / 2) * kOpmTJ + 2 * wy + mj / 2;
+    for (int mj = 0; mj < S::MY; ++mj) {
+      const int pair = (RI * wx + mi / 2) * TJ + RJ * wy + mj / 2;
       const int c1 = 16 * (mi & 1) + r16, c2 = 16 * (mj & 1) + 4 * g;
       bf16x4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = (bf16)acc[mi][mj][e];
       *reinterpret_cast<bf16x4*>(&P[pair * kOpmPP + c1 * kOpmC + c2]) = v;
     }
-  // norm[pair] = sum_s maskT[i][s] maskT[j][s] + eps: 16 lanes per pair
-  {
-    const int pair = threadIdx.x >> 4, part = threadIdx.x & 15;
-    const int i = ti * kOpmTI + pair / kOpmTJ, j = tj * kOpmTJ + pair % kOpmTJ;
-    float sum = 0.f;
-    if (a.maskt) {
-      const float* mi_ = a.maskt + (size_t)i * a.Sp;
-      const float* mj_ = a.maskt + (size_t)j * a.Sp;
-      for (int s = part; s < a.S; s += 16) sum += mi_[s] * mj_[s];
-    } else if (part == 0) {
-      sum = (float)a.S;
-    }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    if (part == 0) normv[pair] = sum + a.eps;
-  }
   __syncthreads();
-  // out[pair][z] = sum_k P[pair][k] W_out[z][k]: wave w takes pairs
-  // 16 (w & 1) .. + 15 and z tiles (w >> 1) + 4 u
-  const int pt = w & 1;
-  f32x4 acc2[NU];
+  // out[pair][z] = sum_k P[pair][k] W_out[z][k]: WZ waves along z, WP
+  // along pairs; wave w takes z tiles w % WZ + WZ u and pair tiles
+  // w / WZ + WP v, so each W_out fragment read from memory serves NV pair
+  // tiles (with c_z >= 128 every W_out row is read once per workgroup)
+  const int zw = w % WZ, pw = w / WZ;
+  f32x4 acc2[NU][NV];
 #pragma unroll
-  for (int u = 0; u < NU; ++u) acc2[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16* prow = P + (16 * pt + r16) * kOpmPP + 8 * g;
-#pragma unroll 4
+  for (int u = 0; u < NU; ++u)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc2[u][v] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bf16* wrow[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+    wrow[u] = a.w_out + (size_t)(16 * (zw + WZ * u) + r16) * (kOpmC * kOpmC) + 8 * g;
+#pragma unroll 8
   for (int ks = 0; ks < kOpmC; ++ks) {
-    Frag<bf16> pf;
-    pf.load(prow + ks * kOpmC);
+    Frag<bf16> wf[NU], pf[NV];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) wf[u].load(wrow[u] + ks * kOpmC);
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      pf[v].load(P + (16 * (pw + WP * v) + r16) * kOpmPP + 8 * g + ks * kOpmC);
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) mma(acc2[u][v], wf[u], pf[v]);  // D[z 4g + r][pair l % 16]
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int pair = 16 * (pw + WP * v) + r16;
+    const int i = ti * TI + pair / TJ, j = tj * TJ + pair % TJ;
+    if (i >= a.N || j >= a.N) continue;
+    const float inv = 1.0f / (a.norm ? a.norm[(size_t)i * a.Np + j] : (float)a.S + a.eps);
+    OT* dst = static_cast<OT*>(a.out) + ((size_t)i * a.N + j) * CZ;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-      Frag<bf16> wf;
-      wf.load(a.w_out + (size_t)(16 * ((w >> 1) + 4 * u) + r16) * (kOpmC * kOpmC) + ks * kOpmC + 8 * g);
-      mma(acc2[u], wf, pf);  // D[row = z 4g + r][col = pair l % 16]
-    }
-  }
-  const int pair = 16 * pt + r16;
-  const int i = ti * kOpmTI + pair / kOpmTJ, j = tj * kOpmTJ + pair % kOpmTJ;
-  if (i >= a.N || j >= a.N) return;
-  const float inv = 1.0f / normv[pair];
-  OT* dst = static_cast<OT*>(a.out) + ((size_t)i * a.N + j) * CZ;
+      const int z0 = 16 * (zw + WZ * u) + 4 * g;
+      float o[4];
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int z0 = 16 * ((w >> 1) + 4 * u) + 4 * g;
-    float v[4];
+      for (int r = 0; r < 4; ++r) {
+        const float bo = a.b_out ? a.b_out[z0 + r] : 0.f;
+        o[r] = round_to<bf16>((acc2[u][v][r] + bo) * inv);
+      }
+      if (a.add) {
+        float zr[4];
+        load4(dst + z0, zr);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float bo = a.b_out ? a.b_out[z0 + r] : 0.f;
-      v[r] = round_to<bf16>((acc2[u][r] + bo) * inv);
+        for (int r = 0; r < 4; ++r) o[r] += zr[r];
+      }
+      store4(dst + z0, o[0], o[1], o[2], o[3]);
     }
-    if (a.add) {
-      float zr[4];
-      load4(dst + z0, zr);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] += zr[r];
-    }
-    store4(dst + z0, v[0], v[1], v[2], v[3]);
   }
 }
 
 namespace {
 
-int opm_np(int n) { return round_up(n, 64); }
+int opm_np(int n) { return round_up(n, 128); }
 int opm_sp(int s) { return round_up(s, kOpmSB); }
 
 uint64_t opm_ws_bytes(const odde_opm_args* a) {
@@ -229,7 +272,10 @@ uint64_t opm_ws_bytes(const odde_opm_args* a) {
   Carver c(nullptr, 0);
   c.take<bf16>(np * kOpmC * sp);
   c.take<bf16>(np * kOpmC * sp);
-  if (a->mask) c.take<float>(np * sp);
+  if (a->mask) {
+    c.take<bf16>(np * sp);
+    c.take<float>(np * np);
+  }
   return c.used;
 }
 
@@ -239,7 +285,8 @@ int run_opm(const odde_opm_args* a, hipStream_t st) {
   Carver c(a->workspace, a->workspace_bytes);
   bf16* at = c.take<bf16>((uint64_t)Np * kOpmC * Sp);
   bf16* bt = c.take<bf16>((uint64_t)Np * kOpmC * Sp);
-  float* maskt = a->mask ? c.take<float>((uint64_t)Np * Sp) : nullptr;
+  bf16* maskt = a->mask ? c.take<bf16>((uint64_t)Np * Sp) : nullptr;
+  float* norm = a->mask ? c.take<float>((uint64_t)Np * Np) : nullptr;
   LaunchScope ls(ODDE_K_OPM, st);
   if (S > 0) {  // with no MSA rows the outer products are empty: update = b_out / eps
     OpmProjArgs p;
@@ -257,18 +304,26 @@ int run_opm(const odde_opm_args* a, hipStream_t st) {
     int rc = check_launch("opm_proj");
     if (rc) return rc;
   }
+  if (norm) {
+    const int nt = Np / 128;
+    hipLaunchKernelGGL(opm_norm_kernel, dim3(nt * nt), dim3(512), 0, st, maskt, Np, Sp, a->eps,
+                       norm);
+    int rc = check_launch("opm_norm");
+    if (rc) return rc;
+  }
   OpmOuterArgs q;
-  q.at = at; q.bt = bt; q.maskt = maskt;
+  q.at = at; q.bt = bt; q.norm = norm;
   q.w_out = static_cast<const bf16*>(a->w_out);
   q.b_out = a->b_out;
   q.out = a->out;
   q.S = S; q.N = N; q.Np = Np; q.Sp = Sp; q.add = a->add_residual; q.eps = a->eps;
-  const unsigned tiles = (unsigned)(Np / kOpmTI) * (unsigned)(Np / kOpmTJ);
+  using TL = OpmTileUsed;
+  const unsigned tiles = (unsigned)(Np / TL::TI) * (unsigned)(Np / TL::TJ);
   switch (a->c_z) {
-    case 64: hipLaunchKernelGGL((opm_outer_kernel<OT, 64>), dim3(tiles), dim3(512), 0, st, q); break;
-    case 128: hipLaunchKernelGGL((opm_outer_kernel<OT, 128>), dim3(tiles), dim3(512), 0, st, q); break;
-    case 256: hipLaunchKernelGGL((opm_outer_kernel<OT, 256>), dim3(tiles), dim3(512), 0, st, q); break;
-    case 384: hipLaunchKernelGGL((opm_outer_kernel<OT, 384>), dim3(tiles), dim3(512), 0, st, q); break;
+    case 64: hipLaunchKernelGGL((opm_outer_kernel<OT, 64, TL>), dim3(tiles), dim3(512), 0, st, q); break;
+    case 128: hipLaunchKernelGGL((opm_outer_kernel<OT, 128, TL>), dim3(tiles), dim3(512), 0, st, q); break;
+    case 256: hipLaunchKernelGGL((opm_outer_kernel<OT, 256, TL>), dim3(tiles), dim3(512), 0, st, q); break;
+    case 384: hipLaunchKernelGGL((opm_outer_kernel<OT, 384, TL>), dim3(tiles), dim3(512), 0, st, q); break;
     default: return set_error(ODDE_EUNSUPPORTED, "outer_product_mean: c_z in {64, 128, 256, 384}");
   }
   return check_launch("opm_outer");

@@ -148,13 +148,14 @@ def _opm_args(S=100, N=70, c_m=64, c=32, c_z=128, mask=True):
 
 
 def test_opm_workspace_query_and_limits():
-    """a and b transposed (rows padded to 64 residues, 64 MSA rows) plus the
-    transposed f32 mask when one is given; unsupported sizes return -2."""
+    """a and b transposed (rows padded to 128 residues, 64 MSA rows) plus the
+    transposed bf16 mask and the f32 norm matrix when a mask is given;
+    unsupported sizes return -2."""
     lib = _lib.load()
     nb = ctypes.c_uint64(0)
     assert lib.odde_opm_workspace_bytes(ctypes.byref(_opm_args()), ctypes.byref(nb)) == 0
     np_, sp = 128, 128
-    assert nb.value >= 2 * np_ * 32 * sp * 2 + np_ * sp * 4
+    assert nb.value >= 2 * np_ * 32 * sp * 2 + np_ * sp * 2 + np_ * np_ * 4
     nb2 = ctypes.c_uint64(0)
     assert lib.odde_opm_workspace_bytes(ctypes.byref(_opm_args(mask=False)), ctypes.byref(nb2)) == 0
     assert nb2.value < nb.value
