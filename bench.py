@@ -186,6 +186,52 @@ def layer_norm_measure(n: int, dev, reps: int = 20):
     return res
 
 
+def opm_measure(n: int, dev, s_rows: int = 1280, reps: int = 10):
+    """The MSA module's OuterProductMean (c_m 64, c_hidden 32, c_z 128; MSA
+    depth 1280, opendde/config/data.py:31) at N residues, with a random MSA
+    mask and the update added into an fp32 pair tensor, bf16 arithmetic:
+    average time of the library's launch scope (projection, mask norms,
+    fused outer product + W_out) from its HIP events; the reference's own
+    torch path on the same inputs under bf16 autocast for comparison."""
+    from opendde_amd.outer_product_mean import OuterProductMean
+    g = torch.Generator().manual_seed(6)
+    mod = OuterProductMean(64, 128, 32)
+    wl.init_module_(mod, g, 0.05)
+    mod = mod.to(dev)
+    m = torch.randn(s_rows, n, 64, generator=g).to(dev)
+    mask = (torch.rand(s_rows, n, generator=g) > 0.1).float().to(dev)
+    z = torch.randn(n, n, 128, generator=g).to(dev)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        mod.hip_apply(m, mask, out=z, add_residual=True)
+        torch.cuda.synchronize()
+        _lib.timing_reset()
+        _lib.timing_enable(True)
+        for _ in range(reps):
+            mod.hip_apply(m, mask, out=z, add_residual=True)
+        torch.cuda.synchronize()
+        _lib.timing_enable(False)
+        tot, cnt = _lib.timing_query(_lib.K_OPM)
+        _lib.timing_reset()
+        mod(m, mask, chunk_size=128)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(2):
+            mod(m, mask, chunk_size=128)
+        e1.record()
+        torch.cuda.synchronize()
+    torch_ms = e0.elapsed_time(e1) / 2
+    ms = tot / cnt
+    # projections 2*S*N*c_m*2c, outer products 2*S*N^2*c^2, W_out 2*N^2*c^2*c_z
+    fl = 2.0 * s_rows * n * 64 * 64 + 2.0 * s_rows * n * n * 32 * 32 + 2.0 * n * n * 32 * 32 * 128
+    res = {"n_seq": s_rows, "n_res": n, "c_m": 64, "c_hidden": 32, "c_z": 128, "dtype": "bf16",
+           "avg_ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1),
+           "pct_bf16_peak": round(100 * fl / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+           "torch_bf16_ms": round(torch_ms, 4)}
+    del m, mask, z
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,6 +241,8 @@ def main():
     ap.add_argument("--blocks", type=int, default=48)
     ap.add_argument("--cpu-sample-n", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-opm", action="store_true",
+                    help="skip the OuterProductMean measurement")
     ap.add_argument("--no-layer-norm", action="store_true",
                     help="skip the standalone fast-LayerNorm measurement")
     ap.add_argument("--preset", choices=["trunk", "opendde_v1"], default="trunk",
@@ -321,6 +369,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": None,
         "layer_norm": None if args.no_layer_norm else layer_norm_measure(n, dev),
+        "outer_product_mean": None if args.no_opm else opm_measure(n, dev),
     }
     if not args.no_cpu_baseline and not v1:
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_n, chunk=128)
