@@ -50,7 +50,8 @@ extern "C" {
 #define ODDE_K_LAYER_NORM 8
 #define ODDE_K_LAYER_NORM_BWD 9
 #define ODDE_K_OPM 10
-#define ODDE_K_COUNT 11
+#define ODDE_K_BIAS_ATTN 11
+#define ODDE_K_COUNT 12
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -273,6 +274,37 @@ typedef struct odde_layer_norm_bwd_args {
 int odde_layer_norm_fwd(const odde_layer_norm_args* args, void* hip_stream);
 int odde_layer_norm_bwd_workspace_bytes(const odde_layer_norm_bwd_args* args, uint64_t* bytes);
 int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* args, void* hip_stream);
+
+/*
+ * Attention with an additive bias in fp32: the core of the single track's
+ * AttentionPairBias (replaces primitives._attention, opendde/model/modules/
+ * primitives.py:220-258, which upcasts q, k, v and the bias to fp32 and runs
+ * SDPA with scale 1; called from Attention.forward, :800-857):
+ *   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
+ * q, k, v, out: element (h, i, d) at base + h*s_h + i*s_n + d (head_dim
+ * contiguous), dtype f32 or bf16 (out in the same dtype); bias: f32
+ * [heads][n_q][n_k] contiguous, or NULL.  head_dim in {8, 16, 24, 32, 48,
+ * 64}.  No workspace.
+ */
+typedef struct odde_bias_attn_args {
+  uint32_t struct_size;
+  int32_t n_q;
+  int32_t n_k;
+  int32_t heads;
+  int32_t head_dim;
+  int32_t dtype;
+  const void* q;
+  int64_t q_sh, q_sn;
+  const void* k;
+  int64_t k_sh, k_sn;
+  const void* v;
+  int64_t v_sh, v_sn;
+  const float* bias;
+  void* out;
+  int64_t o_sh, o_sn;
+} odde_bias_attn_args;
+
+int odde_bias_attn_fwd(const odde_bias_attn_args* args, void* hip_stream);
 
 /*
  * OuterProductMean, the MSA -> pair update of the MSA module (replaces

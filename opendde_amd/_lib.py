@@ -27,12 +27,13 @@ K_TRIATT_RELAYOUT = 6
 K_TRANSITION = 7
 K_LAYER_NORM, K_LAYER_NORM_BWD = 8, 9
 K_OPM = 10
+K_BIAS_ATTN = 11
 KERNEL_NAMES = {
     K_TRIATT_PROJ: "triatt_proj", K_TRIATT_CORE: "triatt_core", K_TRIATT_OUT: "triatt_out",
     K_TRIMUL_PROJ: "trimul_proj", K_TRIMUL_CONTRACT: "trimul_contract",
     K_TRIMUL_OUT: "trimul_out", K_TRIATT_RELAYOUT: "triatt_relayout",
     K_TRANSITION: "transition", K_LAYER_NORM: "layer_norm", K_LAYER_NORM_BWD: "layer_norm_bwd",
-    K_OPM: "outer_product_mean",
+    K_OPM: "outer_product_mean", K_BIAS_ATTN: "bias_attn",
 }
 
 _i32, _i64, _u32, _u64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
@@ -121,6 +122,16 @@ class OpmArgs(ctypes.Structure):
     ]
 
 
+class BiasAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", _u32), ("n_q", _i32), ("n_k", _i32), ("heads", _i32),
+        ("head_dim", _i32), ("dtype", _i32),
+        ("q", _vp), ("q_sh", _i64), ("q_sn", _i64), ("k", _vp), ("k_sh", _i64), ("k_sn", _i64),
+        ("v", _vp), ("v_sh", _i64), ("v_sn", _i64), ("bias", _vp), ("out", _vp),
+        ("o_sh", _i64), ("o_sn", _i64),
+    ]
+
+
 # Every symbol include/opendde_amd.h declares, with its ctypes signature.
 SYMBOLS = {
     "odde_abi_version": (_i32, []),
@@ -140,6 +151,7 @@ SYMBOLS = {
     "odde_layer_norm_bwd": (_i32, [ctypes.POINTER(LayerNormBwdArgs), _vp]),
     "odde_opm_workspace_bytes": (_i32, [ctypes.POINTER(OpmArgs), ctypes.POINTER(_u64)]),
     "odde_opm_fwd": (_i32, [ctypes.POINTER(OpmArgs), _vp]),
+    "odde_bias_attn_fwd": (_i32, [ctypes.POINTER(BiasAttnArgs), _vp]),
     "odde_launch_count": (_i64, [_i32]),
     "odde_timing_enable": (_i32, [_i32]),
     "odde_timing_reset": (_i32, []),

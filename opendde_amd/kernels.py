@@ -406,3 +406,43 @@ def outer_product_mean(m: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     a.workspace, a.workspace_bytes = _ptr(ws), ws.numel()
     _lib.check(lib.odde_opm_fwd(ctypes.byref(a), _stream(m.device)), "odde_opm_fwd")
     return out
+
+
+BIAS_ATTN_HEAD_DIMS = (8, 16, 24, 32, 48, 64)
+
+
+def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """fp32 attention with an additive bias, the single track's attention
+    core (primitives._attention with scale 1): q, k, v [H, N, D] (any head
+    and row strides, D contiguous; f32 or bf16), bias [H, Nq, Nk] or None.
+    Returns [H, Nq, D] in q's dtype."""
+    _require_gpu(q, k, v, bias)
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
+        raise ValueError("q, k, v must be [H, N, D] with matching k and v")
+    h, nq, d = q.shape
+    nk = k.shape[1]
+    if k.shape[0] != h or k.shape[2] != d:
+        raise ValueError("q and k disagree in heads or head dim")
+    if d not in BIAS_ATTN_HEAD_DIMS:
+        raise NotImplementedError(f"HIP bias attention supports head_dim in {BIAS_ATTN_HEAD_DIMS}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise ValueError("q, k, v need a contiguous head dim")
+    b = None
+    if bias is not None:
+        b = bias.to(torch.float32).expand(h, nq, nk).contiguous()
+    out = torch.empty((h, nq, d), dtype=q.dtype, device=q.device)
+    a = _lib.BiasAttnArgs()
+    a.struct_size = ctypes.sizeof(_lib.BiasAttnArgs)
+    a.n_q, a.n_k, a.heads, a.head_dim, a.dtype = nq, nk, h, d, dtype_code(q.dtype)
+    a.q, a.q_sh, a.q_sn = _ptr(q), q.stride(0), q.stride(1)
+    a.k, a.k_sh, a.k_sn = _ptr(k), k.stride(0), k.stride(1)
+    a.v, a.v_sh, a.v_sn = _ptr(v), v.stride(0), v.stride(1)
+    a.bias = _ptr(b)
+    a.out, a.o_sh, a.o_sn = _ptr(out), out.stride(0), out.stride(1)
+    _lib.check(_lib.load().odde_bias_attn_fwd(ctypes.byref(a), _stream(q.device)),
+               "odde_bias_attn_fwd")
+    return out

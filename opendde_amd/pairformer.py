@@ -110,15 +110,21 @@ class SingleAttention(nn.Module):
         if zero_init:
             nn.init.zeros_(self.linear_o.weight)
 
-    def forward(self, q_x, kv_x, attn_bias=None):
+    def forward(self, q_x, kv_x, attn_bias=None, hip: bool = False):
+        """``hip``: run the fp32 attention core on the HIP kernel (one
+        sequence [N, c], GPU tensors, supported head dim)."""
         def heads(t):
             return t.view(t.shape[:-1] + (self.num_heads, -1)).transpose(-2, -3)
         q = heads(self.linear_q(q_x)) / math.sqrt(self.c_hidden)
         k = heads(self.linear_k(kv_x))
         v = heads(self.linear_v(kv_x))
-        if attn_bias is not None and attn_bias.dim() != q.dim():
-            attn_bias = attn_bias.unsqueeze(-3)
-        o = _sdpa_fp32(q, k, v, attn_bias).transpose(-2, -3)
+        if (hip and q.is_cuda and q.dim() == 3 and self.c_hidden in K.BIAS_ATTN_HEAD_DIMS
+                and (attn_bias is None or attn_bias.dim() == 3)):
+            o = K.bias_attention(q, k, v, attn_bias).transpose(-2, -3)
+        else:
+            if attn_bias is not None and attn_bias.dim() != q.dim():
+                attn_bias = attn_bias.unsqueeze(-3)
+            o = _sdpa_fp32(q, k, v, attn_bias).transpose(-2, -3)
         if self.linear_g is not None:
             g = self.sigmoid(self.linear_g(q_x))
             o = o * g.view(g.shape[:-1] + (self.num_heads, -1))
@@ -154,7 +160,8 @@ class AttentionPairBias(nn.Module):
 
     def forward(self, a: torch.Tensor, s: Optional[torch.Tensor], z: torch.Tensor,
                 extra_attn_bias: Optional[torch.Tensor] = None,
-                z_bias: Optional[torch.Tensor] = None, **_unused) -> torch.Tensor:
+                z_bias: Optional[torch.Tensor] = None, hip: bool = False,
+                **_unused) -> torch.Tensor:
         """``z_bias`` ([heads, N, N]) is ``linear_nobias_z(layernorm_z(z))``
         already computed from this z (the fused transition kernel makes it
         while writing z); ``z`` is then not read."""
@@ -170,7 +177,7 @@ class AttentionPairBias(nn.Module):
             if eb.dim() == bias.dim() - 1:
                 eb = eb.unsqueeze(-3)
             bias = bias + eb.to(dtype=bias.dtype, device=bias.device)
-        return self.attention(q_x=a, kv_x=a, attn_bias=bias)
+        return self.attention(q_x=a, kv_x=a, attn_bias=bias, hip=hip)
 
 
 class PairformerBlock(nn.Module):
@@ -246,7 +253,7 @@ class PairformerBlock(nn.Module):
             z = z.add_(upd) if inplace_safe else z + upd
         if self.c_s > 0:
             s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias,
-                                             z_bias=z_bias)
+                                             z_bias=z_bias, hip=hip_mul or hip_att)
             if (hip_mul or hip_att) and self.single_transition.hip_supported(s):
                 s = self.single_transition.hip_apply(s.contiguous(), add_residual=True)
             else:

@@ -39,7 +39,8 @@ def test_library_exports_every_declared_symbol():
                                         ("odde_transition_args", _lib.TransitionArgs),
                                         ("odde_layer_norm_args", _lib.LayerNormArgs),
                                         ("odde_layer_norm_bwd_args", _lib.LayerNormBwdArgs),
-                                        ("odde_opm_args", _lib.OpmArgs)])
+                                        ("odde_opm_args", _lib.OpmArgs),
+                                        ("odde_bias_attn_args", _lib.BiasAttnArgs)])
 def test_struct_layout_matches_header(cname, pyty):
     fields = [f for f, _ in pyty._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
