@@ -282,9 +282,9 @@ int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* args, void* hip_stream);
  * SDPA with scale 1; called from Attention.forward, :800-857):
  *   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
  * q, k, v, out: element (h, i, d) at base + h*s_h + i*s_n + d (head_dim
- * contiguous), dtype f32 or bf16 (out in the same dtype); bias: f32
- * [heads][n_q][n_k] contiguous, or NULL.  head_dim in {8, 16, 24, 32, 48,
- * 64}.  No workspace.
+ * contiguous), dtype f32 or bf16 (out in the same dtype); k and v rows
+ * 16-byte aligned; bias: f32 [heads][n_q][n_k] contiguous, or NULL.
+ * head_dim in {8, 16, 24, 32, 48, 64}.  No workspace.
  */
 typedef struct odde_bias_attn_args {
   uint32_t struct_size;

@@ -4,25 +4,26 @@
 // SDPA with scale 1):
 //   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
 //
-// One workgroup of 256 threads per (head, 16 queries), so that a head of
-// 1024 queries fills 64 workgroups and the pair stack's 16 heads give four
-// workgroups per CU.  Key blocks of 128 are staged in LDS as f32 (K and V,
-// head dim D; the next block and this thread's bias values are loaded into
-// registers while a block is computed); the 16 threads of a query take keys
-// part, part + 16, ... of each block, keep their own running max, sum and output (the online
-// softmax), and merge the 16 partial results (max-rescaled) by lane shuffles
-// at the end.  All arithmetic is f32; the exponentials are exp2 of
-// log2e-scaled logits.
+// One workgroup of 4 waves per (head, 64 queries); wave w takes queries
+// 16 w .. 16 w + 15.  Key blocks of 64 are staged in LDS as f32 by 16-byte
+// loads (the next block's are loaded into registers while a block is
+// computed).  Per 16 keys of a block, on the fp32 MFMA
+// (v_mfma_f32_16x16x4_f32, true fp32 products):
+//   S^T[key][query] = K Q^T over head-dim steps of 4 (lane: key l % 16 of the
+//   A operand, query l % 16 of B, dims 4 s + l / 16),
+//   plus the bias, online softmax per query (running max across the four
+//   16-lane groups, exp2 of log2e-scaled logits),
+//   O^T[dim][query] += V^T P^T in four key steps: step kk takes the
+//   accumulator's register kk of every lane (key 4 (l / 16) + kk) as the B
+//   operand and V[key 4 (l / 16) + kk][dim l % 16] as the A operand, so P
+//   needs no shuffle.
 #include "common.hpp"
 #include "runtime.hpp"
 
 namespace odde {
 
-constexpr int kBaTPQ = 16;             // threads per query
-constexpr int kBaQ = 256 / kBaTPQ;     // queries per workgroup
-constexpr int kBaK = 128;              // keys per staged block
-constexpr int kBaKPT = kBaK / kBaTPQ;  // keys per thread per block
 constexpr int kBaMaxD = 64;
+constexpr int kBaK = 64;  // keys per staged block
 
 struct BiasAttnArgs {
   const void* q; const void* k; const void* v;
@@ -33,124 +34,131 @@ struct BiasAttnArgs {
   int nq, nk;
 };
 
-// The next key block's K and V values (kBaK * D of each, spread over the 256
-// threads) and this thread's bias values, loaded into registers while the
-// current block is computed.
-template <typename T, int D>
-struct BaPrefetch {
-  static constexpr int PER = (kBaK * D + 255) / 256;
-  T kv[2][PER];
-  float b[kBaKPT];
-};
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
-  constexpr int LDK = D + 4;  // LDS row pitch (floats): the parts' rows land on distinct banks
-  using PF = BaPrefetch<T, D>;
-  __shared__ __attribute__((aligned(16))) float ks[kBaK * LDK];
-  __shared__ __attribute__((aligned(16))) float vs[kBaK * LDK];
-  const int h = blockIdx.y, i0 = blockIdx.x * kBaQ;
-  const int t = threadIdx.x, qi = t / kBaTPQ, part = t % kBaTPQ;
-  const int i = i0 + qi;
-  const bool valid = i < a.nq;
-  const T* qp = static_cast<const T*>(a.q) + h * a.q_sh + (int64_t)(valid ? i : 0) * a.q_sn;
-  float q[D];
+  constexpr int NS = D / 4;          // head-dim steps of the QK^T product
+  constexpr int NT = (D + 15) / 16;  // 16-dim tiles of the output
+  constexpr int LD = D + 1;          // LDS row pitch (floats)
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int CPR = D / VEC;       // 16-byte chunks per key row
+  constexpr int CHUNKS = kBaK * CPR; // per operand and block
+  constexpr int PER = (CHUNKS + 255) / 256;
+  static_assert(D % VEC == 0, "rows of whole 16-byte chunks");
+  typedef T tvec __attribute__((ext_vector_type(VEC)));
+  __shared__ float ks[kBaK * LD];
+  __shared__ float vs[kBaK * LD];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int h = blockIdx.y, qi = blockIdx.x * 64 + 16 * w + r16;
+  const bool qvalid = qi < a.nq;
+  const T* qp = static_cast<const T*>(a.q) + h * a.q_sh + (int64_t)(qvalid ? qi : 0) * a.q_sn;
+  float qf[NS];
 #pragma unroll
-  for (int d = 0; d < D; ++d) q[d] = to_f32(qp[d]) * kLog2e;
-  const float* brow = a.bias ? a.bias + ((int64_t)h * a.nq + (valid ? i : 0)) * a.nk : nullptr;
-  float m = -INFINITY, lsum = 0.f, o[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d) o[d] = 0.f;
+  for (int s = 0; s < NS; ++s) qf[s] = qvalid ? to_f32(qp[4 * s + g]) * kLog2e : 0.f;
   const T* kb = static_cast<const T*>(a.k) + h * a.k_sh;
   const T* vb = static_cast<const T*>(a.v) + h * a.v_sh;
-  PF pf;
+  const float* brow = a.bias ? a.bias + ((int64_t)h * a.nq + (qvalid ? qi : 0)) * a.nk : nullptr;
+  const bool bvec = (a.nk & 3) == 0;
+
+  tvec kr[PER], vr[PER];  // the next block's chunks
   auto fetch = [&](int j0) {
-    const int nj = min(kBaK, a.nk - j0);
 #pragma unroll
-    for (int u = 0; u < PF::PER; ++u) {
-      const int e = t + 256 * u, r = e / D, d = e % D;
-      const bool in = e < kBaK * D && r < nj;
-      pf.kv[0][u] = in ? kb[(int64_t)(j0 + r) * a.k_sn + d] : T(0.f);
-      pf.kv[1][u] = in ? vb[(int64_t)(j0 + r) * a.v_sn + d] : T(0.f);
-    }
-#pragma unroll
-    for (int u = 0; u < kBaKPT; ++u) {
-      const int r = kBaTPQ * u + part;
-      pf.b[u] = (brow && r < nj) ? brow[j0 + r] : 0.f;
+    for (int u = 0; u < PER; ++u) {
+      const int c = threadIdx.x + 256 * u, key = j0 + c / CPR, d0 = (c % CPR) * VEC;
+      const bool in = c < CHUNKS && key < a.nk;
+      tvec zk, zv;
+      for (int e = 0; e < VEC; ++e) zk[e] = zv[e] = (T)0.f;
+      kr[u] = in ? *reinterpret_cast<const tvec*>(kb + (int64_t)key * a.k_sn + d0) : zk;
+      vr[u] = in ? *reinterpret_cast<const tvec*>(vb + (int64_t)key * a.v_sn + d0) : zv;
     }
   };
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   fetch(0);
   for (int j0 = 0; j0 < a.nk; j0 += kBaK) {
-    const int nj = min(kBaK, a.nk - j0);
-    __syncthreads();  // the previous block's K, V are no longer read
+    __syncthreads();  // the previous block is no longer read
 #pragma unroll
-    for (int u = 0; u < PF::PER; ++u) {
-      const int e = t + 256 * u;
-      if (e < kBaK * D) {
-        const int r = e / D, d = e % D;
-        ks[r * LDK + d] = to_f32(pf.kv[0][u]);
-        vs[r * LDK + d] = to_f32(pf.kv[1][u]);
+    for (int u = 0; u < PER; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      if (c < CHUNKS) {
+        const int key = c / CPR, d0 = (c % CPR) * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ks[key * LD + d0 + e] = to_f32(kr[u][e]);
+          vs[key * LD + d0 + e] = to_f32(vr[u][e]);
+        }
       }
     }
-    float bcur[kBaKPT];
-#pragma unroll
-    for (int u = 0; u < kBaKPT; ++u) bcur[u] = pf.b[u];
     __syncthreads();
     if (j0 + kBaK < a.nk) fetch(j0 + kBaK);  // in flight during this block
-    // this thread's keys of the block: logits (log2 units), block max
-    float s[kBaKPT];
-    float bm = -INFINITY;
+    const int nsub = min(kBaK, a.nk - j0);
+    for (int sb = 0; sb < nsub; sb += 16) {
+      const int k0 = j0 + sb;
+      // bias[qi][k0 + 4 g + r]
+      float bc[4] = {0.f, 0.f, 0.f, 0.f};
+      if (brow) {
+        if (bvec && k0 + 4 * g + 3 < a.nk) {
+          const f32x4 b4 = *reinterpret_cast<const f32x4*>(brow + k0 + 4 * g);
 #pragma unroll
-    for (int u = 0; u < kBaKPT; ++u) {
-      const int r = kBaTPQ * u + part;
-      const float* kr = ks + r * LDK;
-      float acc = 0.f;
+          for (int r = 0; r < 4; ++r) bc[r] = b4[r];
+        } else {
 #pragma unroll
-      for (int d = 0; d < D; ++d) acc = fmaf(q[d], kr[d], acc);
-      acc = fmaf(bcur[u], kLog2e, acc);
-      s[u] = r < nj ? acc : -INFINITY;
-      bm = fmaxf(bm, s[u]);
-    }
-    const float mn = fmaxf(m, bm);
-    if (mn > -INFINITY) {
-      const float scale = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first block
+          for (int r = 0; r < 4; ++r)
+            if (k0 + 4 * g + r < a.nk) bc[r] = brow[k0 + 4 * g + r];
+        }
+      }
+      f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s)  // [key 4g + r][query r16]
+        sacc = mfma4(ks[(sb + r16) * LD + 4 * s + g], qf[s], sacc);
+      float sv[4], bm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 4 * g + r;
+        sv[r] = key < a.nk ? fmaf(bc[r], kLog2e, sacc[r]) : -INFINITY;
+        bm = fmaxf(bm, sv[r]);
+      }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m, bm);  // finite: every 16-key step has a key
+      const float scale = __builtin_amdgcn_exp2f(m - mn);  // 0 at the first step
       lsum *= scale;
 #pragma unroll
-      for (int d = 0; d < D; ++d) o[d] *= scale;
-#pragma unroll
-      for (int u = 0; u < kBaKPT; ++u) {
-        const float p = __builtin_amdgcn_exp2f(s[u] - mn);  // 0 for keys past the end
-        lsum += p;
-        const float* vr = vs + (kBaTPQ * u + part) * LDK;
-#pragma unroll
-        for (int d = 0; d < D; ++d) o[d] = fmaf(p, vr[d], o[d]);
-      }
+      for (int t = 0; t < NT; ++t) o[t] *= scale;
       m = mn;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(sv[r] - mn);
+        lsum += p[r];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int d = 16 * t + r16;
+          const float vv = d < D ? vs[(sb + 4 * g + kk) * LD + d] : 0.f;
+          o[t] = mfma4(vv, p[kk], o[t]);  // [dim][query r16]
+        }
     }
   }
-  // merge the parts of the query (consecutive lanes of one wave)
-#pragma unroll
-  for (int x = 1; x < kBaTPQ; x <<= 1) {
-    const float m2 = __shfl_xor(m, x, 64);
-    const float l2 = __shfl_xor(lsum, x, 64);
-    const float mn = fmaxf(m, m2);
-    const float s1 = mn > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.f;
-    const float s2 = mn > -INFINITY ? __builtin_amdgcn_exp2f(m2 - mn) : 0.f;
-    lsum = lsum * s1 + l2 * s2;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const float o2 = __shfl_xor(o[d], x, 64);
-      o[d] = o[d] * s1 + o2 * s2;
-    }
-    m = mn;
-  }
-  if (!valid) return;
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (!qvalid) return;
   const float inv = 1.0f / lsum;
-  T* op = static_cast<T*>(a.out) + h * a.o_sh + (int64_t)i * a.o_sn;
-  // part p writes dims p, p + 16, ...
+  T* op = static_cast<T*>(a.out) + h * a.o_sh + (int64_t)qi * a.o_sn;
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d % kBaTPQ == part) op[d] = from_f32<T>(o[d] * inv);
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = 16 * t + 4 * g + r;
+      if (d < D) op[d] = from_f32<T>(o[t][r] * inv);
+    }
 }
 
 namespace {
@@ -164,7 +172,7 @@ int launch_bias_attn(const odde_bias_attn_args* x, hipStream_t st) {
   a.bias = x->bias; a.out = x->out; a.o_sh = x->o_sh; a.o_sn = x->o_sn;
   a.nq = x->n_q; a.nk = x->n_k;
   LaunchScope ls(ODDE_K_BIAS_ATTN, st);
-  dim3 grid((x->n_q + kBaQ - 1) / kBaQ, x->heads);
+  dim3 grid((x->n_q + 63) / 64, x->heads);
   switch (x->head_dim) {
 #define ODDE_BA(D) \
     case D: hipLaunchKernelGGL((bias_attn_kernel<T, D>), grid, dim3(256), 0, st, a); break;
@@ -193,6 +201,12 @@ extern "C" int odde_bias_attn_fwd(const odde_bias_attn_args* x, void* stream) {
   if (x->n_k == 0) return set_error(ODDE_EINVAL, "bias_attn: no keys");
   if (!x->q || !x->k || !x->v || !x->out) return set_error(ODDE_EINVAL, "bias_attn: null tensor pointer");
   if (x->heads > 65535) return set_error(ODDE_EUNSUPPORTED, "bias_attn: at most 65535 heads");
+  {
+    const int64_t es = x->dtype == ODDE_F32 ? 4 : 2;
+    if (((reinterpret_cast<uintptr_t>(x->k) | reinterpret_cast<uintptr_t>(x->v)) & 15) ||
+        ((x->k_sh * es) | (x->k_sn * es) | (x->v_sh * es) | (x->v_sn * es)) & 15)
+      return set_error(ODDE_EINVAL, "bias_attn: k and v rows must be 16-byte aligned");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   return x->dtype == ODDE_F32 ? launch_bias_attn<float>(x, st) : launch_bias_attn<bf16>(x, st);
 }

@@ -431,6 +431,9 @@ def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     for t in (q, k, v):
         if t.stride(-1) != 1:
             raise ValueError("q, k, v need a contiguous head dim")
+    es = q.element_size()
+    if any((t.data_ptr() | t.stride(0) * es | t.stride(1) * es) & 15 for t in (k, v)):
+        k, v = k.contiguous(), v.contiguous()  # rows must start on 16-byte boundaries
     b = None
     if bias is not None:
         b = bias.to(torch.float32).expand(h, nq, nk).contiguous()
