@@ -219,20 +219,23 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 }
 
 // Pipelined form for C = 128, n = 4 (the pair transition).  Two workgroups
-// of 4 waves per CU; a workgroup owns 128 rows at a time, wave w rows
-// 32w..32w+31 (two 16-row blocks).  The rows never go through LDS: each wave
-// loads its rows' K32 fragment slots straight into registers and applies the
-// LayerNorm there (the four lanes of a row reduce by shuffles).  The hidden
-// dimension is walked in chunks of 32 whose W_a / W_b rows and W_o columns
-// (24 KiB) stream into three LDS stages by direct global -> LDS loads, two
-// chunks ahead, continuing across row tiles (every tile walks the same
-// chunks).  At a tile boundary the next tile's rows and this tile's residual
-// rows are loaded together, then the outputs are stored; so the loads of one
+// of 4 waves per CU; a workgroup owns 64 kRB rows at a time, wave w rows
+// 16 kRB w .. (kRB 16-row blocks): every weight fragment read from LDS serves
+// kRB row blocks.  The rows never go through LDS: each wave loads its rows'
+// K32 fragment slots straight into registers and applies the LayerNorm there
+// (the four lanes of a row reduce by shuffles).  The hidden dimension is
+// walked in chunks of 32 whose W_a / W_b rows and W_o columns (24 KiB) stream
+// into three LDS stages by direct global -> LDS loads, two chunks ahead,
+// continuing across row tiles (every tile walks the same chunks).  At a tile
+// boundary the residual rows are loaded one row block at a time and the
+// outputs stored, then the pair bias (if asked) is formed from the stored
+// values, then the next tile's rows are loaded; so the loads of one
 // workgroup overlap the other workgroup's MFMA work.
 // LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
 // bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
 // (4 slots; slot t of row r holds chunk t ^ ((r >> 1) & 3)).
-constexpr int kTpRows = 128;
+constexpr int kRB = 3;                   // 16-row blocks per wave
+constexpr int kTpRows = 64 * kRB;
 constexpr int kTpStages = 3;
 constexpr int kTpChunkElems = 3 * 4096;  // W_a, W_b: 32 x 128; W_o: 128 x 32
 constexpr int kTpOps = 6;                // 1 KiB direct loads per wave per chunk
@@ -328,12 +331,12 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   if (Q > 1) issue(1);
 
   auto row_of = [&](int64_t tile, int rb) -> int64_t {
-    return tile * kTpRows + (2 * w + rb) * 16 + r16;
+    return tile * kTpRows + (kRB * w + rb) * 16 + r16;
   };
-  RowSlots<ZT> xr[2];  // the rows of the tile about to start
+  RowSlots<ZT> xr[kRB];  // the rows of the tile about to start
   auto load_rows = [&](int64_t tile) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = min(row_of(tile, rb), a.rows - 1);  // pad rows read a real row
       xr[rb].load(a.x + row * C, g);
     }
@@ -348,9 +351,9 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   int q = 0;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     // LayerNorm of the wave's rows (already in registers) into B fragments
-    Frag<bf16> xf[2][kC];
+    Frag<bf16> xf[kRB][kC];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < kRB; ++rb) {
       const bool valid = row_of(tile, rb) < a.rows;
       float x[kC][8];
       float s = 0.f;
@@ -386,9 +389,9 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
           xf[rb][t].set(e, valid ? (x[t][e] - mean) * rstd * lw[e] + lb[e] : 0.f);
       }
     }
-    f32x4 acc[2][NCB];
+    f32x4 acc[kRB][NCB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -411,84 +414,86 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       const bf16* wa = ws[q % kTpStages];
       const bf16* wb = wa + 4096;
       const bf16* wo = wa + 8192;
-      // GEMM1 per 16 hidden units (hb): gate and value fragments of hb, both
-      // row blocks; silu(a) * b lands in slots 4hb..4hb+3 of each row block's
-      // hidden fragment
-      Frag<bf16> hf[2];
+      // GEMM1 per 16 hidden units (hb): each gate / value fragment pair of
+      // hb serves both row blocks; silu(a) * b lands in slots 4hb..4hb+3 of
+      // each row block's hidden fragment
+      Frag<bf16> hf[kRB];
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
-        Frag<bf16> fa[kC], fb[kC];
+        f32x4 sa[kRB], sb[kRB];
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) sa[rb] = sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
           const int off = sa_off + hb * 16 * C + ((4 * t + g) ^ r16) * 8;
-          fa[t].load(wa + off);
-          fb[t].load(wb + off);
-        }
+          Frag<bf16> fa, fb;
+          fa.load(wa + off);
+          fb.load(wb + off);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
-#pragma unroll
-          for (int t = 0; t < kC; ++t) {
-            mma(sa, fa[t], xf[rb][t]);
-            mma(sb, fb[t], xf[rb][t]);
+          for (int rb = 0; rb < kRB; ++rb) {
+            mma(sa[rb], fa, xf[rb][t]);
+            mma(sb[rb], fb, xf[rb][t]);
           }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) hf[rb].set(4 * hb + e, siluf_(sa[e]) * sb[e]);
         }
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hf[rb].set(4 * hb + e, siluf_(sa[rb][e]) * sb[rb][e]);
       }
-      Frag<bf16> fo[NCB];  // W_o[c][h0 + slot]: hidden 4g..4g+3 and 16+4g..16+4g+3
+      // GEMM2: W_o[c][h0 + slot] fragments (hidden 4g..4g+3 and 16+4g..16+4g+3)
+      // one 16-channel block at a time, both row blocks
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         const bf16* row = wo + (cb * 16 + r16) * kTrHid + 4 * (g & 1);
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + (((g >> 1)) ^ so_sw) * 8);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + ((2 + (g >> 1)) ^ so_sw) * 8);
+        Frag<bf16> fo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          fo[cb].v[e] = lo[e];
-          fo[cb].v[4 + e] = hi[e];
+          fo.v[e] = lo[e];
+          fo.v[4 + e] = hi[e];
         }
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) mma(acc[rb][cb], fo, hf[rb]);
       }
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) mma(acc[rb][cb], fo[cb], hf[rb]);
     }
     // tile boundary: the next tile's rows and this tile's residual rows are
     // loaded together (this wave's pending chunk loads are older, so they
     // complete first), then the outputs are stored.  With float32 rows the
     // registers do not hold both sets at once: the next rows are loaded after
     // the stores.
-    constexpr bool kEarlyRows = sizeof(ZT) == 2;
-    Quad<ZT> res[2][NCB];
-    if (a.add) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int64_t row = min(row_of(tile, rb), a.rows - 1);
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) res[rb][cb].load(a.x + row * C + cb * 16 + 4 * g);
-      }
-    }
     const int64_t next = tile + gridDim.x;
-    if (kEarlyRows && next < ntiles) load_rows(next);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // epilogue: lane holds row (2w+rb)*16 + r16, channels cb*16 + 4g + e
+    // residual rows one row block at a time; the first block's loads and the
+    // wait below also cover this wave's chunk loads for the next tile
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
       const bool valid = row < a.rows;
+      Quad<ZT> res[NCB];
+      if (a.add) {
+        const int64_t rr = min(row, a.rows - 1);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * g);
+      }
+      if (rb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         if (a.add)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[rb][cb].get(e);
+          for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[cb].get(e);
         if (valid)
           store4(a.out + row * C + cb * 16 + 4 * g, acc[rb][cb][0], acc[rb][cb][1],
                  acc[rb][cb][2], acc[rb][cb][3]);
       }
-      if (a.pb_out)
-        pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, valid, lnp + 2 * C, lnp + 3 * C, pbw);
     }
-    if (!kEarlyRows && next < ntiles) load_rows(next);
+    if (a.pb_out)
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) {
+        const int64_t row = row_of(tile, rb);
+        pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, row < a.rows, lnp + 2 * C, lnp + 3 * C,
+                                         pbw);
+      }
+    if (next < ntiles) load_rows(next);
   }
 }
 
