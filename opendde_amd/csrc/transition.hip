@@ -536,8 +536,8 @@ __global__ __launch_bounds__(256) void transition_pair_bias_kernel(TransitionArg
   }
 }
 
-constexpr int kTwTX = 256, kTwTY = 128, kTwWX = 4, kTwNS = 3;
-using TwShape = GemmShape<kTwTX, kTwTY, kTwWX>;
+constexpr int kTwTX = 256, kTwTY = 128, kTwWX = 4, kTwNS = 3, kTwKC = 32;
+using TwShape = GemmShape<kTwTX, kTwTY, kTwWX, kTwKC>;
 
 __device__ __forceinline__ void tw_tile_map(int L, int ncol, int& rt, int& ct) {
   const int xcd = L & 7, s = L >> 3;  // all column tiles of a row tile on one XCD
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
   const int64_t x0 = (int64_t)rt * kTwTX;
   const int y0 = ct * kTwTY, HID = 4 * C;
   f32x4 acc[TwShape::MX][TwShape::MY];
-  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true>(
+  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
       [&](int r) { return yn + (x0 + r) * C; },
       [&](int r) {
         const int R = y0 + r, t = R & 31;
@@ -591,7 +591,7 @@ __global__ __launch_bounds__(512) void transition_wide_out_kernel(const bf16* __
   const int64_t x0 = (int64_t)rt * kTwTX;
   const int y0 = ct * kTwTY, HID = 4 * C;
   f32x4 acc[TwShape::MX][TwShape::MY];
-  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true>(
+  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
       [&](int r) { return h + (x0 + r) * HID; },
       [&](int r) { return wo + (size_t)(y0 + r) * HID; }, HID, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;

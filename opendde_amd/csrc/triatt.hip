@@ -1166,8 +1166,8 @@ __global__ __launch_bounds__(256) void triatt_mflag_kernel(const float* mb, int*
 //    (gemm.hpp).  Rows are the pairs m = i * Jp + j, padded to a multiple of
 //    2048 (rows past n * Jp are never stored).
 // ---------------------------------------------------------------------------
-constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3;
-using WideShape = GemmShape<kWTX, kWTY, kWWX>;
+constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3, kWKC = 32;
+using WideShape = GemmShape<kWTX, kWTY, kWWX, kWKC>;
 
 __device__ __forceinline__ void wide_tile_map(int L, int ncol, int& rt, int& ct) {
   const int xcd = L & 7, s = L >> 3;  // all column tiles of a row tile on one XCD
@@ -1258,7 +1258,7 @@ __global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT
   auto brow = [&](int r) { return W + (size_t)(o0 + r) * C; };
   f32x4 acc[WideShape::MX][WideShape::MY];
   if (type == 2) {  // v: channel-per-lane orientation
-    gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false>(arow, brow, C, sm, acc);
+    gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false, kWKC>(arow, brow, C, sm, acc);
 #pragma unroll
     for (int i = 0; i < WideShape::MX; ++i) {
       const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3
@@ -1284,7 +1284,7 @@ __global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT
     }
     return;
   }
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(arow, brow, C, sm, acc);
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(arow, brow, C, sm, acc);
   // the wave's 64 pairs lie in one row (Jp and the offsets are multiples of 64)
   const int64_t mw = x0 + wx * (kWTX / kWWX);
   const int row = (int)(mw / jp);
@@ -1336,7 +1336,7 @@ __global__ __launch_bounds__(512) void triatt_out_wide_kernel(TriattOutArgs<ZT, 
   const int64_t x0 = (int64_t)rt * kWTX;
   const int y0 = ct * kWTY;
   f32x4 acc[WideShape::MX][WideShape::MY];
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(
       [&](int r) { return a.o + (x0 + r) * HD; },
       [&](int r) { return a.wo + (size_t)(y0 + r) * HD; }, HD, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;

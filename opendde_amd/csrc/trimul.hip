@@ -575,8 +575,8 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
 //    (gemm.hpp) with the gating / residual epilogues.  Rows are the pairs of
 //    the padded grid, m = x * Np + y (Np^2 rows, a multiple of 2048).
 // ---------------------------------------------------------------------------
-constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3;
-using WideShape = GemmShape<kWTX, kWTY, kWWX>;
+constexpr int kWTX = 256, kWTY = 128, kWWX = 4, kWNS = 3, kWKC = 32;
+using WideShape = GemmShape<kWTX, kWTY, kWWX, kWKC>;
 
 // Linear workgroup id -> (row tile, column tile) such that all column tiles
 // of a row tile run on one XCD (workgroups are dealt to the 8 XCDs
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArg
   const int y0 = ct * kWTY;
   const int C = a.c, CH = a.ch, np = a.np;
   f32x4 acc[WideShape::MX][WideShape::MY];
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false>(
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false, kWKC>(
       [&](int r) { return a.zn + (x0 + r) * C; },
       [&](int r) {
         const int R = y0 + r, side = R / (2 * CH), within = R % (2 * CH), t = within & 31;
@@ -669,10 +669,10 @@ __global__ __launch_bounds__(512) void trimul_out_wide_kernel(TrimulWideOutArgs<
   const int y0 = ct * kWTY;
   const int C = a.c, CH = a.ch, np = a.np;
   f32x4 accy[WideShape::MX][WideShape::MY], accg[WideShape::MX][WideShape::MY];
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(
       [&](int r) { return a.pn + (x0 + r) * CH; },
       [&](int r) { return a.wz + (size_t)(y0 + r) * CH; }, CH, sm, accy);
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true>(
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(
       [&](int r) {
         const int64_t m = x0 + r;  // the incoming form's z rows were normalised transposed
         const int64_t zr = a.zn_transposed ? (m % np) * np + m / np : m;
