@@ -47,6 +47,17 @@ int check_launch(const char* what) {
   return ODDE_OK;
 }
 
+int resident_grid(const void* kernel, int threads) {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;  // one workgroup per CU of an MI355X
+  }
+  return (per > 0 ? per : 1) * (cus > 0 ? cus : 1);
+}
+
 LaunchScope::LaunchScope(int kernel_id, hipStream_t s) : id(kernel_id), stream(s), slot(-1) {
   g_launches[id].fetch_add(1, std::memory_order_relaxed);
   TimingState& t = timing();

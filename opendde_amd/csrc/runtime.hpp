@@ -14,6 +14,10 @@ namespace odde {
 
 int set_error(int code, const std::string& msg);
 int check_launch(const char* what);
+// Workgroups of `threads` threads of `kernel` resident on the current device
+// at once (occupancy x CUs): the grid of a persistent kernel, whose
+// workgroups must all be resident or the late ones finish a whole pass late.
+int resident_grid(const void* kernel, int threads);
 
 // Launch bookkeeping: counts every launch; when timing is on, records a pair
 // of events around it on `stream`.

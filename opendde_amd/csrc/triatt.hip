@@ -258,9 +258,10 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 
 // Weight-stationary form of the projection (used when each wave's weight
 // slice fits in registers, e.g. C = H*D = 128 in bf16): wave 0 holds W_q (and
-// the tri-bias rows), wave 1 W_k, wave 2 W_v, wave 3 W_g; the workgroup loops
-// over 64-row tiles (i, j0..j0+63), staging LN(z) once in LDS per tile.  The
-// next tile's z rows stream into LDS (direct loads) while a tile is computed.
+// the tri-bias rows), wave 1 W_k, wave 2 W_v (the gate is computed by the
+// output kernel, triatt_out_ws_kernel); the workgroup loops over 64-row tiles
+// (i, j0..j0+63), staging LN(z) once in LDS per tile.  The next tile's z rows
+// stream into LDS (direct loads) while a tile is computed.
 template <typename ZT, typename CT, int kC, int kHD>
 __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<ZT, CT> a,
                                                                 int ntiles) {
@@ -275,7 +276,8 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
     lnp[t] = a.ln_w[t];
     lnp[C + t] = a.ln_b[t];
   }
-  const CT* W = w == 0 ? a.wq : w == 1 ? a.wk : w == 2 ? a.wv : a.wg;
+  // wave 3 only helps stage the tile: the gate is computed in the output kernel
+  const CT* W = w == 0 ? a.wq : w == 1 ? a.wk : a.wv;
   Frag<CT> wf[NB][kC];
   load_w_slice<CT, NB, kC>(W, C, 0, HD, wf);
   Frag<CT> wbf[kC];
@@ -345,6 +347,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
     float bmx = -INFINITY;
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      if (w == 3) break;
       Frag<CT> xf[kC];
       tile_frags<CT, C>(xs, rb, xf);
       if (w == 2) {  // v: x W^T -> lane holds channel o, rows jb..jb+3
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
           store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), acc[0] * vk[0],
                  acc[1] * vk[1], acc[2] * vk[2], acc[3] * vk[3]);
         }
-      } else {  // q / k / gate: W x^T -> lane holds row jr, channels o..o+3
+      } else {  // q / k: W x^T -> lane holds row jr, channels o..o+3
         const int jr = j0 + rb * 16 + r16;
         float ss = 0.f;
 #pragma unroll
@@ -374,16 +377,13 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
           if (w == 0) {
             const float sc = a.q_scale;
             store4(a.q + off, acc[0] * sc, acc[1] * sc, acc[2] * sc, acc[3] * sc);
-          } else if (w == 1) {
+          } else {
             store4(a.k + off, acc[0], acc[1], acc[2], acc[3]);
             ss += acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2] + acc[3] * acc[3];
             if (ob & 1) {
               knm[ob >> 1] = fmaxf(knm[ob >> 1], sqrtf(group_sum_fast(ss)));
               ss = 0.f;
             }
-          } else {
-            store4(a.gate + off, sigmoidf_(acc[0]), sigmoidf_(acc[1]), sigmoidf_(acc[2]),
-                   sigmoidf_(acc[3]));
           }
         }
         if (w == 0) {  // tri bias: lane h = r16, rows jb..jb+3
@@ -928,12 +928,17 @@ template <typename ZT, typename CT>
 struct TriattOutArgs {
   const CT* o;  // [I][Jp][HD]
   const CT* wo; // [C][HD]
-  const ZT* res;
+  const ZT* res;  // z: the residual, and the gate's input where the gate is fused here
   int64_t r_s0, r_s1;
   ZT* out;
   int64_t o_s0, o_s1;
   int n, jp, c;
   int add;
+  // gate fused into the output kernel (weight-stationary path)
+  const CT* wg;  // [HD][C]
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
 };
 
 template <typename ZT, typename CT, int kHD>
@@ -967,67 +972,104 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
   }
 }
 
-// Weight-stationary output projection: wave w holds the W_o rows of output
-// channels [w*C/4, (w+1)*C/4); the workgroup loops over 64-row tiles of o,
-// staged in LDS.
+// Weight-stationary output projection with the gate fused in.  Per 64-row
+// tile (i, j0..j0+63) the z rows stream into LDS (direct loads, one tile
+// ahead) and are LayerNorm'd there; wave w computes gate channels
+// [w*HD/4, (w+1)*HD/4) of g = sigmoid(LN(z) W_g^T) with its W_g rows held in
+// registers and scales its columns of the o tile (staged in LDS) by them;
+// then wave w projects output channels [w*C/4, (w+1)*C/4) of the gated tile
+// with its W_o rows held in registers and adds the residual, read from the
+// staged z rows.  Gating here rather than in the flash core saves the gate
+// tensor's write and read in HBM.
 template <typename ZT, typename CT, int kHD, int kC>
 __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT, CT> a, int ntiles) {
-  constexpr int HD = kHD * 32, C = kC * 32, NBO = C / 64, RB = kTileRows / 16;
+  constexpr int HD = kHD * 32, C = kC * 32, NBO = C / 64, NBG = HD / 64, RB = kTileRows / 16;
   constexpr int LD = TileLD<CT, HD>::value;
   constexpr int VEC = 16 / sizeof(CT), PER_ROW = HD / VEC;
   constexpr int OCH = kTileRows * PER_ROW / 256;  // 16-byte chunks of o per thread
+  constexpr int EPC = 16 / (int)sizeof(ZT);       // z elements per 16-byte chunk
+  using Raw = RawTile<ZT, C>;
   static_assert(kTileRows * PER_ROW % 256 == 0, "o tile chunks");
+  static_assert(sizeof(CT) == 2, "gate scaling in LDS takes 4 x 16-bit o values");
   __shared__ __attribute__((aligned(16))) CT xo[kTileRows * LD];
+  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) unsigned char raw[Raw::BYTES];
+  __shared__ float lnp[2 * C];  // LayerNorm weight, bias
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
+  for (int t = threadIdx.x; t < C; t += 256) {
+    lnp[t] = a.ln_w[t];
+    lnp[C + t] = a.ln_b[t];
+  }
   Frag<CT> wof[NBO][kHD];
   load_w_slice<CT, NBO, kHD>(a.wo, HD, w * (C / 4), C, wof);
+  Frag<CT> wgf[NBG][kC];
+  load_w_slice<CT, NBG, kC>(a.wg, C, w * (HD / 4), HD, wgf);
   const int jp = a.jp, n = a.n, tiles_per_row = jp / kTileRows;
 
-  // The next tile's o rows and this lane's residual values are loaded into
-  // registers while the current tile is computed.
+  // The next tile's z rows (into LDS) and o rows (into registers) are loaded
+  // while the current tile is computed; rows past n read row n-1 (always
+  // present), are LayerNorm'd as zeros and never stored.
   f32x4 opre[OCH];
-  float rpre[RB][NBO][4];
   auto fetch = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
+    raw_tile_issue<ZT, C>(
+        [&](int r) -> const ZT* {
+          return a.res + (int64_t)ti * a.r_s0 + (int64_t)min(tj0 + r, n - 1) * a.r_s1;
+        },
+        raw);
     const CT* src = a.o + ((size_t)ti * jp + tj0) * HD;
 #pragma unroll
     for (int k = 0; k < OCH; ++k) {
       const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
       opre[k] = *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
     }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int jr = tj0 + rb * 16 + r16;
-#pragma unroll
-      for (int cb = 0; cb < NBO; ++cb) {
-        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
-        if (a.add && jr < n) {
-          load4(a.res + (int64_t)ti * a.r_s0 + (int64_t)jr * a.r_s1 + c0, rpre[rb][cb]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) rpre[rb][cb][e] = 0.f;
-        }
-      }
-    }
   };
   if ((int)blockIdx.x < ntiles) fetch(blockIdx.x);
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int i = tile / tiles_per_row;
     const int j0 = (tile % tiles_per_row) * kTileRows;
+    raw_tile_wait();  // also: every wave is done with the previous tile's xs and xo
 #pragma unroll
     for (int k = 0; k < OCH; ++k) {
       const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
       *reinterpret_cast<f32x4*>(xo + r * LD + cc) = opre[k];
     }
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, lnp, lnp + C, a.eps, xs);
+    // this lane's residual values: rows rb*16 + r16, channels c0..c0+3
     float res[RB][NBO][4];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
+      const int r = rb * 16 + r16;
 #pragma unroll
-      for (int cb = 0; cb < NBO; ++cb)
+      for (int cb = 0; cb < NBO; ++cb) {
+        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        const ZT* p = reinterpret_cast<const ZT*>(raw + r * Raw::ROW_BYTES +
+                                                  (((c0 / EPC) ^ (r & 7)) * 16)) + c0 % EPC;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) res[rb][cb][e] = rpre[rb][cb][e];
-    lds_barrier();
+        for (int e = 0; e < 4; ++e) res[rb][cb][e] = a.add ? to_f32(p[e]) : 0.f;
+      }
+    }
+    lds_barrier();  // xs and xo ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) fetch(tile + gridDim.x);
+    // gate: lane holds row rb*16 + r16, gate channels o..o+3 of its slice
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      Frag<CT> xf[kC];
+      tile_frags<CT, C>(xs, rb, xf);
+#pragma unroll
+      for (int gb = 0; gb < NBG; ++gb) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < kC; ++t) mma(acc, wgf[gb][t], xf[t]);
+        const int o = w * (HD / 4) + gb * 16 + 4 * g;
+        bf16x4* p = reinterpret_cast<bf16x4*>(xo + (rb * 16 + r16) * LD + o);
+        bf16x4 ov = *p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (bf16)((float)ov[e] * sigmoidf_(acc[e]));
+        *p = ov;
+      }
+    }
+    lds_barrier();  // the gated o tile is complete
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       Frag<CT> xf[kHD];
@@ -1044,7 +1086,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
                res[rb][cb][1] + acc[1], res[rb][cb][2] + acc[2], res[rb][cb][3] + acc[3]);
       }
     }
-    lds_barrier();  // xo is rewritten for the next tile
+    // xs and xo are rewritten only after the barrier in raw_tile_wait()
   }
 }
 
@@ -1398,6 +1440,13 @@ bool triatt_wide(int c, int heads, int dt) {
   return dt == ODDE_BF16 && (c == 128 || c == 256 || c == 384) &&
          (hd == 128 || hd == 256 || hd == 384) && (c >= 256 || hd >= 256);
 }
+// The weight-stationary projection / output pair, with the gate fused into the
+// output kernel: bf16 compute where C and H*32 are 64 or 128 (each wave's
+// weight slices fit in registers).  Disjoint from the wide path.
+bool triatt_ws(int c, int heads, int dt) {
+  const int hd = heads * 32;
+  return dt == ODDE_BF16 && (c == 64 || c == 128) && (hd == 64 || hd == 128);
+}
 // rows of the wide path's GEMMs: the n * Jp pairs padded to whole groups of
 // 8 row tiles
 int64_t triatt_wide_rows(int n) { return (int64_t)round_up(n * round_up(n, 64), 2048); }
@@ -1411,7 +1460,7 @@ TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int cz, int d
   Carver c(base, size);
   TriattWs w;
   carve_core_bufs(c, w.c, n, heads, jp, 1, dt);
-  w.gate = c.take<char>(per);
+  w.gate = triatt_ws(cz, heads, dt) ? nullptr : c.take<char>(per);
   // the wide path reads o as GEMM rows, whole 256-row tiles
   w.o = c.take<char>(wide ? (uint64_t)triatt_wide_rows(n) * heads * 32 * 2 : per);
   w.zn = wide ? c.take<char>((uint64_t)triatt_wide_rows(n) * cz * 2) : nullptr;
@@ -1466,7 +1515,9 @@ bool launch_proj_ws(const TriattProjArgs<ZT, CT>& p, int C, int HD, int n, int j
 template <typename ZT, typename CT, int kHD, int kC>
 void launch_out_ws_t(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   const int ntiles = n * (jp / kTileRows);
-  hipLaunchKernelGGL((triatt_out_ws_kernel<ZT, CT, kHD, kC>), dim3(min(ntiles, 3 * 256)),
+  static const int resident =
+      resident_grid(reinterpret_cast<const void*>(&triatt_out_ws_kernel<ZT, CT, kHD, kC>), 256);
+  hipLaunchKernelGGL((triatt_out_ws_kernel<ZT, CT, kHD, kC>), dim3(min(ntiles, resident)),
                      dim3(256), 0, st, p, ntiles);
 }
 template <typename ZT, typename CT>
@@ -1600,6 +1651,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   TriattWs ws = carve_triatt(a->workspace, a->workspace_bytes, n, H, C, a->compute_dtype);
   bool wide = false;
   if constexpr (sizeof(CT) == 2) wide = triatt_wide(C, H, a->compute_dtype);
+  const bool ws_path = triatt_ws(C, H, a->compute_dtype);
 
   TriattProjArgs<ZT, CT> p;
   p.z = static_cast<const ZT*>(a->z);
@@ -1630,7 +1682,10 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
         if (rc) return rc;
       }
     }
-    if (!wide && !launch_proj_ws<ZT, CT>(p, C, HD, n, jp, st)) {
+    if (ws_path) {
+      if (!launch_proj_ws<ZT, CT>(p, C, HD, n, jp, st))
+        return set_error(ODDE_EUNSUPPORTED, "triatt: no weight-stationary projection for this shape");
+    } else if (!wide) {
       switch (C) {
         case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
         case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
@@ -1645,7 +1700,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
 
   TriattCoreArgs<CT> c;
   fill_core_args(c, ws.c);
-  c.gate = static_cast<const CT*>(ws.gate);
+  c.gate = ws_path ? nullptr : static_cast<const CT*>(ws.gate);  // else gated in triatt_out_ws
   c.out = static_cast<CT*>(ws.o);
   c.o_row = (int64_t)jp * HD; c.o_h = 32; c.o_j = HD;
   c.rows = n; c.heads = H; c.n = n; c.jp = jp; c.rows_per_bias = n;
@@ -1658,6 +1713,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   o.res = static_cast<const ZT*>(a->z); o.r_s0 = a->z_s0; o.r_s1 = a->z_s1;
   o.out = static_cast<ZT*>(a->out); o.o_s0 = a->out_s0; o.o_s1 = a->out_s1;
   o.n = n; o.jp = jp; o.c = C; o.add = a->add_residual;
+  o.wg = static_cast<const CT*>(a->w_g); o.ln_w = a->ln_w; o.ln_b = a->ln_b; o.eps = a->eps;
   {
     LaunchScope ls(ODDE_K_TRIATT_OUT, st);
     if constexpr (sizeof(CT) == 2) {
@@ -1668,7 +1724,11 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
         return check_launch("triatt_out (wide)");
       }
     }
-    if (launch_out_ws<ZT, CT>(o, HD, C, n, jp, st)) return check_launch("triatt_out");
+    if (ws_path) {
+      if (!launch_out_ws<ZT, CT>(o, HD, C, n, jp, st))
+        return set_error(ODDE_EUNSUPPORTED, "triatt: no weight-stationary output for this shape");
+      return check_launch("triatt_out");
+    }
     switch (HD) {
       case 64: launch_out<ZT, CT, 2>(o, n, jp, st); break;
       case 128: launch_out<ZT, CT, 4>(o, n, jp, st); break;

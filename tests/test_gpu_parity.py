@@ -72,13 +72,9 @@ def test_triangle_attention_channel_shapes(c, h):
     assert_fp32(got, exp, f"triatt c={c} h={h}")
 
 
-@pytest.mark.parametrize("c,h", [(384, 12), (256, 8), (128, 8), (384, 4)])
-@pytest.mark.parametrize("starting", [True, False])
-@pytest.mark.parametrize("n", [40, 130])
-def test_triangle_attention_wide_bf16(c, h, starting, n):
-    """Wide channels (C or H*32 >= 256) take the LayerNorm-pass + NT GEMM
-    projection and output; z in bf16, and z in fp32 under bf16 autocast
-    with an in-place residual add through the ending-node strides."""
+def _check_bf16_paths(c, h, starting, n):
+    """z in bf16, and z in fp32 under bf16 autocast with an in-place
+    residual add through the ending-node strides."""
     mod = seeded(TriangleAttention(c, 32, h, starting=starting), 800 + c + h + n, STD * 0.5)
     z = _z(n, c, c + h + n)
     mask = token_pair_mask(n, max(1, n // 10), seed=n + 2, random=True)
@@ -87,14 +83,33 @@ def test_triangle_attention_wide_bf16(c, h, starting, n):
     mod = mod.to(DEV)
     got = mod(zb.to(DEV), mask.to(DEV), triangle_attention="hip")
     assert got.dtype == torch.bfloat16
-    assert_bf16(got, exp, f"triatt wide bf16 c={c} h={h} n={n} start={starting}")
+    assert_bf16(got, exp, f"triatt bf16 c={c} h={h} n={n} start={starting}")
     # the block's form: a starting-node module applied through swapped strides
     mod.starting = True
     exp32 = ref.triangle_attention(z, mask, params_of(mod), h, starting=starting)
     z2 = z.to(DEV)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         mod.hip_apply(z2, mask.to(DEV), transpose=not starting, out=z2, add_residual=True)
-    assert_bf16(z2 - z.to(DEV), exp32, f"triatt wide fp32-z c={c} h={h} n={n} start={starting}")
+    assert_bf16(z2 - z.to(DEV), exp32, f"triatt fp32-z c={c} h={h} n={n} start={starting}")
+
+
+@pytest.mark.parametrize("c,h", [(384, 12), (256, 8), (128, 8), (384, 4)])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("n", [40, 130])
+def test_triangle_attention_wide_bf16(c, h, starting, n):
+    """Wide channels (C or H*32 >= 256) take the LayerNorm-pass + NT GEMM
+    projection and output."""
+    _check_bf16_paths(c, h, starting, n)
+
+
+@pytest.mark.parametrize("c,h", [(128, 4), (64, 2), (128, 2), (64, 4)])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("n", [40, 130])
+def test_triangle_attention_weight_stationary_bf16(c, h, starting, n):
+    """C and H*32 in {64, 128} take the weight-stationary projection and the
+    output kernel with the gate (sigmoid(LN(z) W_g^T)) fused in, for z in
+    bf16 and in fp32."""
+    _check_bf16_paths(c, h, starting, n)
 
 
 def test_triangle_attention_no_mask_and_in_place_add():
