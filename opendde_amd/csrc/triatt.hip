@@ -24,11 +24,13 @@
 //                      uniform softmax, i.e. the mean of v, as in the
 //                      reference's float32 arithmetic.
 //   3. triatt_out    — o W_o^T on MFMA plus the residual add, written through
-//                      the (possibly transposed) output strides.
+//                      the (possibly transposed) output strides; on the
+//                      weight-stationary path (bf16, C and H*32 of 64 or 128)
+//                      it also computes the gate from the z rows it stages.
 // The N x N x N logits never touch memory.
 //
 // Workspace layouts (CT = compute type, Jp = N rounded up to 64, I = rows):
-//   q, k, gate : [I][H][Jp][32]
+//   q, k, gate : [I][H][Jp][32]           (no gate plane on the weight-stationary path)
 //   v          : [I][H][Jp/32][2][64][8]  MFMA-ready V^T fragments: per block
 //                of 32 keys, channel half db, lane (d%16 + 16*g), slot e holds
 //                key 4g+e (e<4) or 16+4g+(e-4) (e>=4)
@@ -40,7 +42,8 @@
 //   bmax       : [Bb][H][Jp] (ordered int) max over keys of the bias row
 //   rowflag    : [I]                       row needs the exact path
 //   anykeep    : [I]                       row keeps at least one key
-//   o          : [I][Jp][H*32]             gated attention output (module path)
+//   o          : [I][Jp][H*32]             attention output (gated off the
+//                                           weight-stationary path)
 #include <stdio.h>
 #include <stdlib.h>
 
