@@ -308,20 +308,23 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       blockIdx.x < ntiles ? (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0;
   if (my_tiles == 0) return;
   const int Q = my_tiles * NCHUNK;
+  // A chunk is 24 blocks of 1 KiB (8 per region: W_a, W_b, W_o); wave w's op
+  // `op` loads block bi = 4 (op & 1) + w of region op >> 1, so the region is
+  // known at compile time and the lane's part of the source offset is fixed
+  // per wave: W_a / W_b block bi holds rows 4 bi + (l >> 4) (whose swizzle
+  // key, row & 15 = 4 w + (l >> 4), does not depend on op), W_o block bi
+  // holds channels 16 bi + (l >> 2).
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int lane_ab = (l >> 4) * C + ((l & 15) ^ (4 * w + (l >> 4))) * 8;
+  const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((l >> 3) & 3)) * 8;
   auto issue = [&](int q) {
     const int h0 = (q % NCHUNK) * kTrHid;
     bf16* base = ws[q % kTpStages];
-#pragma unroll 1
-    for (int op = 0; op < kTpOps; ++op) {  // one address live at a time
-      const int b = w * kTpOps + op, region = b >> 3, bi = b & 7;  // 24 KiB = 24 blocks
-      const bf16* src;
-      if (region < 2) {  // W_a / W_b rows h0 + row, 4 rows per block
-        const int row = bi * 4 + (l >> 4), chunk = (l & 15) ^ (row & 15);
-        src = (region ? a.wb : a.wa) + (size_t)(h0 + row) * C + chunk * 8;
-      } else {           // W_o columns h0.., 16 rows (channels) per block
-        const int row = bi * 16 + (l >> 2), chunk = (l & 3) ^ ((row >> 1) & 3);
-        src = a.wo + (size_t)row * HID + h0 + chunk * 8;
-      }
+#pragma unroll
+    for (int op = 0; op < kTpOps; ++op) {
+      const int region = op >> 1, bi = 4 * (op & 1) + wu;
+      const bf16* src = region == 2 ? a.wo + bi * 16 * HID + h0 + lane_o
+                                    : (region ? a.wb : a.wa) + (h0 + bi * 4) * C + lane_ab;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)src,
           (__attribute__((address_space(3))) void*)(base + region * 4096 + bi * 512), 16, 0, 0);
