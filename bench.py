@@ -64,8 +64,11 @@ def kernel_bytes(n, c_z=128, h=4, ch=128, z_bytes=4, ct_bytes=2):
     np_ = (n + 127) // 128 * 128
     hd = h * 32
     zrw = n * n * c_z * z_bytes
+    # q, k, v planes, plus the gate plane off the weight-stationary path (where
+    # the output kernel computes the gate from the z rows it reads anyway)
+    planes = 3 if (c_z in (64, 128) and hd in (64, 128)) else 4
     return {
-        "triatt_proj": zrw + 4 * n * jp * hd * ct_bytes + h * jp * jp * 4 + n * jp * 4,
+        "triatt_proj": zrw + planes * n * jp * hd * ct_bytes + h * jp * jp * 4 + n * jp * 4,
         "triatt_out": n * jp * hd * ct_bytes + 2 * zrw,
         "trimul_proj": zrw + 2 * ch * np_ * np_ * ct_bytes,
         "trimul_out": ch * np_ * np_ * ct_bytes + 2 * zrw,
