@@ -91,22 +91,51 @@ struct RawTile {
   static_assert(kTileRows % (4 * ROWS_PER_OP) == 0, "tile rows per wave");
 };
 
-// Issue the tile's loads.  row_ptr(r) must return a readable row for every
-// r < kTileRows (callers clamp rows past the end to a real row and mask them
-// in raw_tile_ln).  Completion is awaited by raw_tile_wait().
-template <typename ZT, int C, typename RowPtr>
-__device__ __forceinline__ void raw_tile_issue(RowPtr row_ptr, unsigned char* raw) {
+// Issue the tile's loads.  Tile row r is row min(r0 + r, n - 1) of a view
+// whose row 0 starts at `base` with rows `s1` elements apart (rows past the
+// end re-read the last real row; raw_tile_ln masks them).  Completion is
+// awaited by raw_tile_wait().
+//
+// Wave w loads tile rows [w R, (w + 1) R), R = kTileRows / 4, one op of
+// ROWS_PER_OP rows at a time.  Where all of them exist the addresses are
+// affine in the op: the lane's row pointer is formed once and each op adds a
+// uniform step; the row swizzle (r & 7) repeats every 8 / ROWS_PER_OP ops,
+// so that many lane pointers (chunk offset folded in) cover every op.
+template <typename ZT, int C>
+__device__ __forceinline__ void raw_tile_issue(const ZT* base, int64_t s1, int r0, int n,
+                                               unsigned char* raw) {
   using T = RawTile<ZT, C>;
-  const int w = wave_id(), l = lane_id();
+  constexpr int RPO = T::ROWS_PER_OP, OPS = T::OPS_PER_WAVE;
+  constexpr int P = RPO >= 8 ? 1 : 8 / RPO;  // ops per period of the row swizzle
+  static_assert(OPS % P == 0 && (OPS * RPO) % 8 == 0, "swizzle period");
+  const int w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int rl = l / T::CHUNKS, cl = l % T::CHUNKS;
+  const int first = w * OPS * RPO;  // a multiple of 8: r & 7 = (op * RPO + rl) & 7
+  unsigned char* dst = raw + w * OPS * 1024;
+  if (r0 + first + OPS * RPO <= n) {
+    const unsigned char* lrow =
+        reinterpret_cast<const unsigned char*>(base + (int64_t)(r0 + first + rl) * s1);
+    const int64_t step = (int64_t)RPO * s1 * (int64_t)sizeof(ZT);  // bytes per op
+    const unsigned char* lp[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) lp[k] = lrow + (cl ^ ((k * RPO + rl) & 7)) * 16;
+#pragma unroll
+    for (int op = 0; op < OPS; ++op)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(lp[op % P] + op * step),
+          (__attribute__((address_space(3))) void*)(dst + op * 1024), 16, 0, 0);
+  } else {
 #pragma unroll 1
-  for (int op = 0; op < T::OPS_PER_WAVE; ++op) {  // one address live at a time
-    const int blk = w * T::OPS_PER_WAVE + op;
-    const int r = blk * T::ROWS_PER_OP + l / T::CHUNKS;
-    const int chunk = (l % T::CHUNKS) ^ (r & 7);
-    const unsigned char* src = reinterpret_cast<const unsigned char*>(row_ptr(r)) + chunk * 16;
-    __builtin_amdgcn_global_load_lds(
-        (const __attribute__((address_space(1))) void*)src,
-        (__attribute__((address_space(3))) void*)(raw + blk * 1024), 16, 0, 0);
+    for (int op = 0; op < OPS; ++op) {  // one address live at a time
+      const int r = first + op * RPO + rl;
+      const int chunk = cl ^ (r & 7);
+      const unsigned char* src =
+          reinterpret_cast<const unsigned char*>(base + (int64_t)min(r0 + r, n - 1) * s1) +
+          chunk * 16;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(dst + op * 1024), 16, 0, 0);
+    }
   }
 }
 

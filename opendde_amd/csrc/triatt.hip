@@ -293,11 +293,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
   // rows past n read row n-1 (always present) and are masked in the LN pass
   auto issue = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(
-        [&](int r) -> const ZT* {
-          return a.z + (int64_t)ti * a.z_s0 + (int64_t)min(tj0 + r, n - 1) * a.z_s1;
-        },
-        raw);
+    raw_tile_issue<ZT, C>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
   };
   // the next tile's mask value (wave 0, lane = key) and row flag are loaded
   // with its z rows, so no global load latency sits inside a tile
@@ -1015,11 +1011,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
   f32x4 opre[OCH];
   auto fetch = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(
-        [&](int r) -> const ZT* {
-          return a.res + (int64_t)ti * a.r_s0 + (int64_t)min(tj0 + r, n - 1) * a.r_s1;
-        },
-        raw);
+    raw_tile_issue<ZT, C>(a.res + (int64_t)ti * a.r_s0, a.r_s1, tj0, n, raw);
     const CT* src = a.o + ((size_t)ti * jp + tj0) * HD;
 #pragma unroll
     for (int k = 0; k < OCH; ++k) {

@@ -346,11 +346,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   // outside n x n read a real row and are masked in the LN pass
   auto issue = [&](int tl) {
     const int tx = min(tl / tiles_per_row, n - 1), ty0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(
-        [&](int r) -> const ZT* {
-          return a.z + (int64_t)tx * a.z_s0 + (int64_t)min(ty0 + r, n - 1) * a.z_s1;
-        },
-        raw);
+    raw_tile_issue<ZT, C>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
   };
   // wave 0 loads the next tile's mask values (lane = column) with its z rows
   float mnext = 0.f;
@@ -444,11 +440,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   auto issue = [&](int tl) {  // the next tile's z rows (for LN_in), as in the projection
     const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(
-        [&](int r) -> const ZT* {
-          return a.z + (int64_t)tx * a.z_s0 + (int64_t)min(ty0 + r, n - 1) * a.z_s1;
-        },
-        raw);
+    raw_tile_issue<ZT, C>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
   };
   // P[:, x, y0:y0+64] of the next tile is loaded into registers while the
   // current tile is computed, then written transposed to xp[y][c]: thread t
