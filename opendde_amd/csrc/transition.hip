@@ -421,6 +421,15 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       // hb serves both row blocks; silu(a) * b lands in slots 4hb..4hb+3 of
       // each row block's hidden fragment
       Frag<bf16> hf[kRB];
+      // W_a / W_b fragments of step s = 4 hb + t, double buffered: step s + 1's
+      // LDS reads are in flight while step s multiplies
+      Frag<bf16> fa[2], fb[2];
+      auto load_ab = [&](int s, int buf) {
+        const int off = sa_off + (s >> 2) * 16 * C + ((4 * (s & 3) + g) ^ r16) * 8;
+        fa[buf].load(wa + off);
+        fb[buf].load(wb + off);
+      };
+      load_ab(0, 0);
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
         f32x4 sa[kRB], sb[kRB];
@@ -428,15 +437,15 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
         for (int rb = 0; rb < kRB; ++rb) sa[rb] = sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-          const int off = sa_off + hb * 16 * C + ((4 * t + g) ^ r16) * 8;
-          Frag<bf16> fa, fb;
-          fa.load(wa + off);
-          fb.load(wb + off);
+          const int s = 4 * hb + t, buf = s & 1;
+          if (s + 1 < 2 * kC) load_ab(s + 1, buf ^ 1);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int rb = 0; rb < kRB; ++rb) {
-            mma(sa[rb], fa, xf[rb][t]);
-            mma(sb[rb], fb, xf[rb][t]);
+            mma(sa[rb], fa[buf], xf[rb][t]);
+            mma(sb[rb], fb[buf], xf[rb][t]);
           }
+          __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
