@@ -413,6 +413,198 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
   }
 }
 
+// Projection for H*32 = 128 with the 384 q, k, v output channels split evenly
+// over the four waves, 96 each (whole heads): wave 0 q heads 0-2 (and the
+// tri-bias rows), wave 1 q head 3 and k heads 0-1, wave 2 k heads 2-3 and v
+// head 0, wave 3 v heads 1-3 (with the gate computed by the output kernel,
+// the three-matrix split of triatt_proj_ws_kernel leaves a wave idle).  Each
+// wave keeps its 6 x kC weight fragments in registers.  A wave's results
+// stay in registers until its part of the next tile's z rows has landed and
+// are stored only then, so no wave waits for its own stores: they drain
+// while the next tile is normalised and multiplied.
+// Keeps a value packed where it is formed (the 4 x bf16 results are held
+// until after a wait; left to the scheduler, their f32 sources stay live).
+__device__ __forceinline__ void pin(bf16x4& v) { asm volatile("" : "+v"(v)); }
+
+template <int W, typename ZT, typename CT, int kC>
+__device__ __forceinline__ void proj_ws4_role(const TriattProjArgs<ZT, CT>& a, const CT* xs,
+                                              const float* keep_s, const Frag<CT> (&wf)[6][kC],
+                                              const Frag<CT> (&wbf)[kC], int i, int j0,
+                                              bool zero_v) {
+  constexpr int RB = kTileRows / 16, H = 4;
+  const int l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int jp = a.jp;
+  bf16x4 out[RB][6];
+  f32x4 bo[RB];
+  float knm[H], ss = 0.f, bmx = -INFINITY;
+#pragma unroll
+  for (int h = 0; h < H; ++h) knm[h] = 0.f;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    Frag<CT> xf[kC];
+    tile_frags<CT, 32 * kC>(xs, rb, xf);
+#pragma unroll
+    for (int ob = 0; ob < 6; ++ob) {
+      constexpr int base = 96 * W;
+      const int gc = base + 16 * ob, mat = gc >> 7, ch = gc & 127;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (mat == 2) {  // v: x W^T -> lane holds channel ch + r16, rows 4g..4g+3
+#pragma unroll
+        for (int t = 0; t < kC; ++t) mma(acc, xf[t], wf[ob][t]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          out[rb][ob][e] = (bf16)(acc[e] * (zero_v ? keep_s[rb * 16 + 4 * g + e] : 1.f));
+        pin(out[rb][ob]);
+      } else {  // q, k: W x^T -> lane holds row r16, channels ch + 4g..4g+3
+#pragma unroll
+        for (int t = 0; t < kC; ++t) mma(acc, wf[ob][t], xf[t]);
+        const float sc = mat == 0 ? a.q_scale : 1.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[rb][ob][e] = (bf16)(acc[e] * sc);
+        pin(out[rb][ob]);
+        if (mat == 1) {
+          ss += acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2] + acc[3] * acc[3];
+          if (ch & 16) {  // the 32 channels of k head ch / 32 are complete
+            knm[ch >> 5] = fmaxf(knm[ch >> 5], sqrtf(group_sum_fast(ss)));
+            ss = 0.f;
+          }
+        }
+      }
+    }
+    if (W == 0) {  // tri bias: lane h = r16, rows 4g..4g+3
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < kC; ++t) mma(acc, xf[t], wbf[t]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bo[rb][e] = acc[e] * kLog2e;
+      bmx = fmaxf(bmx, fmaxf(fmaxf(bo[rb][0], bo[rb][1]), fmaxf(bo[rb][2], bo[rb][3])));
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of the next tile landed
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int ob = 0; ob < 6; ++ob) {
+      const int gc = 96 * W + 16 * ob, mat = gc >> 7, ch = gc & 127;
+      CT* dst;
+      if (mat == 2) {
+        const int o = ch + r16;
+        dst = a.v + vperm_offset(i, o >> 5, H, jp, j0 + rb * 16 + 4 * g, o & 31);
+      } else {
+        const int o = ch + 4 * g;
+        dst = (mat ? a.k : a.q) + (((size_t)i * H + (o >> 5)) * jp + j0 + rb * 16 + r16) * 32 +
+              (o & 31);
+      }
+      *reinterpret_cast<bf16x4*>(dst) = out[rb][ob];
+    }
+    if (W == 0 && r16 < H)
+      *reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g) =
+          bo[rb];
+  }
+  if (W == 1 || W == 2) {
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const int kh0 = W == 1 ? 0 : 2;  // this wave's k heads: kh0, kh0 + 1
+      if (h < kh0 || h > kh0 + 1) continue;
+      const float v = lanes16_max(knm[h]);
+      if (l == 0) atomicMax(&a.kmax[i * H + h], __float_as_uint(v));
+    }
+  }
+  if (W == 0) {
+    const float bm = group_max_fast(bmx);
+    if (g == 0 && r16 < H) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
+  }
+}
+
+template <typename ZT, typename CT, int kC>
+__global__ __launch_bounds__(256, 2) void triatt_proj_ws4_kernel(TriattProjArgs<ZT, CT> a,
+                                                                 int ntiles) {
+  constexpr int C = kC * 32, HD = 128;
+  static_assert(sizeof(CT) == 2, "bf16 compute");
+  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
+  __shared__ float keep_s[kTileRows];
+  __shared__ float lnp[2 * C];  // LayerNorm weight, bias
+  const int w = wave_id(), l = lane_id();
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int jp = a.jp, n = a.n;
+  for (int t = threadIdx.x; t < C; t += 256) {
+    lnp[t] = a.ln_w[t];
+    lnp[C + t] = a.ln_b[t];
+  }
+  Frag<CT> wf[6][kC];
+#pragma unroll
+  for (int ob = 0; ob < 6; ++ob) {
+    const int gc = 96 * wu + 16 * ob, mat = gc >> 7;
+    const CT* W = mat == 0 ? a.wq : mat == 1 ? a.wk : a.wv;
+#pragma unroll
+    for (int t = 0; t < kC; ++t) load_w_frag(W, C, gc & 127, HD, t, wf[ob][t]);
+  }
+  Frag<CT> wbf[kC];
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    if (wu == 0) load_w_frag(a.wb, C, 0, a.heads, t, wbf[t]);
+    else wbf[t].zero();
+  }
+  const int tiles_per_row = jp / kTileRows;
+  auto issue = [&](int tl) {
+    const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
+    raw_tile_issue<ZT, C>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
+  };
+  // the next tile's mask value (wave 0, lane = key) and row flag are loaded
+  // with its z rows
+  float mnext = 1.f;
+  int aknext = 0;
+  auto mfetch = [&](int tl) {
+    const int ti = tl / tiles_per_row, j = (tl % tiles_per_row) * kTileRows + l;
+    if (w == 0 && a.mask && j < n) mnext = a.mask[(int64_t)ti * a.m_s0 + (int64_t)j * a.m_s1];
+    aknext = a.anykeep[ti];
+  };
+  if ((int)blockIdx.x < ntiles) {
+    issue(blockIdx.x);
+    mfetch(blockIdx.x);
+  }
+  raw_tile_wait();
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int i = tile / tiles_per_row;
+    const int j0 = (tile % tiles_per_row) * kTileRows;
+    const float mcur = mnext;
+    const bool zero_v = aknext != 0;
+    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, lnp, lnp + C, a.eps, xs);
+    if (w == 0) {  // mask row of the tile's 64 keys (lane l = key j0 + l)
+      const int j = j0 + l;
+      float mv = -INFINITY, kp = 0.f;
+      if (j < n) {
+        mv = (mcur - 1.0f) * a.mask_inf;
+        kp = mcur == 1.0f ? 1.f : 0.f;
+      }
+      a.mb[(size_t)i * jp + j] = mv;
+      keep_s[l] = kp;
+      const uint64_t bal = __ballot(mv != 0.f);
+      if (l < 2)
+        a.mflag[(size_t)i * (jp >> 5) + (j0 >> 5) + l] =
+            ((l == 0 ? bal : bal >> 32) & 0xffffffffull) != 0;
+    }
+    lds_barrier();  // xs and keep_s ready; raw consumed
+    if (tile + (int)gridDim.x < ntiles) {
+      issue(tile + gridDim.x);  // raw is free again
+      mfetch(tile + gridDim.x);
+    }
+    if (threadIdx.x < kTileRows) {
+      const int t = threadIdx.x, kb = t >> 5, sl = t & 31;
+      a.keep[((size_t)i * (jp >> 5) + (j0 >> 5) + kb) * 32 + sl] =
+          from_f32<CT>(keep_s[kb * 32 + slot_key(sl >> 3, sl & 7)]);
+    }
+    switch (wu) {
+      case 0: proj_ws4_role<0>(a, xs, keep_s, wf, wbf, i, j0, zero_v); break;
+      case 1: proj_ws4_role<1>(a, xs, keep_s, wf, wbf, i, j0, zero_v); break;
+      case 2: proj_ws4_role<2>(a, xs, keep_s, wf, wbf, i, j0, zero_v); break;
+      default: proj_ws4_role<3>(a, xs, keep_s, wf, wbf, i, j0, zero_v); break;
+    }
+    lds_barrier();  // every wave's part of the next raw tile landed; xs, keep_s free
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 2. flash cores
 // ---------------------------------------------------------------------------
@@ -1494,15 +1686,25 @@ void launch_proj_ws_t(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_
                      ntiles);
 }
 
+// H*32 = 128: the q, k, v channels split over all four waves.
+template <typename ZT, typename CT, int kC>
+void launch_proj_ws4_t(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
+  const int ntiles = n * (jp / kTileRows);
+  static const int resident =
+      resident_grid(reinterpret_cast<const void*>(&triatt_proj_ws4_kernel<ZT, CT, kC>), 256);
+  hipLaunchKernelGGL((triatt_proj_ws4_kernel<ZT, CT, kC>), dim3(min(ntiles, resident)), dim3(256),
+                     0, st, p, ntiles);
+}
+
 template <typename ZT, typename CT>
 bool launch_proj_ws(const TriattProjArgs<ZT, CT>& p, int C, int HD, int n, int jp, hipStream_t st) {
   if constexpr (sizeof(CT) != 2) {
     return false;
   } else {
-  if (C == 128 && HD == 128) { launch_proj_ws_t<ZT, CT, 4, 4>(p, n, jp, st); return true; }
+  if (C == 128 && HD == 128) { launch_proj_ws4_t<ZT, CT, 4>(p, n, jp, st); return true; }
   if (C == 64 && HD == 64) { launch_proj_ws_t<ZT, CT, 2, 2>(p, n, jp, st); return true; }
   if (C == 128 && HD == 64) { launch_proj_ws_t<ZT, CT, 4, 2>(p, n, jp, st); return true; }
-  if (C == 64 && HD == 128) { launch_proj_ws_t<ZT, CT, 2, 4>(p, n, jp, st); return true; }
+  if (C == 64 && HD == 128) { launch_proj_ws4_t<ZT, CT, 2>(p, n, jp, st); return true; }
     return false;
   }
 }
