@@ -1681,9 +1681,10 @@ void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st)
 template <typename ZT, typename CT, int kC, int kHD>
 void launch_proj_ws_t(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   const int ntiles = n * (jp / kTileRows);
-  const int grid = min(ntiles, 2 * 256);
-  hipLaunchKernelGGL((triatt_proj_ws_kernel<ZT, CT, kC, kHD>), dim3(grid), dim3(256), 0, st, p,
-                     ntiles);
+  static const int resident =
+      resident_grid(reinterpret_cast<const void*>(&triatt_proj_ws_kernel<ZT, CT, kC, kHD>), 256);
+  hipLaunchKernelGGL((triatt_proj_ws_kernel<ZT, CT, kC, kHD>), dim3(min(ntiles, resident)),
+                     dim3(256), 0, st, p, ntiles);
 }
 
 // H*32 = 128: the q, k, v channels split over all four waves.

@@ -838,7 +838,9 @@ void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
 template <typename ZT, typename CT, int kC, int kCH>
 void launch_tp_ws_t(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   const int ntiles = p.np * (p.np / kTileRows);
-  hipLaunchKernelGGL((trimul_proj_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, 2 * 256)),
+  static const int resident =
+      resident_grid(reinterpret_cast<const void*>(&trimul_proj_ws_kernel<ZT, CT, kC, kCH>), 256);
+  hipLaunchKernelGGL((trimul_proj_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, resident)),
                      dim3(256), 0, st, p, ntiles);
 }
 template <typename ZT, typename CT>
@@ -855,7 +857,9 @@ bool launch_tp_ws(const TrimulProjArgs<ZT, CT>& p, int C, int ch, hipStream_t st
 template <typename ZT, typename CT, int kC, int kCH>
 void launch_to_ws_t(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
   const int ntiles = p.n * (p.np / kTileRows);
-  hipLaunchKernelGGL((trimul_out_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, 2 * 256)),
+  static const int resident =
+      resident_grid(reinterpret_cast<const void*>(&trimul_out_ws_kernel<ZT, CT, kC, kCH>), 256);
+  hipLaunchKernelGGL((trimul_out_ws_kernel<ZT, CT, kC, kCH>), dim3(min(ntiles, resident)),
                      dim3(256), 0, st, p, ntiles);
 }
 template <typename ZT, typename CT>
