@@ -4,9 +4,11 @@
 // SDPA with scale 1):
 //   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
 //
-// One workgroup of 4 waves per (head, 64 queries); wave w takes queries
-// 16 w .. 16 w + 15.  Key blocks of 64 are staged in LDS as f32 by 16-byte
-// loads (the next block's are loaded into registers while a block is
+// One workgroup per (head, 64 queries); within it, KS groups of 4 waves
+// (KS = 4 for head dims up to 32, else 1) take disjoint ranges of key blocks
+// and merge their partial softmaxes at the end; wave w of a group takes
+// queries 16 w .. 16 w + 15.  Key blocks of 64 are staged in LDS as f32 by
+// 16-byte loads (the next block's are loaded into registers while a block is
 // computed).  Per 16 keys of a block, on the fp32 MFMA
 // (v_mfma_f32_16x16x4_f32, true fp32 products):
 //   S^T[key][query] = K Q^T over head-dim steps of 4 (lane: key l % 16 of the
@@ -38,8 +40,16 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Keys are split over KS groups of four waves (KS = 4 for head dims up to 32,
+// whose K/V blocks are small): group s runs the online softmax over its own
+// range of key blocks with its own LDS staging, and the groups' partial
+// (max, sum, output) are merged in LDS at the end.  With one workgroup per
+// (head, 64 queries) a single group would leave one wave per SIMD.
+template <int D> struct BaSplit { static constexpr int KS = D <= 32 ? 4 : 1; };
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
+__global__ __launch_bounds__(256 * BaSplit<D>::KS) void bias_attn_kernel(BiasAttnArgs a) {
+  constexpr int KS = BaSplit<D>::KS;
   constexpr int NS = D / 4;          // head-dim steps of the QK^T product
   constexpr int NT = (D + 15) / 16;  // 16-dim tiles of the output
   constexpr int LD = D + 1;          // LDS row pitch (floats)
@@ -49,9 +59,10 @@ __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
   constexpr int PER = (CHUNKS + 255) / 256;
   static_assert(D % VEC == 0, "rows of whole 16-byte chunks");
   typedef T tvec __attribute__((ext_vector_type(VEC)));
-  __shared__ float ks[kBaK * LD];
-  __shared__ float vs[kBaK * LD];
-  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  // group s stages its K block at kv + 2 s kBaK LD and its V block right after
+  __shared__ float kv[KS * 2 * kBaK * LD];
+  const int sp = wave_id() / 4, w = wave_id() % 4, tid = threadIdx.x % 256;
+  const int l = lane_id(), g = l >> 4, r16 = l & 15;
   const int h = blockIdx.y, qi = blockIdx.x * 64 + 16 * w + r16;
   const bool qvalid = qi < a.nq;
   const T* qp = static_cast<const T*>(a.q) + h * a.q_sh + (int64_t)(qvalid ? qi : 0) * a.q_sn;
@@ -62,12 +73,16 @@ __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
   const T* vb = static_cast<const T*>(a.v) + h * a.v_sh;
   const float* brow = a.bias ? a.bias + ((int64_t)h * a.nq + (qvalid ? qi : 0)) * a.nk : nullptr;
   const bool bvec = (a.nk & 3) == 0;
+  // this group's key blocks [blk0, blk1); every group runs nbs steps so that
+  // the workgroup's barriers match
+  const int nblk = (a.nk + kBaK - 1) / kBaK, nbs = (nblk + KS - 1) / KS;
+  const int blk0 = sp * nbs, blk1 = min(nblk, blk0 + nbs);
 
   tvec kr[PER], vr[PER];  // the next block's chunks
   auto fetch = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int c = threadIdx.x + 256 * u, key = j0 + c / CPR, d0 = (c % CPR) * VEC;
+      const int c = tid + 256 * u, key = j0 + c / CPR, d0 = (c % CPR) * VEC;
       const bool in = c < CHUNKS && key < a.nk;
       tvec zk, zv;
       for (int e = 0; e < VEC; ++e) zk[e] = zv[e] = (T)0.f;
@@ -79,23 +94,30 @@ __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
   f32x4 o[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  for (int j0 = 0; j0 < a.nk; j0 += kBaK) {
+  if (blk0 < blk1) fetch(blk0 * kBaK);
+  float* kss = kv + 2 * sp * kBaK * LD;
+  float* vss = kss + kBaK * LD;
+  for (int b = 0; b < nbs; ++b) {
+    const int blk = blk0 + b, j0 = blk * kBaK;
+    const bool live = blk < blk1;
     __syncthreads();  // the previous block is no longer read
+    if (live) {
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int c = threadIdx.x + 256 * u;
-      if (c < CHUNKS) {
-        const int key = c / CPR, d0 = (c % CPR) * VEC;
+      for (int u = 0; u < PER; ++u) {
+        const int c = tid + 256 * u;
+        if (c < CHUNKS) {
+          const int key = c / CPR, d0 = (c % CPR) * VEC;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          ks[key * LD + d0 + e] = to_f32(kr[u][e]);
-          vs[key * LD + d0 + e] = to_f32(vr[u][e]);
+          for (int e = 0; e < VEC; ++e) {
+            kss[key * LD + d0 + e] = to_f32(kr[u][e]);
+            vss[key * LD + d0 + e] = to_f32(vr[u][e]);
+          }
         }
       }
     }
     __syncthreads();
-    if (j0 + kBaK < a.nk) fetch(j0 + kBaK);  // in flight during this block
+    if (!live) continue;
+    if (blk + 1 < blk1) fetch(j0 + kBaK);  // in flight during this block
     const int nsub = min(kBaK, a.nk - j0);
     for (int sb = 0; sb < nsub; sb += 16) {
       const int k0 = j0 + sb;
@@ -115,7 +137,7 @@ __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < NS; ++s)  // [key 4g + r][query r16]
-        sacc = mfma4(ks[(sb + r16) * LD + 4 * s + g], qf[s], sacc);
+        sacc = mfma4(kss[(sb + r16) * LD + 4 * s + g], qf[s], sacc);
       float sv[4], bm = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -142,13 +164,45 @@ __global__ __launch_bounds__(256) void bias_attn_kernel(BiasAttnArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const int d = 16 * t + r16;
-          const float vv = d < D ? vs[(sb + 4 * g + kk) * LD + d] : 0.f;
+          const float vv = d < D ? vss[(sb + 4 * g + kk) * LD + d] : 0.f;
           o[t] = mfma4(vv, p[kk], o[t]);  // [dim][query r16]
         }
     }
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+  if constexpr (KS > 1) {
+    // merge the groups' partial softmaxes: groups 1.. leave (m, lsum, o) per
+    // lane in LDS (the staging area, free once every group left its loop) and
+    // group 0 merges them into its own
+    constexpr int W = 2 + 4 * NT;  // floats per lane
+    static_assert((KS - 1) * 256 * W <= KS * 2 * kBaK * LD, "merge area fits the staging area");
+    __syncthreads();
+    if (sp > 0) {
+      float* dst = kv + ((sp - 1) * 256 + w * 64 + l) * W;
+      dst[0] = m;
+      dst[1] = lsum;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[2 + 4 * t + r] = o[t][r];
+    }
+    __syncthreads();
+    if (sp > 0) return;
+#pragma unroll
+    for (int s = 1; s < KS; ++s) {
+      const float* src = kv + ((s - 1) * 256 + w * 64 + l) * W;
+      const float ms = src[0];
+      const float mn = fmaxf(m, ms);  // finite: group 0 always holds key 0
+      const float fa = __builtin_amdgcn_exp2f(m - mn), fb = __builtin_amdgcn_exp2f(ms - mn);
+      lsum = lsum * fa + src[1] * fb;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[t][r] = o[t][r] * fa + src[2 + 4 * t + r] * fb;
+      m = mn;
+    }
+  }
   if (!qvalid) return;
   const float inv = 1.0f / lsum;
   T* op = static_cast<T*>(a.out) + h * a.o_sh + (int64_t)qi * a.o_sn;
@@ -175,7 +229,9 @@ int launch_bias_attn(const odde_bias_attn_args* x, hipStream_t st) {
   dim3 grid((x->n_q + 63) / 64, x->heads);
   switch (x->head_dim) {
 #define ODDE_BA(D) \
-    case D: hipLaunchKernelGGL((bias_attn_kernel<T, D>), grid, dim3(256), 0, st, a); break;
+    case D:                                                                            \
+      hipLaunchKernelGGL((bias_attn_kernel<T, D>), grid, dim3(256 * BaSplit<D>::KS), 0, st, a); \
+      break;
     ODDE_BA(8) ODDE_BA(16) ODDE_BA(24) ODDE_BA(32) ODDE_BA(48) ODDE_BA(64)
 #undef ODDE_BA
     default: return set_error(ODDE_EUNSUPPORTED, "bias_attn: head_dim in {8, 16, 24, 32, 48, 64}");

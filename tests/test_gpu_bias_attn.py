@@ -37,7 +37,9 @@ def _expected(q, k, v, b):
 
 
 @pytest.mark.parametrize("h,nq,nk,d", [(3, 17, 130, 24), (2, 64, 64, 8), (4, 100, 37, 16),
-                                       (1, 129, 200, 32), (2, 70, 65, 48), (2, 33, 128, 64)])
+                                       (1, 129, 200, 32), (2, 70, 65, 48), (2, 33, 128, 64),
+                                       # key blocks split unevenly over the four key groups
+                                       (2, 40, 300, 32), (1, 64, 513, 24)])
 def test_bias_attention_fp32_matches_oracle(h, nq, nk, d):
     say(f"[gpu] bias attn h={h} nq={nq} nk={nk} d={d}")
     q, k, v, b = _inputs(h, nq, nk, d, 10 + nq + d)
