@@ -380,14 +380,23 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
       issue(tile + gridDim.x);  // raw is free again
       mfetch(tile + gridDim.x);
     }
+    // Row block rb covers tile rows 32 (rb >> 1) + 8 (m >> 2) + 4 (rb & 1) + (m & 3)
+    // for MFMA row m, so a lane's outputs of row blocks 2p and 2p + 1 are the
+    // 8 consecutive rows 32 p + 8 g .. + 7 of one channel: one 16-byte store.
     bf16x4 ov[kTileRows / 16][NB];
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
+      const int rbase = 32 * (rb >> 1) + 4 * (rb & 1);
       Frag<CT> xf[kC];
-      tile_frags<CT, C>(xs, rb, xf);
+      {
+        constexpr int LD = TileLD<CT, C>::value;
+        const CT* row = xs + (rbase + 8 * (r16 >> 2) + (r16 & 3)) * LD + 8 * g;
+#pragma unroll
+        for (int t = 0; t < kC; ++t) xf[t].load(row + 32 * t);
+      }
       float mk[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) mk[e] = mk_s[rb * 16 + 4 * g + e];
+      for (int e = 0; e < 4; ++e) mk[e] = mk_s[rbase + 8 * g + e];
 #pragma unroll
       for (int cb = 0; cb < NB; ++cb) {
         f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap;
@@ -402,12 +411,18 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next raw tile (own part) landed
 #pragma unroll
-    for (int rb = 0; rb < kTileRows / 16; ++rb) {
-      const int yb = y0 + rb * 16 + 4 * g;
+    for (int p = 0; p < kTileRows / 32; ++p) {
+      const int yb = y0 + 32 * p + 8 * g;
 #pragma unroll
       for (int cb = 0; cb < NB; ++cb) {
         const int c = half * (CH / 2) + cb * 16 + r16;
-        *reinterpret_cast<bf16x4*>(dst + ((size_t)c * np + x) * np + yb) = ov[rb][cb];
+        bf16x8 v8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v8[e] = ov[2 * p][cb][e];
+          v8[4 + e] = ov[2 * p + 1][cb][e];
+        }
+        *reinterpret_cast<bf16x8*>(dst + ((size_t)c * np + x) * np + yb) = v8;
       }
     }
     lds_barrier();  // every wave's part of the next raw tile landed; xs, mk_s free
