@@ -486,16 +486,30 @@ __device__ __forceinline__ void proj_ws4_role(const TriattProjArgs<ZT, CT>& a, c
 #pragma unroll
     for (int ob = 0; ob < 6; ++ob) {
       const int gc = 96 * W + 16 * ob, mat = gc >> 7, ch = gc & 127;
-      CT* dst;
+      bf16x8 v8;
       if (mat == 2) {
+        // keys 4g..4g+3 of row block rb and the same keys + 16 of row block
+        // rb + 1 fill one 16-byte slot group of the V fragment layout
+        if (rb & 1) continue;
         const int o = ch + r16;
-        dst = a.v + vperm_offset(i, o >> 5, H, jp, j0 + rb * 16 + 4 * g, o & 31);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v8[e] = out[rb][ob][e];
+          v8[4 + e] = out[rb + 1][ob][e];
+        }
+        *reinterpret_cast<bf16x8*>(a.v + vperm_offset(i, o >> 5, H, jp, j0 + rb * 16 + 4 * g,
+                                                      o & 31)) = v8;
       } else {
-        const int o = ch + 4 * g;
-        dst = (mat ? a.k : a.q) + (((size_t)i * H + (o >> 5)) * jp + j0 + rb * 16 + r16) * 32 +
-              (o & 31);
+        if (ch & 16) continue;  // stored with the head's first block
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v8[e] = out[rb][ob][e];
+          v8[4 + e] = out[rb][ob + 1][e];
+        }
+        *reinterpret_cast<bf16x8*>((mat ? a.k : a.q) +
+                                   (((size_t)i * H + (ch >> 5)) * jp + j0 + rb * 16 + r16) * 32 +
+                                   8 * g) = v8;
       }
-      *reinterpret_cast<bf16x4*>(dst) = out[rb][ob];
     }
     if (W == 0 && r16 < H)
       *reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g) =
@@ -532,13 +546,22 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws4_kernel(TriattProjArgs<
     lnp[t] = a.ln_w[t];
     lnp[C + t] = a.ln_b[t];
   }
+  // q, k: output block ob of a head (the head's 32 channels in two blocks)
+  // computes channels 8 (m >> 2) + 4 (ob & 1) + (m & 3) for MFMA row m, so a
+  // lane's results of the two blocks are 8 consecutive channels (one 16-byte
+  // store); v keeps the natural order (its lanes hold channels)
   Frag<CT> wf[6][kC];
+  {
+    const int r16 = l & 15, g = l >> 4;
 #pragma unroll
-  for (int ob = 0; ob < 6; ++ob) {
-    const int gc = 96 * wu + 16 * ob, mat = gc >> 7;
-    const CT* W = mat == 0 ? a.wq : mat == 1 ? a.wk : a.wv;
+    for (int ob = 0; ob < 6; ++ob) {
+      const int gc = 96 * wu + 16 * ob, mat = gc >> 7, ch = gc & 127;
+      const CT* W = mat == 0 ? a.wq : mat == 1 ? a.wk : a.wv;
+      const int row = mat == 2 ? ch + r16
+                               : (ch & ~31) + 8 * (r16 >> 2) + 4 * ((ch >> 4) & 1) + (r16 & 3);
 #pragma unroll
-    for (int t = 0; t < kC; ++t) load_w_frag(W, C, gc & 127, HD, t, wf[ob][t]);
+      for (int t = 0; t < kC; ++t) wf[ob][t].load(W + (size_t)row * C + 32 * t + 8 * g);
+    }
   }
   Frag<CT> wbf[kC];
 #pragma unroll
