@@ -32,8 +32,9 @@
 // Workspace layouts (CT = compute type, Jp = N rounded up to 64, I = rows):
 //   q, k, gate : [I][H][Jp][32]           (no gate plane on the weight-stationary path)
 //   v          : [I][H][Jp/32][2][64][8]  MFMA-ready V^T fragments: per block
-//                of 32 keys, channel half db, lane (d%16 + 16*g), slot e holds
-//                key 4g+e (e<4) or 16+4g+(e-4) (e>=4)
+//                of 32 keys, channel half db, lane (m + 16*g) with channel
+//                d = 8 (m >> 2) + 4 db + (m & 3), slot e holds key 4g+e (e<4)
+//                or 16+4g+(e-4) (e>=4)
 //   keep       : [I][Jp/32][4][8]          the same key-slot order, 1 = kept
 //   bias       : [Bb][H][Jp][Jp] f32       log2e-scaled tri bias (Bb batches)
 //   mb         : [I][Jp] f32               log2e-scaled additive mask, -inf pads
@@ -76,7 +77,10 @@ __device__ __forceinline__ float lanes16_max(float v) {
 __device__ __forceinline__ size_t vperm_offset(int row, int h, int heads, int jp, int j, int d) {
   const int kb = j >> 5, jj = j & 31;
   const int half = jj >> 4, gp = (jj & 15) >> 2, e = 4 * half + (jj & 3);
-  const int db = d >> 4, dl = d & 15;
+  // channel d = 8 (dl >> 2) + 4 db + (dl & 3): the PV accumulator row m of
+  // channel half db is channel 8 (m >> 2) + 4 db + (m & 3), so a lane's two
+  // halves hold 8 consecutive channels of its query (one 16-byte store)
+  const int db = (d >> 2) & 1, dl = 4 * (d >> 3) + (d & 3);
   return (((((size_t)row * heads + h) * (jp >> 5) + kb) * 2 + db) * 64 + dl + 16 * gp) * 8 + e;
 }
 // slot (g, e) of a 32-key block -> key offset within the block
@@ -648,6 +652,7 @@ struct TriattCoreArgs {
   CT* out;
   int64_t o_row, o_h, o_j;  // element strides of out[row][h][q][d]
   int rows, heads, n, jp, rows_per_bias;
+  int out16;  // bf16 out with every (row, h, q) start 16-byte aligned
 };
 
 // Row sums of the probabilities: bf16 pairs through v_dot2 (the same rounded
@@ -691,19 +696,33 @@ __device__ __forceinline__ void core_store(const TriattCoreArgs<CT>& a, int row0
     for (int qb = 0; qb < QB; ++qb) {
       const int qq = q0 + 16 * qb + r16;
       if (row >= a.rows || qq >= a.n) continue;
+      // lane (g, r16) holds channels 8g .. 8g + 7 of query qq: half db gives
+      // 8g + 4db + e (the V fragment channel order)
+      float ov[8];
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const int d0 = 16 * db + 4 * g;
-        float ov[4];
-        for (int e = 0; e < 4; ++e) ov[e] = o[r][db][qb][e] * inv[r][qb];
-        if (a.gate) {
-          float gv[4];
-          load4(a.gate + (((size_t)row * a.heads + h) * a.jp + qq) * 32 + d0, gv);
-          for (int e = 0; e < 4; ++e) ov[e] *= gv[e];
-        }
-        store4(a.out + (int64_t)row * a.o_row + (int64_t)h * a.o_h + (int64_t)qq * a.o_j + d0,
-               ov[0], ov[1], ov[2], ov[3]);
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[4 * db + e] = o[r][db][qb][e] * inv[r][qb];
+      if (a.gate) {
+        const CT* gp = a.gate + (((size_t)row * a.heads + h) * a.jp + qq) * 32 + 8 * g;
+        float gv[8];
+        load4(gp, gv);
+        load4(gp + 4, gv + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ov[e] *= gv[e];
       }
+      CT* dst = a.out + (int64_t)row * a.o_row + (int64_t)h * a.o_h + (int64_t)qq * a.o_j + 8 * g;
+      if constexpr (sizeof(CT) == 2) {
+        if (a.out16) {
+          bf16x8 v8;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v8[e] = (bf16)ov[e];
+          *reinterpret_cast<bf16x8*>(dst) = v8;
+          continue;
+        }
+      }
+      store4(dst, ov[0], ov[1], ov[2], ov[3]);
+      store4(dst + 4, ov[4], ov[5], ov[6], ov[7]);
     }
   }
 }
@@ -995,7 +1014,7 @@ __global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<C
       for (int k0 = 0; k0 < jp; k0 += 32) {
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
-          Frag<CT> vf;  // lane: channel 16*db + r16, keys k0 + slot_key(g, e)
+          Frag<CT> vf;  // lane: channel half db, row r16; keys k0 + slot_key(g, e)
           vf.load(Vr + (size_t)(k0 >> 5) * 1024 + (db * 64 + l) * 8);
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -1795,7 +1814,10 @@ void launch_core_t(const TriattCoreArgs<CT>& p, hipStream_t st) {
 }
 
 template <typename CT>
-int launch_core(const TriattCoreArgs<CT>& p, int batches, hipStream_t st) {
+int launch_core(const TriattCoreArgs<CT>& p0, int batches, hipStream_t st) {
+  TriattCoreArgs<CT> p = p0;
+  p.out16 = sizeof(CT) == 2 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 &&
+            ((p.o_row | p.o_h | p.o_j) & 7) == 0;
   const CoreTile t = core_tile(p.rows_per_bias, batches, sizeof(CT) == 4);
   LaunchScope ls(ODDE_K_TRIATT_CORE, st);
 #define ODDE_TILE(R, QB, RG, QS)                                              \
