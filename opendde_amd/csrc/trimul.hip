@@ -609,8 +609,9 @@ struct TrimulWideProjArgs {
 // Output rows of the GEMM are the 4*Ch projections interleaved in 16-row
 // blocks [a_p | a_g | a_p | a_g ... | b_p | b_g ...] (read in place through
 // the row functor, no copy), so a wave's fragments j (value) and j + 1
-// (gate) hold the same 16 channels.  Accumulator: one channel, four
-// consecutive pairs per lane -> 8-byte stores into the channel-major planes.
+// (gate) hold the same 16 channels.  Accumulator: one channel, four pairs
+// per lane per row block; two row blocks give 8 consecutive pairs -> 16-byte
+// stores into the channel-major planes.
 __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArgs a, int ncol) {
   __shared__ __attribute__((aligned(16))) bf16 sm[kWNS * WideShape::STAGE_ELEMS];
   int rt, ct;
@@ -619,8 +620,16 @@ __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArg
   const int y0 = ct * kWTY;
   const int C = a.c, CH = a.ch, np = a.np;
   f32x4 acc[WideShape::MX][WideShape::MY];
+  // Tile row r (staged in LDS row r) is pair x0 + wide_pair_perm(r): within
+  // each 32 rows, row block 2p + b, MFMA row m is pair 8 (m >> 2) + 4 b +
+  // (m & 3), so a lane's results of row blocks 2p and 2p + 1 are 8
+  // consecutive pairs of one channel (one 16-byte store).
+  auto wide_pair_perm = [](int r) {
+    const int m = r & 15;
+    return (r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3);
+  };
   gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false, kWKC>(
-      [&](int r) { return a.zn + (x0 + r) * C; },
+      [&](int r) { return a.zn + (x0 + wide_pair_perm(r)) * C; },
       [&](int r) {
         const int R = y0 + r, side = R / (2 * CH), within = R % (2 * CH), t = within & 31;
         const int chan = side * CH + (within >> 5) * 16 + (t & 15);
@@ -629,13 +638,15 @@ __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArg
       C, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % kWWX, wy = w / kWWX;
+  static_assert(WideShape::MX % 2 == 0 && (kWTX / kWWX) % 32 == 0, "row blocks pair up");
 #pragma unroll
-  for (int i = 0; i < WideShape::MX; ++i) {
-    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3, one row x
+  for (int i = 0; i < WideShape::MX; i += 2) {
+    // pairs m .. m+7 (one row x): row blocks i (m..m+3) and i + 1 (m+4..m+7)
+    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 8 * g;
     const int x = (int)(m / np), y = (int)(m % np);
-    float mk[4];
+    float mk[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int e = 0; e < 8; ++e)
       mk[e] = (x < a.n && y + e < a.n)
                   ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)(y + e) * a.m_s1] : 1.0f)
                   : 0.f;
@@ -643,10 +654,13 @@ __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArg
     for (int j = 0; j < WideShape::MY; j += 2) {
       const int R = y0 + wy * (kWTY / WideShape::WY) + 16 * j;  // first row of the value block
       const int side = R / (2 * CH), chan = ((R % (2 * CH)) >> 5) * 16 + r16;
-      bf16x4 v;
+      bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (bf16)(mk[e] * sigmoidf_(acc[i][j + 1][e]) * acc[i][j][e]);
-      *reinterpret_cast<bf16x4*>((side ? a.B : a.A) + ((size_t)chan * np + x) * np + y) = v;
+      for (int e = 0; e < 4; ++e) {
+        v[e] = (bf16)(mk[e] * sigmoidf_(acc[i][j + 1][e]) * acc[i][j][e]);
+        v[4 + e] = (bf16)(mk[4 + e] * sigmoidf_(acc[i + 1][j + 1][e]) * acc[i + 1][j][e]);
+      }
+      *reinterpret_cast<bf16x8*>((side ? a.B : a.A) + ((size_t)chan * np + x) * np + y) = v;
     }
   }
 }
