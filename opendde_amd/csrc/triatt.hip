@@ -1527,35 +1527,51 @@ __global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT
   const int wx = w % kWWX, wy = w / kWWX;
   auto arow = [&](int r) { return zn + (x0 + r) * C; };
   auto brow = [&](int r) { return W + (size_t)(o0 + r) * C; };
+  // q, k, gate: within each 32 weight rows (one head), row block 2p + b, MFMA
+  // row m is channel 8 (m >> 2) + 4 b + (m & 3), so a lane's results of the
+  // head's two row blocks are 8 consecutive channels (one 16-byte store)
+  auto brow_perm = [&](int r) {
+    const int m = r & 15;
+    return W + (size_t)(o0 + (r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * C;
+  };
   f32x4 acc[WideShape::MX][WideShape::MY];
+  static_assert(WideShape::MX % 2 == 0 && WideShape::MY % 2 == 0, "row blocks pair up");
   if (type == 2) {  // v: channel-per-lane orientation
     gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, false, kWKC>(arow, brow, C, sm, acc);
+    // row blocks i and i + 1 hold keys 4g..4g+3 and the same keys + 16 of a
+    // 32-key block: one 16-byte slot group of the V layout
 #pragma unroll
-    for (int i = 0; i < WideShape::MX; ++i) {
-      const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3
+    for (int i = 0; i < WideShape::MX; i += 2) {
+      const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 4 * g;  // pairs m .. m+3, m+16 ..
       const int row = (int)(m / jp), jj = (int)(m % jp);
       if (row >= n) continue;
-      float vk[4] = {1.f, 1.f, 1.f, 1.f};
+      float vk[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
       if (a.anykeep[row] != 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float mv = jj + e < n ? (a.mask ? a.mask[(int64_t)row * a.m_s0 +
-                                                         (int64_t)(jj + e) * a.m_s1]
-                                                : 1.0f)
-                                      : 0.f;
+        for (int e = 0; e < 8; ++e) {
+          const int key = jj + (e & 3) + 16 * (e >> 2);
+          const float mv = key < n ? (a.mask ? a.mask[(int64_t)row * a.m_s0 +
+                                                      (int64_t)key * a.m_s1]
+                                             : 1.0f)
+                                   : 0.f;
           vk[e] = mv == 1.0f ? 1.f : 0.f;
         }
       }
 #pragma unroll
       for (int j = 0; j < WideShape::MY; ++j) {
         const int o = o0 + wy * (kWTY / WideShape::WY) + 16 * j + r16;
-        store4(a.v + vperm_offset(row, o >> 5, H, jp, jj, o & 31), acc[i][j][0] * vk[0],
-               acc[i][j][1] * vk[1], acc[i][j][2] * vk[2], acc[i][j][3] * vk[3]);
+        bf16x8 v8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v8[e] = (bf16)(acc[i][j][e] * vk[e]);
+          v8[4 + e] = (bf16)(acc[i + 1][j][e] * vk[4 + e]);
+        }
+        *reinterpret_cast<bf16x8*>(a.v + vperm_offset(row, o >> 5, H, jp, jj, o & 31)) = v8;
       }
     }
     return;
   }
-  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(arow, brow, C, sm, acc);
+  gemm_nt_mainloop<kWTX, kWTY, kWWX, kWNS, true, kWKC>(arow, brow_perm, C, sm, acc);
   // the wave's 64 pairs lie in one row (Jp and the offsets are multiples of 64)
   const int64_t mw = x0 + wx * (kWTX / kWWX);
   const int row = (int)(mw / jp);
@@ -1567,18 +1583,31 @@ __global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT
     const int jj = (int)((mw + 16 * i + r16) % jp);
     float ss[2] = {0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < WideShape::MY; ++j) {
-      const int o = ob + 16 * j + 4 * g;
+    for (int j = 0; j < WideShape::MY; j += 2) {
+      const int o = ob + 16 * j + 8 * g;  // 8 channels: block j gives o..o+3, j + 1 o+4..o+7
       const size_t off = (((size_t)row * H + (o >> 5)) * jp + jj) * 32 + (o & 31);
-      const f32x4 v = acc[i][j];
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = acc[i][j][e];
+        v[4 + e] = acc[i][j + 1][e];
+      }
+      bf16x8 v8;
       if (type == 0) {
-        const float sc = a.q_scale;
-        store4(a.q + off, v[0] * sc, v[1] * sc, v[2] * sc, v[3] * sc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v8[e] = (bf16)(v[e] * a.q_scale);
+        *reinterpret_cast<bf16x8*>(a.q + off) = v8;
       } else if (type == 1) {
-        store4(a.k + off, v[0], v[1], v[2], v[3]);
-        ss[j >> 1] += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v8[e] = (bf16)v[e];
+          ss[j >> 1] += v[e] * v[e];
+        }
+        *reinterpret_cast<bf16x8*>(a.k + off) = v8;
       } else {
-        store4(a.gate + off, sigmoidf_(v[0]), sigmoidf_(v[1]), sigmoidf_(v[2]), sigmoidf_(v[3]));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v8[e] = (bf16)sigmoidf_(v[e]);
+        *reinterpret_cast<bf16x8*>(a.gate + off) = v8;
       }
     }
     if (type == 1) {
