@@ -204,20 +204,36 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
   f32x4 acc[S::MX][S::MY];
   const bf16* Ab = a.A + c * plane + (size_t)x0 * a.np;
   const bf16* Bb = a.B + c * plane + (size_t)y0 * a.np;
-  gemm_nt_mainloop<TX, TY, WX, NS, true, KC>([&](int r) { return Ab + (size_t)r * a.np; },
-                                         [&](int r) { return Bb + (size_t)r * a.np; }, a.np, sm,
-                                         acc);
-  // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16), rows y = y0 + wy*TY/WY + 16j + 4g + r
+  // B row r of the tile (staged in LDS row r) is column y0 + perm(r): within
+  // each 32 rows, row block 2p + b, MFMA row m is column 8 (m >> 2) + 4 b +
+  // (m & 3), so a lane's results of row blocks 2p and 2p + 1 are 8
+  // consecutive columns (one 16-byte store)
+  gemm_nt_mainloop<TX, TY, WX, NS, true, KC>(
+      [&](int r) { return Ab + (size_t)r * a.np; },
+      [&](int r) {
+        const int m = r & 15;
+        return Bb + (size_t)((r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * a.np;
+      },
+      a.np, sm, acc);
+  // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16); rows = columns
+  // y0 + wy*TY/WY + 16 (j & ~1) + 8g + 4 (j & 1) + r
+  static_assert(S::MY % 2 == 0 && (TY / S::WY) % 32 == 0, "row blocks pair up");
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % WX, wy = w / WX;
   bf16* Pb = a.P + c * plane;
 #pragma unroll
   for (int i = 0; i < S::MX; ++i)
 #pragma unroll
-    for (int j = 0; j < S::MY; ++j) {
+    for (int j = 0; j < S::MY; j += 2) {
       const int xx = x0 + wx * (TX / WX) + i * 16 + r16;
-      const int yy = y0 + wy * (TY / S::WY) + j * 16 + 4 * g;
-      store4(Pb + (size_t)xx * a.np + yy, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      const int yy = y0 + wy * (TY / S::WY) + j * 16 + 8 * g;
+      bf16x8 v8;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v8[e] = (bf16)acc[i][j][e];
+        v8[4 + e] = (bf16)acc[i][j + 1][e];
+      }
+      *reinterpret_cast<bf16x8*>(Pb + (size_t)xx * a.np + yy) = v8;
     }
 }
 
