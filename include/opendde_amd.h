@@ -177,7 +177,9 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  * 182-217, whose flat row chunking is numerically neutral):
  *   y = LN(x); out = (add_residual ? x : 0) + (silu(y W_a^T) * (y W_b^T)) W_o^T
  * x, out: [rows][c] contiguous (out may alias x); W_a, W_b: [n*c][c],
- * W_o: [c][n*c] in compute_dtype (bf16 only); LN params f32.
+ * W_o: [c][n*c] in compute_dtype; LN params f32.  c in {64, 128, 256, 384},
+ * n = 4.  compute_dtype ODDE_BF16 takes f32 or bf16 rows; ODDE_F32 (true
+ * fp32 products) takes f32 rows.
  * Optional (pb_heads = 16; 0 = off): the pair-bias projection that the single
  * track's AttentionPairBias takes from the updated pair tensor
  * (linear_nobias_z(layernorm_z(z)), opendde/model/modules/transformer.py:
@@ -185,10 +187,10 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  *   pb_out[h][r] = sum_c LN'(out[r])[c] * pb_w[h][c]     (f32, [16][rows])
  * with LN' = LayerNorm(pb_ln_w, pb_ln_b (may be NULL), pb_eps); pb_w is
  * [16][c] in compute_dtype.  This saves the separate pass over all of z.
- * Wide rows (c = 384) run as a LayerNorm pass and two GEMMs whose hidden
- * activations live in the workspace (odde_transition_workspace_bytes; 0 for
- * the fused kernels, which need none), and the pair-bias projection as a pass
- * over the rows written.
+ * Wide rows (c = 384) in bf16 arithmetic run as a LayerNorm pass and two
+ * GEMMs whose hidden activations live in the workspace
+ * (odde_transition_workspace_bytes; 0 for the fused kernels, which need
+ * none), and the pair-bias projection as a pass over the rows written.
  */
 typedef struct odde_transition_args {
   uint32_t struct_size;

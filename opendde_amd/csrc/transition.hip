@@ -509,6 +509,87 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   }
 }
 
+// fp32 arithmetic (true fp32 products on v_mfma_f32_16x16x4_f32), any C in
+// {64, 128, 256, 384}, n = 4.  A workgroup of 4 waves owns 16 rows at a time;
+// every wave LayerNorms the 16 rows into K32 fragments (registers) and takes
+// every fourth hidden chunk (wave w: chunks w, w + 4, ...), keeping a partial
+// 16 x C output in registers.  Waves 1..3 hand their partials to wave 0
+// through LDS, which sums them in a fixed order (deterministic), adds the
+// residual, stores, and forms the pair bias from the stored values.  Weight
+// fragments come straight from global memory: the whole weight set (12 C^2
+// floats, <= 7 MB) stays resident in L2 and the rows of a workgroup read it
+// once.  Splitting the hidden dimension over the waves keeps short row counts
+// (the single track's N rows) spread over 4x more waves than a row split.
+template <typename ZT, int kC>
+__global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, float> a,
+                                                             int64_t nblk) {
+  constexpr int C = kC * 32, HID = 4 * C, NCB = C / 16, NCHUNK = HID / kTrHid;
+  static_assert(NCHUNK % 4 == 0, "hidden chunks split evenly over the 4 waves");
+  __shared__ f32x4 part[3][NCB][64];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int64_t row = b * 16 + r16;
+    const bool valid = row < a.rows;
+    Frag<float> xf[kC];
+    ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
+                                   xf);
+    f32x4 acc[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hc = w; hc < NCHUNK; hc += 4) {
+      const int h0 = hc * kTrHid;
+      // GEMM1 (W x^T orientation): lane (g, r16) ends with hidden units
+      // h0 + 16 hb + 4g + e of row r16 -- slot 4 hb + e of a B fragment
+      Frag<float> hf;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+          Frag<float> fa, fb;
+          load_w_frag(a.wa, C, h0 + 16 * hb, HID, t, fa);
+          load_w_frag(a.wb, C, h0 + 16 * hb, HID, t, fb);
+          mma(sa, fa, xf[t]);
+          mma(sb, fb, xf[t]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
+      }
+      // GEMM2: W_o[c][h0 + slot] with the same slot -> hidden map
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const float* wrow = a.wo + (size_t)(cb * 16 + r16) * HID + h0;
+        Frag<float> fo;
+        fo.lo = *reinterpret_cast<const f32x4*>(wrow + 4 * g);
+        fo.hi = *reinterpret_cast<const f32x4*>(wrow + 16 + 4 * g);
+        mma(acc[cb], fo, hf);
+      }
+    }
+    if (w) {
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) part[w - 1][cb][l] = acc[cb];
+    }
+    __syncthreads();
+    if (w == 0) {
+      // lane holds row r16, channels cb*16 + 4g + e
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc[cb] += part[k][cb][l];
+        const int c0 = cb * 16 + 4 * g;
+        float base[4] = {0.f, 0.f, 0.f, 0.f};
+        if (valid && a.add) load4(a.x + row * C + c0, base);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[cb][e] += base[e];
+        if (valid) store4(a.out + row * C + c0, acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
+      }
+      if (a.pb_out)
+        pair_bias_epilogue<ZT, float, kC>(a, acc, row, valid, a.pb_ln_w, a.pb_ln_b, a.pb_w);
+    }
+    __syncthreads();  // part is reused by the next row block
+  }
+}
+
 // Wide form (C = 384): a LayerNorm pass into bf16 rows, then two NT GEMMs on
 // the shared mainloop (gemm.hpp) with the hidden activations in the
 // workspace:  h = silu(y W_a^T) * (y W_b^T)  ([Mp][4C] bf16), then
@@ -689,6 +770,33 @@ int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
   return check_launch("transition (wide)");
 }
 
+int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
+  TransitionArgs<float, float> p;
+  p.x = static_cast<const float*>(a->x);
+  p.out = static_cast<float*>(a->out);
+  p.ln_w = a->ln_w; p.ln_b = a->ln_b;
+  p.wa = static_cast<const float*>(a->w_a);
+  p.wb = static_cast<const float*>(a->w_b);
+  p.wo = static_cast<const float*>(a->w_o);
+  p.rows = a->rows; p.add = a->add_residual; p.eps = a->eps;
+  p.pb_ln_w = a->pb_ln_w; p.pb_ln_b = a->pb_ln_b;
+  p.pb_w = static_cast<const float*>(a->pb_w);
+  p.pb_out = a->pb_heads ? a->pb_out : nullptr;
+  p.pb_eps = a->pb_eps;
+  p.pb_zero = nullptr;
+  const int64_t nblk = (p.rows + 15) / 16;
+  const int grid = (int)std::min<int64_t>(nblk, 8 * 256);
+  LaunchScope ls(ODDE_K_TRANSITION, st);
+  switch (a->c) {
+    case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 384: hipLaunchKernelGGL((transition_f32_kernel<float, 12>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    default: return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256, 384} with n = 4");
+  }
+  return check_launch("transition (fp32)");
+}
+
 template <typename ZT, typename CT>
 int run_transition(const odde_transition_args* a, hipStream_t st) {
   if (transition_wide(a->c, a->n_factor, a->compute_dtype)) return run_transition_wide<ZT>(a, st);
@@ -740,8 +848,10 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
     return set_error(ODDE_EUNSUPPORTED, "transition: at most 2^31 - 1 rows per call");
   if (!valid_dtype(a->x_dtype) || !valid_dtype(a->compute_dtype))
     return set_error(ODDE_EINVAL, "transition: bad dtype");
-  if (a->compute_dtype != ODDE_BF16)
-    return set_error(ODDE_EUNSUPPORTED, "transition: the fused kernel computes in bf16");
+  if (a->compute_dtype == ODDE_F32 && a->x_dtype != ODDE_F32)
+    return set_error(ODDE_EUNSUPPORTED, "transition: fp32 arithmetic needs float32 rows");
+  if (a->n_factor != 4 || (a->c != 64 && a->c != 128 && a->c != 256 && a->c != 384))
+    return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256, 384} with n = 4");
   if (!a->x || !a->out || !a->ln_w || !a->ln_b || !a->w_a || !a->w_b || !a->w_o)
     return set_error(ODDE_EINVAL, "transition: null tensor pointer");
   if ((reinterpret_cast<uintptr_t>(a->x) | reinterpret_cast<uintptr_t>(a->out)) & 15)
@@ -762,6 +872,7 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
   }
   if (a->rows == 0) return ODDE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->compute_dtype == ODDE_F32) return run_transition_f32(a, st);
   if (a->x_dtype == ODDE_F32) return run_transition<float, bf16>(a, st);
   return run_transition<bf16, bf16>(a, st);
 }

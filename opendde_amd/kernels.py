@@ -289,10 +289,12 @@ TRANSITION_CHANNELS = (64, 128, 256, 384)
 
 def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torch.Tensor] = None,
                add_residual: bool = False, eps: float = 1e-5,
-               pair_bias: Optional[tuple] = None) -> torch.Tensor:
-    """Fused SwiGLU transition over the last dim of ``x`` (bf16 arithmetic):
+               pair_bias: Optional[tuple] = None,
+               compute_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Fused SwiGLU transition over the last dim of ``x``:
     out = (x if add_residual else 0) + W_o(silu(W_a LN(x)) * W_b LN(x)).
-    ``out`` may be ``x`` (in-place residual update).
+    ``out`` may be ``x`` (in-place residual update).  Arithmetic is bf16 for
+    bf16 ``x`` or under bf16 autocast, fp32 otherwise (float32 ``x``).
 
     ``pair_bias = (ln_w, ln_b, w, eps, dest)`` also writes
     ``dest[h, r] = (LN(out[r]) @ w.T)[h]`` (w: [16, c], dest: float32
@@ -309,13 +311,16 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
         out = torch.empty_like(x)
     if not out.is_contiguous() or out.shape != x.shape or out.dtype != x.dtype:
         raise ValueError("out must be a contiguous tensor like x")
-    bf = torch.bfloat16
+    ct = compute_dtype or autocast_compute_dtype(x)
+    if x.dtype == torch.bfloat16 and ct == torch.float32:
+        raise NotImplementedError("bf16 storage with fp32 compute is not provided")
+    bf = ct
     keep = [prepared(ln_w, torch.float32), prepared(ln_b, torch.float32),
             prepared(w_a, bf), prepared(w_b, bf), prepared(w_o, bf)]
     a = _lib.TransitionArgs()
     a.struct_size = ctypes.sizeof(_lib.TransitionArgs)
     a.c, a.n_factor = c, nf
-    a.x_dtype, a.compute_dtype = dtype_code(x.dtype), _lib.BF16
+    a.x_dtype, a.compute_dtype = dtype_code(x.dtype), dtype_code(ct)
     a.add_residual = 1 if add_residual else 0
     a.rows = x.numel() // c
     a.x, a.out = _ptr(x), _ptr(out)
@@ -433,7 +438,11 @@ def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             raise ValueError("q, k, v need a contiguous head dim")
     es = q.element_size()
     if any((t.data_ptr() | t.stride(0) * es | t.stride(1) * es) & 15 for t in (k, v)):
-        k, v = k.contiguous(), v.contiguous()  # rows must start on 16-byte boundaries
+        # rows must start on 16-byte boundaries: a fresh allocation is 256-byte
+        # aligned (.contiguous() would return a contiguous but misaligned view
+        # unchanged)
+        k = k.clone(memory_format=torch.contiguous_format)
+        v = v.clone(memory_format=torch.contiguous_format)
     b = None
     if bias is not None:
         b = bias.to(torch.float32).expand(h, nq, nk).contiguous()

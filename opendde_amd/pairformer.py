@@ -6,8 +6,12 @@ With an accelerated triangle kernel value on GPU tensors the block runs the
 fused HIP kernels with the residual add folded in, in place when
 ``inplace_safe``; the ending-node attention reads and writes z through
 transposed strides instead of the reference's two full transposed copies of z
-(pairformer.py:218-226).  The pair transition and the single track run as
-PyTorch ops.
+(pairformer.py:218-226).  The pair and single transitions run as fused HIP
+kernels (bf16 or fp32 arithmetic); the pair transition's epilogue also forms
+the single track's 16-head pair bias from the rows it writes, and the single
+track's attention core runs on the HIP fp32 bias-attention kernel.  The
+single track's small s-side projections (LayerNorm and linears over N x 384)
+stay PyTorch ops.
 """
 
 from __future__ import annotations
@@ -44,10 +48,12 @@ class Transition(nn.Module):
                                            initializer="zeros")
 
     def hip_supported(self, x: torch.Tensor) -> bool:
-        """The fused HIP kernel runs bf16 arithmetic: bf16 inputs, or float32
-        inputs under bf16 autocast (the reference's bf16 mode)."""
+        """The fused HIP kernels take n = 4 and c in ``K.TRANSITION_CHANNELS``,
+        in bf16 arithmetic (bf16 inputs, or float32 inputs under bf16
+        autocast, the reference's bf16 mode) or fp32 arithmetic (float32
+        inputs without autocast)."""
         return (x.is_cuda and self.n == 4 and self.c_in in K.TRANSITION_CHANNELS
-                and K.autocast_compute_dtype(x) == torch.bfloat16 and x.is_contiguous())
+                and x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous())
 
     def hip_apply(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                   add_residual: bool = False, pair_bias: Optional[tuple] = None) -> torch.Tensor:
@@ -76,7 +82,7 @@ class Transition(nn.Module):
             del a
             b = self.linear_no_bias(b)
             if outputs is None:
-                outputs = torch.empty((xf.shape[0], self.c_in), dtype=b.dtype, device=b.device)
+                outputs = torch.empty((xf.shape[0], self.c_in), dtype=x.dtype, device=x.device)
             outputs[start:start + b.shape[0]] = b
             start += b.shape[0]
         return outputs.reshape(*other, self.c_in)

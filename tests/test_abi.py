@@ -89,6 +89,14 @@ def test_bad_arguments_return_status_and_message():
     tr.x_dtype, tr.compute_dtype = 0, 1
     for f in ("x", "out", "ln_w", "ln_b", "w_a", "w_b", "w_o"):
         setattr(tr, f, ctypes.c_void_p(0x1000))
+    tr.x_dtype, tr.compute_dtype = 1, 0  # bf16 rows with fp32 arithmetic
+    rc, msg = _status("odde_transition_fwd", tr)
+    assert rc == -2 and "float32 rows" in msg
+    tr.x_dtype, tr.compute_dtype = 0, 1
+    tr.c = 96
+    rc, msg = _status("odde_transition_fwd", tr)
+    assert rc == -2 and "c in" in msg
+    tr.c = 128
     tr.pb_heads = 8
     rc, msg = _status("odde_transition_fwd", tr)
     assert rc == -2 and "16 heads" in msg

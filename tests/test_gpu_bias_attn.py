@@ -81,3 +81,21 @@ def test_bias_attention_strided_heads_at_pair_stack_size():
                                                            v.contiguous(), attn_mask=b, scale=1.0)
     got = K.bias_attention(q, k, v, b)
     torch.testing.assert_close(got, exp, rtol=0, atol=1e-4)
+
+
+def test_bias_attention_contiguous_but_misaligned_kv():
+    """k and v that are contiguous but start 4 bytes past a 16-byte boundary
+    (a view one element into a buffer) are copied to aligned memory, not
+    rejected."""
+    say("[gpu] bias attn misaligned k/v")
+    q, k, v, b = _inputs(2, 40, 72, 24, 9)
+    exp = _expected(q, k, v, b)
+    kbuf = torch.empty(k.numel() + 1, device=DEV)
+    vbuf = torch.empty(v.numel() + 1, device=DEV)
+    kd = kbuf[1:].view(k.shape)
+    vd = vbuf[1:].view(v.shape)
+    kd.copy_(k)
+    vd.copy_(v)
+    assert kd.is_contiguous() and kd.data_ptr() % 16 == 4
+    got = K.bias_attention(q.to(DEV), kd, vd, b.to(DEV)).cpu()
+    torch.testing.assert_close(got, exp, rtol=0, atol=1e-4)

@@ -320,6 +320,48 @@ def test_transition_bf16(c, rows):
     assert_bf16(got, exp, f"transition c={c} rows={rows}")
 
 
+@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 130), (384, 17)])
+def test_transition_fp32(c, rows):
+    # fp32 arithmetic (no autocast): the fp32 tier's max-abs 1e-4
+    from opendde_amd.pairformer import Transition
+    mod = seeded(Transition(c, 4), 730 + c, 0.7 * STD * (128 / c) ** 0.5)
+    x = torch.randn(rows, c, generator=torch.Generator().manual_seed(c + 1))
+    exp = ref.transition(x, params_of(mod))
+    before = _lib.launch_count(_lib.K_TRANSITION)
+    mod = mod.to(DEV)
+    xg = x.to(DEV)
+    assert mod.hip_supported(xg)
+    got = mod.hip_apply(xg)
+    assert _lib.launch_count(_lib.K_TRANSITION) == before + 1
+    assert got.dtype == torch.float32
+    assert_fp32(got, exp, f"transition fp32 c={c} rows={rows}")
+    # in place, with the residual
+    got2 = mod.hip_apply(xg, out=xg, add_residual=True)
+    assert got2.data_ptr() == xg.data_ptr()
+    assert_fp32(got2, x + exp, f"transition fp32 in place c={c} rows={rows}")
+
+
+@pytest.mark.parametrize("c,ln_offset", [(128, True), (64, False), (384, True)])
+def test_transition_fp32_pair_bias_projection(c, ln_offset):
+    # the fp32 tier's pair bias from the fused epilogue, against the oracle
+    from opendde_amd.pairformer import AttentionPairBias, Transition
+    n = 37
+    tr = seeded(Transition(c, 4), 740, STD * (128 / c) ** 0.5)
+    apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=c, create_offset_ln_z=ln_offset), 741,
+                 0.1 * (128 / c) ** 0.5)
+    x = torch.randn(n, n, c, generator=torch.Generator().manual_seed(7))
+    z_new = x + ref.transition(x, params_of(tr))
+    pz = params_of(apb)
+    exp_bias = ref.linear(ref.layer_norm(z_new, pz["layernorm_z.weight"], pz.get("layernorm_z.bias")),
+                          pz["linear_nobias_z.weight"]).permute(2, 0, 1)
+    tr, apb = tr.to(DEV), apb.to(DEV)
+    xg = x.to(DEV)
+    dest = torch.full((16, n, n), float("nan"), device=DEV)
+    out = tr.hip_apply(xg, out=xg, add_residual=True, pair_bias=apb.pair_bias_spec(dest.view(16, -1)))
+    assert_fp32(out, z_new, f"fp32 transition update c={c}")
+    assert_fp32(dest, exp_bias, f"fp32 pair bias c={c} offset={ln_offset}")
+
+
 @pytest.mark.parametrize("c", [128, 384])
 def test_transition_fp32_residual_under_autocast_in_place(c):
     from opendde_amd.pairformer import Transition
