@@ -166,6 +166,13 @@ typedef struct odde_trimul_args {
   float eps;
   void* workspace;
   uint64_t workspace_bytes;
+  /* Optional (may be NULL): p_out_weight in f32.  With bf16 compute the
+   * output projection takes LN_out(p) W_z^T as rstd (p W'^T - mean s) + c,
+   * W' = W_z diag(norm_out_weight) rounded to bf16 once, s = row sums of W',
+   * c = W_z norm_out_bias: p enters the MFMA as stored, with no second
+   * rounding after the LayerNorm.  W' is formed from this f32 copy when it
+   * is given (one rounding), else from the bf16 p_out_weight. */
+  const float* p_out_weight_f32;
 } odde_trimul_args;
 
 int odde_trimul_workspace_bytes(const odde_trimul_args* args, uint64_t* bytes);

@@ -81,6 +81,7 @@ class TrimulArgs(ctypes.Structure):
         ("p_in_weight", _vp), ("g_in_weight", _vp), ("p_out_weight", _vp), ("g_out_weight", _vp),
         ("eps", _f32),
         ("workspace", _vp), ("workspace_bytes", _u64),
+        ("p_out_weight_f32", _vp),
     ]
 
 

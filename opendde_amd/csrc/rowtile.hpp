@@ -146,11 +146,16 @@ __device__ __forceinline__ void raw_tile_wait() {
 }
 
 // LayerNorm of the raw tile into `lds` (row stride TileLD), as stage_ln_tile;
-// rows with !valid(r) become zeros.  The caller synchronises afterwards.
+// rows with !valid(r) become zeros.  With `lds_lo` (bf16 only) the rounding
+// remainder y - bf16(y) goes there too, so that hi + lo carries y to about
+// 16 significant bits (two MFMAs, hi and lo against one weight fragment, then
+// replace one bf16 rounding of the activation).  The caller synchronises
+// afterwards.
 template <typename ZT, typename CT, int C, typename Valid>
 __device__ __forceinline__ void raw_tile_ln(const unsigned char* raw, Valid valid,
                                             const float* __restrict__ ln_w,
-                                            const float* __restrict__ ln_b, float eps, CT* lds) {
+                                            const float* __restrict__ ln_b, float eps, CT* lds,
+                                            CT* lds_lo = nullptr) {
   using T = RawTile<ZT, C>;
   constexpr int Q = C / 4;                        // channels per thread
   constexpr int EPC = 16 / (int)sizeof(ZT);       // elements per chunk
@@ -200,6 +205,14 @@ __device__ __forceinline__ void raw_tile_ln(const unsigned char* raw, Valid vali
 #pragma unroll
     for (int k = 0; k < 4; ++k) y[k] = ok ? (x[e + k] - mean) * rstd * w[k] + b[k] : 0.f;
     store4(dst + e, y[0], y[1], y[2], y[3]);
+    if constexpr (sizeof(CT) == 2) {
+      if (lds_lo) {
+        float lo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lo[k] = y[k] - round_to<CT>(y[k]);
+        store4(lds_lo + r * LD + quarter * Q + e, lo[0], lo[1], lo[2], lo[3]);
+      }
+    }
   }
 }
 

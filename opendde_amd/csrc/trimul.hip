@@ -267,12 +267,53 @@ struct TrimulOutArgs {
   const float* ln_in_b;
   const float* ln_out_w;
   const float* ln_out_b;
-  const CT* wz;  // [C][Ch]
+  const CT* wz;  // [C][Ch] (the weight-stationary kernel: W_z diag(ln_out_w))
   const CT* wg;  // [C][C]
+  const float* wz_sum;   // weight-stationary kernel: row sums of wz
+  const float* wz_bias;  // weight-stationary kernel: W_z ln_out_b
   int n, np, c;
   int add;
   float eps;
 };
+
+// LN_out folded into the output projection (weight-stationary kernel):
+// W'[o][k] = bf16(W_z[o][k] ln_out_w[k]) (from the f32 W_z when given, one
+// rounding), s[o] = sum_k W'[o][k] (the values the MFMA multiplies),
+// c[o] = sum_k ln_out_b[k] W_z[o][k].  One workgroup per output row, sums in
+// a fixed order.
+__global__ __launch_bounds__(256) void trimul_fold_ln_out_kernel(const float* __restrict__ wz32,
+                                                                 const bf16* __restrict__ wz16,
+                                                                 const float* __restrict__ lw,
+                                                                 const float* __restrict__ lb,
+                                                                 int ch, bf16* __restrict__ wf,
+                                                                 float* __restrict__ s,
+                                                                 float* __restrict__ c) {
+  __shared__ float red[2][256];
+  const int o = blockIdx.x, t = threadIdx.x;
+  float ss = 0.f, cc = 0.f;
+  for (int k = t; k < ch; k += 256) {
+    const size_t i = (size_t)o * ch + k;
+    const float wv = wz32 ? wz32[i] : (float)wz16[i];
+    const bf16 f = (bf16)(wv * lw[k]);
+    wf[i] = f;
+    ss += (float)f;
+    cc += lb[k] * wv;
+  }
+  red[0][t] = ss;
+  red[1][t] = cc;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if (t < h) {
+      red[0][t] += red[0][t + h];
+      red[1][t] += red[1][t + h];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    s[o] = red[0][0];
+    c[o] = red[1][0];
+  }
+}
 
 template <typename ZT, typename CT, int kC, int kCh>
 __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a) {
@@ -342,7 +383,10 @@ template <typename ZT, typename CT, int kC, int kCH>
 __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<ZT, CT> a,
                                                                 int ntiles) {
   constexpr int C = kC * 32, CH = kCH * 32, NB = kCH;  // NB blocks of 16 = Ch/2 channels
+  // bf16: the value projections also take the rounding remainder of LN(z)
+  constexpr bool kSplit = sizeof(CT) == 2;
   __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  __shared__ __attribute__((aligned(16))) CT xs_lo[kSplit ? kTileRows * TileLD<CT, C>::value : 8];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float mk_s[kTileRows];
   __shared__ float lnp[2 * C];  // LayerNorm weight, bias
@@ -389,7 +433,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
     const int y0 = (tile % tiles_per_row) * kTileRows;
     const float mcur = mnext;
     raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, lnp, lnp + C,
-                           a.eps, xs);
+                           a.eps, xs, kSplit ? xs_lo : nullptr);
     if (w == 0) mk_s[l] = mcur;
     lds_barrier();  // xs and mk_s ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) {
@@ -403,12 +447,15 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       const int rbase = 32 * (rb >> 1) + 4 * (rb & 1);
-      Frag<CT> xf[kC];
+      Frag<CT> xf[kC], xl[kSplit ? kC : 1];
       {
         constexpr int LD = TileLD<CT, C>::value;
-        const CT* row = xs + (rbase + 8 * (r16 >> 2) + (r16 & 3)) * LD + 8 * g;
+        const int off = (rbase + 8 * (r16 >> 2) + (r16 & 3)) * LD + 8 * g;
 #pragma unroll
-        for (int t = 0; t < kC; ++t) xf[t].load(row + 32 * t);
+        for (int t = 0; t < kC; ++t) {
+          xf[t].load(xs + off + 32 * t);
+          if constexpr (kSplit) xl[t].load(xs_lo + off + 32 * t);
+        }
       }
       float mk[4];
 #pragma unroll
@@ -418,6 +465,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
         f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap;
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
+          if constexpr (kSplit) mma(ap, xl[t], wpf[cb][t]);
           mma(ap, xf[t], wpf[cb][t]);
           mma(ag, xf[t], wgf[cb][t]);
         }
@@ -445,9 +493,13 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   }
 }
 
-// Epilogue: wave w produces output channels [w*C/4, (w+1)*C/4): W_z and W_g
-// slices in registers; LN_out(P) (P staged transposed from its channel-major
-// planes) and LN_in(z) tiles in LDS.
+// Epilogue: wave w produces output channels [w*C/4, (w+1)*C/4): W' and W_g
+// slices in registers; P (staged transposed from its channel-major planes,
+// as stored) and LN_in(z) tiles in LDS.  LN_out is folded into the weights
+// (a.wz = W' = W_z diag(ln_out_w) in bf16, a.wz_sum = row sums of W',
+// a.wz_bias = W_z ln_out_b):  LN_out(p) W_z^T = rstd (p W'^T - mean s) + c,
+// with the row statistics of p from LDS, so p enters the MFMA without being
+// rounded again after the normalisation.
 template <typename ZT, typename CT, int kC, int kCH>
 __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT, CT> a, int ntiles) {
   constexpr int C = kC * 32, CH = kCH * 32, NBO = C / 64;
@@ -455,15 +507,14 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   __shared__ __attribute__((aligned(16))) CT xp[kTileRows * LDP];
   __shared__ __attribute__((aligned(16))) CT xz[kTileRows * TileLD<CT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
-  __shared__ float lnp[2 * C + 2 * CH];  // LN_in weight, bias; LN_out weight, bias
+  __shared__ __attribute__((aligned(16))) float lnp[4 * C];  // LN_in weight, bias; s; c
+  __shared__ float pst[2 * kTileRows];                      // LN_out mean, rstd per row
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   for (int t = threadIdx.x; t < C; t += 256) {
     lnp[t] = a.ln_in_w[t];
     lnp[C + t] = a.ln_in_b[t];
-  }
-  for (int t = threadIdx.x; t < CH; t += 256) {
-    lnp[2 * C + t] = a.ln_out_w[t];
-    lnp[2 * C + CH + t] = a.ln_out_b[t];
+    lnp[2 * C + t] = a.wz_sum[t];
+    lnp[3 * C + t] = a.wz_bias[t];
   }
   Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
   load_w_slice<CT, NBO, kCH>(a.wz, CH, w * (C / 4), C, wzf);
@@ -514,10 +565,10 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
     }
     raw_tile_wait();  // z rows landed; every wave is done with the previous tile
     raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return y0 + r < n; }, lnp, lnp + C, a.eps, xz);
-    {  // LN_out over the channels of each staged P row, in place
+    {  // LN_out statistics of each staged P row (the row itself stays as stored)
       constexpr int Q = CH / 4;
       const int r = threadIdx.x >> 2, quarter = threadIdx.x & 3;
-      CT* row = xp + r * LDP + quarter * Q;
+      const CT* row = xp + r * LDP + quarter * Q;
       float v[Q];
 #pragma unroll
       for (int e = 0; e < Q; e += 8) load8(row + e, v + e);
@@ -532,14 +583,9 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       for (int e = 0; e < Q; ++e) q += (v[e] - mean) * (v[e] - mean);
       q += __shfl_xor(q, 1, 64);
       q += __shfl_xor(q, 2, 64);
-      const float rstd = rsqrtf(q * (1.0f / CH) + a.eps);
-#pragma unroll
-      for (int e = 0; e < Q; e += 4) {
-        float wv[4], bv[4];
-        load4(lnp + 2 * C + quarter * Q + e, wv);
-        load4(lnp + 2 * C + CH + quarter * Q + e, bv);
-        store4(row + e, (v[e] - mean) * rstd * wv[0] + bv[0], (v[e + 1] - mean) * rstd * wv[1] + bv[1],
-               (v[e + 2] - mean) * rstd * wv[2] + bv[2], (v[e + 3] - mean) * rstd * wv[3] + bv[3]);
+      if (quarter == 0) {
+        pst[r] = mean;
+        pst[kTileRows + r] = rsqrtf(q * (1.0f / CH) + a.eps);
       }
     }
     // residual z values of this lane's outputs, taken from the raw tile before
@@ -573,6 +619,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       tile_frags<CT, CH>(xp, rb, pf);
       tile_frags<CT, C>(xz, rb, zf);
       const int yr = y0 + rb * 16 + r16;
+      const float pmean = pst[rb * 16 + r16], prstd = pst[kTileRows + rb * 16 + r16];
 #pragma unroll
       for (int cb = 0; cb < NBO; ++cb) {
         f32x4 ay = {0.f, 0.f, 0.f, 0.f}, ag = ay;
@@ -582,9 +629,15 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         for (int t = 0; t < kC; ++t) mma(ag, wgf[cb][t], zf[t]);
         if (yr >= n) continue;
         const int c0 = w * (C / 4) + cb * 16 + 4 * g;
+        float sw[4], cw[4];
+        load4(lnp + 2 * C + c0, sw);
+        load4(lnp + 3 * C + c0, cw);
         float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = res[rb][cb][e] + ay[e] * sigmoidf_(ag[e]);
+        for (int e = 0; e < 4; ++e) {
+          const float y = prstd * (ay[e] - pmean * sw[e]) + cw[e];
+          r[e] = res[rb][cb][e] + y * sigmoidf_(ag[e]);
+        }
         store4(a.out + (int64_t)x * a.o_s0 + (int64_t)yr * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
       }
     }
@@ -750,7 +803,17 @@ bool trimul_wide(int c, int ch, int dt) {
   return dt == ODDE_BF16 && (c == 128 || c == 256 || c == 384) && (c >= 256 || ch >= 256);
 }
 
-struct TrimulWs { void* A; void* B; void* P; void* zn; uint64_t bytes; };
+// Shapes of the weight-stationary (register-resident weight slices) kernels:
+// bf16 compute with (C, Ch) in {(128, 128), (64, 64), (64, 128)}.
+bool trimul_ws_shape(int c, int ch, int dt) {
+  return dt == ODDE_BF16 && ((c == 128 && ch == 128) || (c == 64 && (ch == 64 || ch == 128)));
+}
+
+struct TrimulWs {
+  void* A; void* B; void* P; void* zn;
+  bf16* wfold; float* wsum; float* wbias;  // LN_out folded into W_z (ws shapes)
+  uint64_t bytes;
+};
 
 TrimulWs carve_trimul(void* base, uint64_t size, int n, int c, int ch, int dt) {
   const int np = round_up(n, 128);
@@ -763,6 +826,10 @@ TrimulWs carve_trimul(void* base, uint64_t size, int n, int c, int ch, int dt) {
   // the wide path's LN_in(z) rows (its LN_out(P) rows reuse A after the
   // contraction)
   w.zn = trimul_wide(c, ch, dt) ? cv.take<char>((uint64_t)np * np * c * 2) : nullptr;
+  const bool fold = trimul_ws_shape(c, ch, dt);
+  w.wfold = fold ? cv.take<bf16>((uint64_t)c * ch) : nullptr;
+  w.wsum = fold ? cv.take<float>(c) : nullptr;
+  w.wbias = fold ? cv.take<float>(c) : nullptr;
   w.bytes = (cv.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -1000,9 +1067,21 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   o.ln_out_w = a->norm_out_weight; o.ln_out_b = a->norm_out_bias;
   o.wz = static_cast<const CT*>(a->p_out_weight);
   o.wg = static_cast<const CT*>(a->g_out_weight);
+  o.wz_sum = o.wz_bias = nullptr;
   o.n = n; o.np = np; o.c = C; o.add = a->add_residual; o.eps = a->eps;
   {
     LaunchScope ls(ODDE_K_TRIMUL_OUT, st);
+    if constexpr (sizeof(CT) == 2) {
+      if (trimul_ws_shape(C, ch, a->compute_dtype)) {
+        hipLaunchKernelGGL(trimul_fold_ln_out_kernel, dim3(C), dim3(256), 0, st,
+                           a->p_out_weight_f32, static_cast<const bf16*>(a->p_out_weight),
+                           a->norm_out_weight, a->norm_out_bias, ch, ws.wfold, ws.wsum,
+                           ws.wbias);
+        o.wz = ws.wfold;
+        o.wz_sum = ws.wsum;
+        o.wz_bias = ws.wbias;
+      }
+    }
     bool ok = launch_to_ws<ZT, CT>(o, C, ch, st);
     if (!ok) switch (C) {
       case 64: ok = dispatch_to<ZT, CT, 2>(o, ch, st); break;

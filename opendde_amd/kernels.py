@@ -175,10 +175,12 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
                             norm_out_weight, norm_out_bias, p_out_weight, g_out_weight,
                             out: Optional[torch.Tensor] = None, add_residual: bool = False,
                             compute_dtype: Optional[torch.dtype] = None,
-                            eps: float = 1e-5) -> torch.Tensor:
+                            eps: float = 1e-5, f32_out_weight: bool = True) -> torch.Tensor:
     """Fused triangle multiplicative update on one pair tensor z [N, N, C];
     same ``out`` / ``add_residual`` contract as :func:`triangle_attention`.
-    ``p_in_weight``/``g_in_weight`` are [2*Ch, C] (a rows then b rows)."""
+    ``p_in_weight``/``g_in_weight`` are [2*Ch, C] (a rows then b rows).
+    ``f32_out_weight``: with bf16 compute, also hand the library linear_z in
+    f32 (it folds LN_out into that weight with a single bf16 rounding)."""
     _require_gpu(z, mask)
     _pair_view_ok(z, "z")
     n, c = z.shape[0], z.shape[2]
@@ -212,6 +214,9 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
             prepared(p_out_weight, ct), prepared(g_out_weight, ct)]
     (a.norm_in_weight, a.norm_in_bias, a.norm_out_weight, a.norm_out_bias,
      a.p_in_weight, a.g_in_weight, a.p_out_weight, a.g_out_weight) = (_ptr(t) for t in keep)
+    if ct == torch.bfloat16 and f32_out_weight:
+        keep.append(prepared(p_out_weight, f32))
+        a.p_out_weight_f32 = _ptr(keep[-1])
     a.eps = float(eps)
     lib = _lib.load()
     nb = ctypes.c_uint64(0)

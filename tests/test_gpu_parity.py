@@ -9,7 +9,8 @@ rel-L2 <= 1e-2 and max-abs <= 5e-2 vs the fp32 oracle fed the same
 import pytest
 import torch
 
-from helpers import (assert_bf16, assert_fp32, params_of, say, seeded, token_pair_mask)
+from helpers import (assert_bf16, assert_fp32, params_of, rel_l2, say, seeded,
+                     token_pair_mask)
 from oracle import reference as ref
 from opendde_amd import _lib
 from opendde_amd.pairformer import PairformerBlock
@@ -429,3 +430,40 @@ def test_pairformer_block_bf16_autocast():
     assert zg.dtype == torch.float32
     assert_bf16(zg - z.to(DEV), ze - z, "block update z (bf16 arithmetic)")
     assert_bf16(sg - s.to(DEV), se - s, "block update s (bf16 arithmetic)")
+
+
+# ------------------------------------------------- bf16 accuracy of tri-mul
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_bf16_rounding_budget(outgoing):
+    """The bf16 multiplication keeps the rounding remainder of LN_in(z) for
+    the value projections (hi + lo bf16) and folds LN_out into W_z, so p
+    enters the output projection as stored.  Without those the relative error
+    of the update against the fp32 oracle is about 5.0e-3 at this size (one
+    bf16 rounding each of x, the weights, a and b, p and LN_out(p)); with
+    them about 4.1e-3.  Over the 48-block trunk that margin is what keeps the
+    accumulated update within max-abs 5e-2.  Also: without the f32 copy of
+    linear_z the fold rounds the weight twice and stays within the tier."""
+    n = 192
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(128, 128), 900 + outgoing, 0.02)  # the workload's weight scale
+    z = _z(n, 128, 901)
+    exp = ref.triangle_multiplication(z, None, params_of(mod), outgoing)
+    mod = mod.to(DEV)
+    zg = z.to(DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        got = mod.hip_apply(zg, None)
+    rl = rel_l2(got, exp)
+    say(f"    trimul bf16 n={n} out={outgoing} rel_l2={rl:.3e}")
+    assert rl <= 4.6e-3, f"rel-L2 {rl:.3e}: bf16 rounding budget exceeded"
+    from opendde_amd import kernels as K
+    w = mod
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        got2 = K.triangle_multiplication(
+            zg, None, outgoing=outgoing, norm_in_weight=w.layer_norm_in.weight,
+            norm_in_bias=w.layer_norm_in.bias,
+            p_in_weight=torch.cat([w.linear_a_p.weight, w.linear_b_p.weight]),
+            g_in_weight=torch.cat([w.linear_a_g.weight, w.linear_b_g.weight]),
+            norm_out_weight=w.layer_norm_out.weight, norm_out_bias=w.layer_norm_out.bias,
+            p_out_weight=w.linear_z.weight, g_out_weight=w.linear_g.weight,
+            f32_out_weight=False)
+    assert_bf16(got2, exp, f"trimul bf16 without the f32 linear_z, out={outgoing}")
