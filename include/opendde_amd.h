@@ -285,6 +285,23 @@ int odde_layer_norm_bwd_workspace_bytes(const odde_layer_norm_bwd_args* args, ui
 int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* args, void* hip_stream);
 
 /*
+ * odde_layer_norm_bwd without a workspace and without any allocation.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as odde_layer_norm_bwd; the
+ * workspace fields are ignored.  The partial column sums go to a fixed
+ * 16 MiB device array inside the library (one per GPU, held until the
+ * process ends): a call whose partial sums need more
+ * (odde_layer_norm_bwd_workspace_bytes > 16 MiB, i.e. a large n2) returns
+ * ODDE_EUNSUPPORTED.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (concurrent streams, or host threads) race; serialise
+ * them.  Nothing in the array needs clearing between calls (every partial
+ * row a call reads, it writes first).  Instrumentation events are not
+ * recorded for it (odde_timing_*); the launch counter still counts it.
+ */
+int odde_layer_norm_bwd_noalloc(const odde_layer_norm_bwd_args* args, void* hip_stream);
+
+/*
  * Attention with an additive bias in fp32: the core of the single track's
  * AttentionPairBias (replaces primitives._attention, opendde/model/modules/
  * primitives.py:220-258, which upcasts q, k, v and the bias to fp32 and runs

@@ -150,6 +150,7 @@ SYMBOLS = {
     "odde_layer_norm_bwd_workspace_bytes": (_i32, [ctypes.POINTER(LayerNormBwdArgs),
                                                    ctypes.POINTER(_u64)]),
     "odde_layer_norm_bwd": (_i32, [ctypes.POINTER(LayerNormBwdArgs), _vp]),
+    "odde_layer_norm_bwd_noalloc": (_i32, [ctypes.POINTER(LayerNormBwdArgs), _vp]),
     "odde_opm_workspace_bytes": (_i32, [ctypes.POINTER(OpmArgs), ctypes.POINTER(_u64)]),
     "odde_opm_fwd": (_i32, [ctypes.POINTER(OpmArgs), _vp]),
     "odde_bias_attn_fwd": (_i32, [ctypes.POINTER(BiasAttnArgs), _vp]),

@@ -26,6 +26,8 @@
 // kernels: a wave per row with strided scalar access, and a column-partial
 // kernel for grad_gamma / grad_beta.
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "common.hpp"
 #include "runtime.hpp"
@@ -535,7 +537,8 @@ int run_fwd(const odde_layer_norm_args* a, hipStream_t st) {
 }
 
 template <typename T>
-int run_bwd(const odde_layer_norm_bwd_args* a, uint64_t need_ws, hipStream_t st) {
+int run_bwd(const odde_layer_norm_bwd_args* a, uint64_t need_ws, hipStream_t st,
+            bool events = true) {
   const LnPlan p = plan_shape(a->n1, a->n2, a->dtype, true);
   const bool use_rows = p.rows && aligned16(a->x) && aligned16(a->dout) &&
                         aligned16(a->grad_input) && aligned16(a->gamma);
@@ -544,7 +547,7 @@ int run_bwd(const odde_layer_norm_bwd_args* a, uint64_t need_ws, hipStream_t st)
   const int64_t nparts = a->n1 == 0 ? 0 : use_rows ? p.blocks : generic_parts(a->n1);
   if (want_params && uint64_t(nparts) * 2 * uint64_t(a->n2) * sizeof(float) > need_ws)
     return set_error(ODDE_EINVAL, "layer_norm backward: internal workspace plan error");
-  LaunchScope ls(ODDE_K_LAYER_NORM_BWD, st);
+  LaunchScope ls(ODDE_K_LAYER_NORM_BWD, st, events);
   if (a->n1 > 0 && use_rows) {
     switch (p.nv) {
       case 1: launch_bwd_rows<T, 1>(p, a, part, st); break;
@@ -575,6 +578,51 @@ int run_bwd(const odde_layer_norm_bwd_args* a, uint64_t need_ws, hipStream_t st)
 }
 
 bool valid_ln_dtype(int dt) { return dt == ODDE_F32 || dt == ODDE_BF16 || dt == ODDE_F16; }
+
+// Partial column sums of the allocation-free backward: a fixed device array
+// (each GPU holds its own copy at its own address for the life of the
+// process).  Host code never passes `scratch` itself to a kernel: its name on
+// the host is a stand-in, not a device address.  The device address is
+// looked up once per device with hipGetSymbolAddress and cached.
+constexpr uint64_t kLnScratchBytes = uint64_t(16) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kLnScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return set_error(ODDE_EHIP, "layer_norm backward (no-alloc): no current HIP device");
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return set_error(ODDE_EHIP, std::string("layer_norm backward (no-alloc): "
+                                              "hipGetSymbolAddress(scratch) failed: ") +
+                                      hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ODDE_OK;
+}
+
+int check_bwd_args(const odde_layer_norm_bwd_args* a) {
+  if (!a) return set_error(ODDE_EINVAL, "layer_norm backward: null args");
+  if (a->struct_size != sizeof(odde_layer_norm_bwd_args))
+    return set_error(ODDE_EINVAL, "layer_norm backward: struct_size mismatch (ABI version skew)");
+  if (a->n1 < 0 || a->n2 <= 0) return set_error(ODDE_EINVAL, "layer_norm backward: bad sizes");
+  if (!valid_ln_dtype(a->dtype)) return set_error(ODDE_EINVAL, "layer_norm backward: bad dtype");
+  if (a->n1 > 0 && (!a->dout || !a->x || !a->mean || !a->invvar || !a->grad_input))
+    return set_error(ODDE_EINVAL, "layer_norm backward: null tensor pointer");
+  return ODDE_OK;
+}
 
 uint64_t bwd_workspace(int64_t n1, int n2, int dt) {
   LnPlan rows = plan_shape(n1, n2, dt, true);
@@ -616,13 +664,7 @@ int odde_layer_norm_bwd_workspace_bytes(const odde_layer_norm_bwd_args* a, uint6
 }
 
 int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* a, void* stream) {
-  if (!a) return set_error(ODDE_EINVAL, "layer_norm backward: null args");
-  if (a->struct_size != sizeof(odde_layer_norm_bwd_args))
-    return set_error(ODDE_EINVAL, "layer_norm backward: struct_size mismatch (ABI version skew)");
-  if (a->n1 < 0 || a->n2 <= 0) return set_error(ODDE_EINVAL, "layer_norm backward: bad sizes");
-  if (!valid_ln_dtype(a->dtype)) return set_error(ODDE_EINVAL, "layer_norm backward: bad dtype");
-  if (a->n1 > 0 && (!a->dout || !a->x || !a->mean || !a->invvar || !a->grad_input))
-    return set_error(ODDE_EINVAL, "layer_norm backward: null tensor pointer");
+  if (const int rc = check_bwd_args(a)) return rc;
   const bool want_params = a->grad_gamma || a->grad_beta;
   const uint64_t need = bwd_workspace(a->n1, a->n2, a->dtype);
   if (want_params && need > 0) {
@@ -635,6 +677,31 @@ int odde_layer_norm_bwd(const odde_layer_norm_bwd_args* a, void* stream) {
   if (a->dtype == ODDE_F32) return run_bwd<float>(a, need, st);
   if (a->dtype == ODDE_BF16) return run_bwd<bf16>(a, need, st);
   return run_bwd<f16>(a, need, st);
+}
+
+int odde_layer_norm_bwd_noalloc(const odde_layer_norm_bwd_args* a, void* stream) {
+  if (const int rc = check_bwd_args(a)) return rc;
+  const bool want_params = a->grad_gamma || a->grad_beta;
+  const uint64_t need = bwd_workspace(a->n1, a->n2, a->dtype);
+  odde_layer_norm_bwd_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (want_params && need > 0) {
+    if (need > kLnScratchBytes)
+      return set_error(ODDE_EUNSUPPORTED,
+                       "layer_norm backward (no-alloc): the partial column sums need " +
+                           std::to_string(need) + " bytes, more than the " +
+                           std::to_string(kLnScratchBytes) +
+                           "-byte scratch array; use odde_layer_norm_bwd with a workspace");
+    void* p = nullptr;
+    if (const int rc = scratch_address(&p)) return rc;
+    b.workspace = p;
+    b.workspace_bytes = kLnScratchBytes;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->dtype == ODDE_F32) return run_bwd<float>(&b, need, st, false);
+  if (a->dtype == ODDE_BF16) return run_bwd<bf16>(&b, need, st, false);
+  return run_bwd<f16>(&b, need, st, false);
 }
 
 }  // extern "C"

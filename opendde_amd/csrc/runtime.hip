@@ -58,8 +58,10 @@ int resident_grid(const void* kernel, int threads) {
   return (per > 0 ? per : 1) * (cus > 0 ? cus : 1);
 }
 
-LaunchScope::LaunchScope(int kernel_id, hipStream_t s) : id(kernel_id), stream(s), slot(-1) {
+LaunchScope::LaunchScope(int kernel_id, hipStream_t s, bool events)
+    : id(kernel_id), stream(s), slot(-1) {
   g_launches[id].fetch_add(1, std::memory_order_relaxed);
+  if (!events) return;
   TimingState& t = timing();
   std::lock_guard<std::mutex> lk(t.mu);
   if (!t.enabled) return;

@@ -19,10 +19,11 @@ int check_launch(const char* what);
 // workgroups must all be resident or the late ones finish a whole pass late.
 int resident_grid(const void* kernel, int threads);
 
-// Launch bookkeeping: counts every launch; when timing is on, records a pair
-// of events around it on `stream`.
+// Launch bookkeeping: counts every launch; when timing is on (and `events`),
+// records a pair of events around it on `stream` (creating events the first
+// time; callers that must not allocate pass events = false).
 struct LaunchScope {
-  LaunchScope(int kernel_id, hipStream_t stream);
+  LaunchScope(int kernel_id, hipStream_t stream, bool events = true);
   ~LaunchScope();
   int id;
   hipStream_t stream;

@@ -174,3 +174,22 @@ def test_opm_workspace_query_and_limits():
         assert "outer_product_mean" in lib.odde_last_error().decode()
     rc, msg = _status("odde_opm_fwd", _opm_args())
     assert rc == -1 and "null tensor pointer" in msg
+
+
+def test_noalloc_layer_norm_bwd_rejects_what_its_scratch_cannot_hold():
+    # the partial column sums of n2 = 4096 over 2^20 rows need far more than
+    # the 16 MiB scratch array: the call returns EUNSUPPORTED before any
+    # device work (the pointers are never dereferenced)
+    a = _lib.LayerNormBwdArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.dtype, a.n1, a.n2 = _lib.F32, 1 << 20, 4096
+    for f in ("dout", "mean", "invvar", "x", "gamma", "grad_input", "grad_gamma", "grad_beta"):
+        setattr(a, f, ctypes.c_void_p(0x1000))
+    nb = ctypes.c_uint64(0)
+    assert _lib.load().odde_layer_norm_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)) == 0
+    assert nb.value > 16 << 20
+    rc, msg = _status("odde_layer_norm_bwd_noalloc", a)
+    assert rc == -2 and "scratch" in msg
+    a.struct_size = 8
+    rc, msg = _status("odde_layer_norm_bwd_noalloc", a)
+    assert rc == -1 and "struct_size" in msg
