@@ -8,25 +8,34 @@ float32 and module arithmetic in bf16 (CUDA autocast, the reference's bf16
 inference mode).  Inputs are resident in HBM before timing; each step starts
 by restoring z from a resident copy (a 512 MB device copy, ~0.1 ms).
 
-Prints ONE JSON line.  ``value`` is the trunk's algorithmic throughput in
-TFLOP/s (flop counts of the path, multiply-add = 2) over the timed steps,
-which run without instrumentation.  Per-kernel figures come from one further
-step during which the library records HIP events around every launch on the
-stream it runs on.  ``roofline.traffic`` is the dominant kernel's HBM bytes
-per launch from the committed rocprofv3 --pmc summary of this workload
+Prints ONE JSON line on stdout (progress goes to stderr).  ``value`` is the
+trunk's algorithmic throughput in TFLOP/s (flop counts of the path,
+multiply-add = 2) over the timed steps, which run without instrumentation.
+Per-kernel figures come from one further step during which the library
+records HIP events around every launch on the stream it runs on.
+``roofline.traffic`` is the dominant kernel's HBM bytes per launch from the
+committed rocprofv3 --pmc summary of this workload
 (profiles/pmc_traffic_trunk_n<N>.json, made with ``--pmc-probe``), or null.
 ``cpu_baseline`` times the CPU oracle (fp32) on one block of the same
-workload on this host.  ``layer_norm`` times the standalone fast LayerNorm
-(forward and backward) on the workload's pair tensor shape, N*N x 128 bf16,
-outside the trunk step.
+workload on this host (median of 5).  ``configs`` holds the other workloads
+the path is specified on, each timed on the GPU (median of per-iteration HIP
+events) and, for the first three and one block of the trunk, on the CPU
+oracle (median of 5 runs after 1 warm-up): the N=128 block in fp32, N=384
+triangle attention, N=768 triangle multiplication (both directions), the
+N=2048 x 4-block stress stack.  ``machine`` holds the MFMA rates and HBM copy
+bandwidth measured on this GPU next to the data sheet's.  ``layer_norm``
+times the standalone fast LayerNorm (forward and backward) on the workload's
+pair tensor shape, N*N x 128 bf16, outside the trunk step.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -37,7 +46,9 @@ sys.path.insert(0, ROOT)
 
 from opendde_amd import _lib  # noqa: E402
 from opendde_amd import workload as wl  # noqa: E402
-from opendde_amd.pairformer import PairformerStack  # noqa: E402
+from opendde_amd.pairformer import PairformerBlock, PairformerStack  # noqa: E402
+from opendde_amd.triangular import (TriangleAttention, TriangleMultiplicationIncoming,  # noqa: E402
+                                    TriangleMultiplicationOutgoing)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_F32_TFLOPS = 157.3     # MI355X fp32 MFMA
@@ -86,29 +97,258 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(n: int, chunk: int):
-    """Time the CPU oracle (fp32) on one PairformerBlock of the workload at n."""
-    from oracle import reference as ref
+def log(msg: str) -> None:
+    """Progress line on stderr (stdout carries only the JSON line)."""
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _cpu_params(mod):
+    return {k: v.detach().float().cpu() for k, v in mod.named_parameters()}
+
+
+def cpu_median(fn, runs: int = 5, warm: int = 1):
+    """Median wall time (s) of ``runs`` calls of fn after ``warm`` calls."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def cpu_threads():
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_baseline(n: int, chunk: int, runs: int = 5):
+    """Time the CPU oracle (fp32) on one PairformerBlock of the workload at n:
+    a 16-token block first (thread pool and allocator warm-up), then the
+    median of ``runs`` runs of the full block."""
+    from oracle import reference as ref
+    cores = cpu_threads()
     cfg = wl.PairConfig("cpu_sample", n, n_pad=max(0, n * 5 // 100), random_pad=True, seed=3)
     z, s, mask, gen = wl.make_inputs(cfg)
     params = wl.param_values(wl.block_specs(), gen)
-    # warm the thread pool and allocator on a tiny block
     ref.pairformer_block(s[:16], z[:16, :16], mask[:16, :16], params, chunk_size=chunk)
-    t0 = time.perf_counter()
-    ref.pairformer_block(s, z, mask, params, chunk_size=chunk)
-    dt = time.perf_counter() - t0
+    med, ts = cpu_median(lambda: ref.pairformer_block(s, z, mask, params, chunk_size=chunk),
+                         runs=runs, warm=0)
     f = flops(n)["block"]
     return {
-        "value": round(f / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "value": round(f / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle (CPU PyTorch restatement of the reference torch path) fp32, one "
-                  f"PairformerBlock at N={n} (tri-attn row chunk {chunk}), {dt:.2f} s; "
-                  f"CPU {cpu_model()}, "
-                  f"{cores} cores in affinity",
-        "block_ms": round(dt * 1e3, 1),
+                  f"PairformerBlock at N={n} (tri-attn row chunk {chunk}) of the 48, median of "
+                  f"{runs} runs ({', '.join(f'{t:.2f}' for t in ts)} s) after a 16-token "
+                  f"warm-up; CPU {cpu_model()}, {cores} cores in affinity",
+        "block_ms": round(med * 1e3, 1),
     }
+
+
+def gpu_median_ms(fn, warm: int = 3, iters: int = 20):
+    """Median of per-iteration times (HIP events on the current stream, the
+    stream every library call here launches on)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def kernel_avg_ms(fn, kid, reps: int = 5):
+    """Average launch time of library kernel ``kid`` over ``reps`` calls of
+    fn, from the library's HIP events."""
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    tot, cnt = _lib.timing_query(kid)
+    _lib.timing_reset()
+    return tot / cnt if cnt else None
+
+
+def probe_machine(dev):
+    """Sustained MFMA rates (bf16 16x16x32, f32 16x16x4; 2 workgroups of 4
+    waves per CU, 8 independent chains per wave) and HBM copy bandwidth
+    (2 GiB device copy, bytes read + written) on this GPU."""
+    lib = _lib.load()
+    sink = torch.zeros(256, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {"cus": cus}
+    for name, code, iters in (("bf16", _lib.BF16, 4000), ("f32", _lib.F32, 1000)):
+        fl = ctypes.c_double(0.0)
+        call = lambda it: _lib.check(lib.odde_probe_mfma(code, it, 2 * cus,  # noqa: E731
+                                                         ctypes.c_void_p(sink.data_ptr()),
+                                                         ctypes.byref(fl), stream),
+                                     "odde_probe_mfma")
+        call(100)
+        ms = kernel_avg_ms(lambda: call(iters), _lib.K_PROBE, reps=3)
+        out[f"mfma_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
+    out["mfma_bf16_tflops_spec"] = PEAK_BF16_TFLOPS
+    out["mfma_f32_tflops_spec"] = PEAK_F32_TFLOPS
+    src = torch.empty(1 << 29, device=dev)
+    dst = torch.empty_like(src)
+    ms = gpu_median_ms(lambda: dst.copy_(src), warm=2, iters=5)
+    out["hbm_copy_gbs"] = round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)
+    out["hbm_gbs_spec"] = PEAK_HBM_GBS
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
+def config_legs(dev, with_cpu: bool):
+    """The path's other specified workloads: GPU time (median of per-iteration
+    events), TFLOP/s over the algorithmic flops, % of peak, the compulsory
+    HBM bytes per ms of the module legs, and the CPU oracle (fp32, median of
+    5 after 1 warm-up) beside them."""
+    if with_cpu:
+        from oracle import reference as ref
+    cores = cpu_threads() if with_cpu else None
+    res = {}
+
+    def cpu_leg(fn, fl):
+        if not with_cpu:
+            return {}
+        med, ts = cpu_median(fn)
+        return {"cpu_ms": round(med * 1e3, 2), "cpu_gflops": round(fl / med / 1e9, 2),
+                "cpu_cores": cores, "cpu_runs_s": [round(t, 3) for t in ts]}
+
+    # cfg1: one PairformerBlock at N=128, fp32 (c_s 384, 16 single heads)
+    cfg = wl.BLOCK_N128
+    z, s, mask, gen = wl.make_inputs(cfg)
+    blk = PairformerBlock(n_heads=16, c_z=128, c_s=384, c_hidden_mul=128,
+                          c_hidden_pair_att=32, no_heads_pair=4)
+    wl.init_module_(blk, gen)
+    blk = blk.eval()
+    p = _cpu_params(blk)
+    blk = blk.to(dev)
+    zg, sg, mg = z.to(dev), s.to(dev), mask.to(dev)
+    f = flops(cfg.n)["block"]
+    with torch.no_grad():
+        ms = gpu_median_ms(lambda: blk(sg, zg, mg, triangle_multiplicative="hip",
+                                       triangle_attention="hip"))
+    t = f / (ms * 1e-3) / 1e12
+    res["cfg1_block_n128_fp32"] = dict(
+        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2), dtype="fp32",
+        **cpu_leg(lambda: ref.pairformer_block(s, z, mask, p), f))
+    log(f"bench: cfg1 block n=128 fp32 {ms:.3f} ms")
+    del blk, zg, sg, mg
+
+    # cfg2: TriangleAttention starting node at N=384, bf16 z, last 38 tokens padded
+    cfg = wl.TRIATT_N384
+    z, _, mask, gen = wl.make_inputs(cfg)
+    mod = TriangleAttention(cfg.c_z, cfg.head_dim, cfg.heads)
+    wl.init_module_(mod, gen)
+    mod = mod.eval()
+    p = _cpu_params(mod)
+    mod = mod.to(dev)
+    zb = z.to(torch.bfloat16)
+    zg, mg = zb.to(dev), mask.to(dev)
+    fa = flops(cfg.n)
+    f = fa["core"] + fa["att_lin"]
+    fn = lambda: mod(zg, mg, triangle_attention="hip")  # noqa: E731
+    with torch.no_grad():
+        ms = gpu_median_ms(fn)
+        core_ms = kernel_avg_ms(fn, _lib.K_TRIATT_CORE)
+    t, tc = f / (ms * 1e-3) / 1e12, fa["core"] / (core_ms * 1e-3) / 1e12
+    zf = zb.float()
+    res["cfg2_triatt_start_n384_bf16"] = dict(
+        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+        pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+        core_ms=round(core_ms, 4), core_tflops=round(tc, 2),
+        core_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
+        hbm_gbs=round((2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
+        dtype="bf16", pad_tokens=cfg.n_pad,
+        **cpu_leg(lambda: ref.triangle_attention(zf, mask, p, cfg.heads), f))
+    log(f"bench: cfg2 tri-attn n=384 {ms:.3f} ms")
+    del mod, zg, mg
+
+    # cfg3: TriangleMultiplication outgoing + incoming at N=768, bf16 z
+    cfg = wl.TRIMUL_N768
+    z, _, mask, gen = wl.make_inputs(cfg)
+    mo = TriangleMultiplicationOutgoing(cfg.c_z, cfg.c_hidden_mul)
+    mi = TriangleMultiplicationIncoming(cfg.c_z, cfg.c_hidden_mul)
+    wl.init_module_(mo, gen)
+    wl.init_module_(mi, gen)
+    po, pi = _cpu_params(mo), _cpu_params(mi)
+    mo, mi = mo.eval().to(dev), mi.eval().to(dev)
+    zb = z.to(torch.bfloat16)
+    zg, mg = zb.to(dev), mask.to(dev)
+    fm = flops(cfg.n)
+    f = 2 * (fm["contract"] + fm["mul_lin"])
+
+    def fn():
+        mo(zg, mg, triangle_multiplicative="hip")
+        mi(zg, mg, triangle_multiplicative="hip")
+
+    with torch.no_grad():
+        ms = gpu_median_ms(fn)
+        ct_ms = kernel_avg_ms(fn, _lib.K_TRIMUL_CONTRACT)
+    t, tc = f / (ms * 1e-3) / 1e12, fm["contract"] / (ct_ms * 1e-3) / 1e12
+    zf = zb.float()
+
+    def cpu3():
+        ref.triangle_multiplication(zf, mask, po, True)
+        ref.triangle_multiplication(zf, mask, pi, False)
+
+    res["cfg3_trimul_out_in_n768_bf16"] = dict(
+        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+        pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+        contract_ms=round(ct_ms, 4), contract_tflops=round(tc, 2),
+        contract_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
+        hbm_gbs=round(2 * (2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
+        dtype="bf16", **cpu_leg(cpu3, f))
+    log(f"bench: cfg3 tri-mul n=768 out+in {ms:.3f} ms")
+    del mo, mi, zg, mg
+    torch.cuda.empty_cache()
+
+    # cfg5: N=2048, 4 blocks (no single track), bench mode, peak memory
+    cfg = wl.STRESS_N2048
+    z, _, mask, gen = wl.make_inputs(cfg)
+    stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=16, c_z=cfg.c_z, c_s=0)
+    wl.init_module_(stack, gen)
+    stack = stack.eval().to(dev)
+    z0, mg = z.to(dev), mask.to(dev)
+    zw = torch.empty_like(z0)
+
+    def stress():
+        zw.copy_(z0)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            stack(None, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
+                  inplace_safe=True)
+
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    ms = gpu_median_ms(stress, warm=1, iters=3)
+    peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+    fb = flops(cfg.n, c_s=0)
+    f = cfg.n_blocks * fb["block"]
+    t = f / (ms * 1e-3) / 1e12
+    res["cfg5_stress_4x_n2048_bf16"] = dict(
+        gpu_ms=round(ms, 2), block_ms=round(ms / cfg.n_blocks, 3), gflop=round(f / 1e9, 1),
+        tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+        peak_gib_above_inputs=round(peak, 2), total_gib_in_use=round(
+            torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2), dtype="bf16",
+        residual_dtype="fp32")
+    log(f"bench: cfg5 stress n=2048 x4 {ms:.1f} ms, peak {peak:.1f} GiB")
+    del stack, z0, zw, mg
+    torch.cuda.empty_cache()
+    return res
 
 
 CALIB_BYTES = 1 << 30  # bytes read (and written) by the calibration kernel
@@ -248,6 +488,11 @@ def main():
                     help="skip the OuterProductMean measurement")
     ap.add_argument("--no-layer-norm", action="store_true",
                     help="skip the standalone fast-LayerNorm measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other specified workloads (N=128 fp32 block, N=384 "
+                         "attention, N=768 multiplication, N=2048 x 4 stack)")
+    ap.add_argument("--no-machine", action="store_true",
+                    help="skip the MFMA-rate and HBM-copy probes")
     ap.add_argument("--preset", choices=["trunk", "opendde_v1"], default="trunk",
                     help="trunk: c_z 128, 4 triangle heads, hidden 128 (the benchmark "
                          "configuration); opendde_v1: the shipped model's pair width, c_z 384 "
@@ -285,6 +530,7 @@ def main():
         pmc_probe(step, dev)
         return
 
+    log(f"bench: trunk {args.blocks} blocks n={args.n}: {args.warmup} warm-up, {args.steps} timed")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -302,6 +548,7 @@ def main():
     torch.cuda.synchronize()
     _lib.timing_enable(False)
 
+    log(f"bench: trunk {dt * 1e3 / args.steps:.1f} ms per step")
     n = args.n
     f = flops(n, c_z=c_z, h=heads, ch=ch)
     ms_step = dt * 1e3 / args.steps
@@ -319,6 +566,13 @@ def main():
         if name == "triatt_core":
             t = f["core"] / (avg * 1e-3) / 1e12
             ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
+            # the rows of padded tokens keep no key: the fast core skips them
+            # (their output, the mean of v, costs O(N) per row); executed work
+            # counts the kept rows only
+            pad = n * 5 // 100
+            te = t * (n - pad) / n
+            ent.update(tflops_executed=round(te, 2), rows_executed=n - pad,
+                       pct_bf16_peak_executed=round(100 * te / PEAK_BF16_TFLOPS, 2))
         elif name == "trimul_contract":
             t = f["contract"] / (avg * 1e-3) / 1e12
             ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
@@ -371,11 +625,35 @@ def main():
         "kernels": kernels,
         "roofline": roof,
         "cpu_baseline": None,
-        "layer_norm": None if args.no_layer_norm else layer_norm_measure(n, dev),
-        "outer_product_mean": None if args.no_opm else opm_measure(n, dev),
+        "machine": None,
+        "configs": None,
+        "layer_norm": None,
+        "outer_product_mean": None,
     }
-    if not args.no_cpu_baseline and not v1:
+    del stack, z, z0, s0
+    torch.cuda.empty_cache()
+    if not args.no_layer_norm:
+        out["layer_norm"] = layer_norm_measure(n, dev)
+        log("bench: layer norm done")
+    if not args.no_opm:
+        out["outer_product_mean"] = opm_measure(n, dev)
+        log("bench: outer product mean done")
+    if not args.no_machine:
+        m = probe_machine(dev)
+        out["machine"] = m
+        if roof["unit"] == "TFLOP/s":
+            roof["frac_of_measured_peak"] = round(roof["achieved"] / m["mfma_bf16_tflops"], 4)
+            roof["measured_peak"] = m["mfma_bf16_tflops"]
+        else:
+            roof["frac_of_measured_peak"] = round(roof["achieved"] / m["hbm_copy_gbs"], 4)
+            roof["measured_peak"] = m["hbm_copy_gbs"]
+        log(f"bench: machine {m}")
+    cpu = not args.no_cpu_baseline and not v1
+    if not args.no_configs and not v1:
+        out["configs"] = config_legs(dev, with_cpu=cpu)
+    if cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_n, chunk=128)
+        log("bench: cpu baseline done")
     print(json.dumps(out), flush=True)
 
 

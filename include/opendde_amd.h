@@ -51,7 +51,8 @@ extern "C" {
 #define ODDE_K_LAYER_NORM_BWD 9
 #define ODDE_K_OPM 10
 #define ODDE_K_BIAS_ATTN 11
-#define ODDE_K_COUNT 12
+#define ODDE_K_PROBE 12
+#define ODDE_K_COUNT 13
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -384,6 +385,16 @@ int64_t odde_launch_count(int kernel_id);
 int odde_timing_enable(int on);
 int odde_timing_reset(void);
 int odde_timing_query(int kernel_id, double* total_ms, int64_t* launches);
+
+/* Machine-rate probe (no counterpart in the reference): launches `grid`
+ * workgroups of 4 waves that each run 8 independent MFMA accumulator chains
+ * of `iters` instructions (dtype ODDE_BF16: v_mfma_f32_16x16x32_bf16;
+ * ODDE_F32: v_mfma_f32_16x16x4_f32) and returns the flops it performs in
+ * *flops; time it with odde_timing_* (kernel id ODDE_K_PROBE) to get the
+ * sustained MFMA rate.  `sink`: 256 floats of device memory (practically
+ * never written). */
+int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flops,
+                    void* hip_stream);
 
 #ifdef __cplusplus
 }
