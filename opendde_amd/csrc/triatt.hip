@@ -752,12 +752,18 @@ __device__ __forceinline__ int kswz(int key, int chunk, int kch) {
 
 // One workgroup = RG x QS waves over R_WG = RG*R rows and Q_WG = QS*16*QB
 // queries of one head.  Per 32-key block the workgroup stages K, V, keep and
-// the bias tile in LDS once (double buffered, loads for block t+1 in flight
-// while block t is computed), so each byte fetched from L2 feeds R_WG rows x
-// Q_WG queries.  Wave (rg, qs) owns rows rg*R.. and queries qs*16*QB..: S^T =
-// K Q^T on MFMA with the accumulator initialised from the bias fragment
-// (shared by its R rows), p = exp2(s), row sums sum_k keep[k] p[k] by dot2,
-// O^T += V^T P^T on MFMA.
+// the bias tile in LDS once (double buffered: the loads of block t+1 are in
+// flight while block t is computed), so each byte fetched from L2 feeds R_WG
+// rows x Q_WG queries.  The staging goes straight from global memory into LDS
+// (buffer loads with the LDS flag): each lane's byte offsets into K, V, keep
+// and the bias are fixed for the whole kernel and the block advance is a
+// uniform scalar offset, so staging costs no registers, no LDS writes by the
+// waves and no per-block vector address arithmetic.  Wave (rg, qs) owns rows
+// rg*R.. and queries qs*16*QB..: S^T = K Q^T on MFMA with the accumulator
+// initialised from the bias fragment (shared by its R rows), p = exp2(s), row
+// sums sum_k keep[k] p[k] (bf16: one more MFMA per query block with the keep
+// flags as the A operand, so the sum is over the same rounded p the PV product
+// consumes; f32: fused multiply-adds), O^T += V^T P^T on MFMA.
 // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Map the
 // linear id L to (query block x, group) so that the nx query blocks of one
 // group (a set of rows of one head) run back to back on one XCD: that
@@ -775,17 +781,41 @@ __device__ __forceinline__ void xcd_group_map(int L, int nx, int ngroups, int& x
   x = s % nx;
 }
 
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes
+// land at lds + 16 l.  `base` / `bytes` describe a raw buffer (offsets at or
+// past `bytes` read as zero); voff is the lane's byte offset, soff a uniform
+// one.
+__device__ __forceinline__ void buffer_load_lds16(const void* base, uint32_t bytes, void* lds,
+                                                  uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voff, soff, 0, 0);
+#endif
+}
+__host__ __device__ __forceinline__ uint32_t clamp_bytes(uint64_t b) {
+  return b > 0xffffffffull ? 0xffffffffu : (uint32_t)b;
+}
+
 template <typename CT, int R, int QB, int RG, int QS>
 __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a, int nx,
                                                                         int ny) {
-  constexpr int NT = 64 * RG * QS;
+  constexpr int NW = RG * QS;
   constexpr int R_WG = RG * R, Q_WG = QS * 16 * QB;
   typedef CoreStage<CT, R_WG, Q_WG> Stage;
   constexpr int VEC = Stage::VEC, KCH = Stage::KCH;
-  constexpr int ROUNDS = (Stage::TOTAL + NT - 1) / NT;
+  constexpr bool kMfmaSum = sizeof(CT) == 2;
+  // direct-load instructions (64 lanes x 16 bytes) per region, dealt to the
+  // waves round-robin
+  constexpr int NKI = Stage::K_CHUNKS / 64, NBI = Stage::B_CHUNKS / 64;
+  constexpr int KPW = (NKI + NW - 1) / NW, BPW = (NBI + NW - 1) / NW;
+  static_assert(Stage::K_CHUNKS % 64 == 0 && Stage::B_CHUNKS % 64 == 0, "whole instructions");
+  static_assert(Stage::KP_CHUNKS <= 64, "keep flags of a block in one instruction");
   __shared__ Stage st[2];
 
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
   const int rg = w / QS, qs = w % QS;
   int bx, grp;
   xcd_group_map(blockIdx.x, nx, ny * a.heads, bx, grp);
@@ -798,60 +828,57 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
   const int bb = min(wg_row0, a.rows - 1) / a.rows_per_bias;
   const float* B = a.bias + ((size_t)bb * a.heads + h) * jp * jp;
 
-  // ---- staging plan: this thread's chunks (same for every key block) ----
-  const CT* src[ROUNDS];
-  int dst[ROUNDS];  // chunk index into the stage, or -1
+  // ---- staging plan: raw buffers based at the workgroup's first row ----
+  const int base_row = min(wg_row0, a.rows - 1);
+  const size_t row_elems = (size_t)a.heads * jp * 32;
+  const CT* kbase = a.k + (size_t)base_row * row_elems;
+  const CT* vbase = a.v + (size_t)base_row * row_elems;
+  const CT* kpbase = a.keep + (size_t)base_row * jp;
+  const uint32_t kv_bytes = clamp_bytes((uint64_t)(a.rows - base_row) * row_elems * sizeof(CT));
+  const uint32_t kp_bytes = clamp_bytes((uint64_t)(a.rows - base_row) * jp * sizeof(CT));
+  const uint32_t b_bytes = clamp_bytes((uint64_t)jp * jp * sizeof(float));
+  uint32_t ok[KPW], ov[KPW], ob[BPW], okp = 0;
 #pragma unroll
-  for (int rd = 0; rd < ROUNDS; ++rd) {
-    int idx = rd * NT + threadIdx.x;
-    src[rd] = nullptr;
-    dst[rd] = -1;
-    if (idx < 2 * Stage::K_CHUNKS) {  // K then V
-      const bool isv = idx >= Stage::K_CHUNKS;
-      if (isv) idx -= Stage::K_CHUNKS;
-      const int rr = idx / (32 * KCH), key = (idx / KCH) % 32, ch = idx % KCH;
-      const int row = min(wg_row0 + rr, a.rows - 1);
-      const size_t rh = (size_t)row * a.heads + h;
-      if (!isv) {
-        src[rd] = a.k + (rh * jp + key) * 32 + ch * VEC;
-        dst[rd] = (rr * 32 + key) * KCH + kswz(key, ch, KCH);
-      } else {  // V blocks are already in fragment order: copy 1:1
-        src[rd] = a.v + rh * jp * 32 + idx % (32 * KCH) * VEC;
-        dst[rd] = Stage::K_CHUNKS + idx;
-      }
-    } else if ((idx -= 2 * Stage::K_CHUNKS) < Stage::KP_CHUNKS) {
-      const int rr = idx / KCH, ch = idx % KCH;
-      const int row = min(wg_row0 + rr, a.rows - 1);
-      src[rd] = a.keep + (size_t)row * jp + ch * VEC;
-      dst[rd] = 2 * Stage::K_CHUNKS + idx;
-    } else if ((idx -= Stage::KP_CHUNKS) < Stage::B_CHUNKS) {
-      const int qq = idx >> 3, ch = idx & 7;
-      const int qrow = min(min(wg_q0 + qq, n - 1), jp - 1);
-      src[rd] = reinterpret_cast<const CT*>(B + (size_t)qrow * jp + ch * 4);
-      dst[rd] = 2 * Stage::K_CHUNKS + Stage::KP_CHUNKS + qq * 8 + (ch ^ (qq & 7));
-    }
+  for (int j = 0; j < KPW; ++j) {
+    const int p = (wu + j * NW) * 64 + l;  // chunk position in the K (V) region
+    const int rr = min(p / (32 * KCH), R_WG - 1), key = (p / KCH) % 32;
+    const int ch = kswz(key, p % KCH, KCH);  // an involution: the source chunk
+    const int lrow = min(wg_row0 + rr, a.rows - 1) - base_row;
+    const size_t rh = (size_t)lrow * a.heads + h;
+    ok[j] = (uint32_t)(((rh * jp + key) * 32 + ch * VEC) * sizeof(CT));
+    ov[j] = (uint32_t)((rh * jp * 32 + (p % (32 * KCH)) * VEC) * sizeof(CT));
   }
-  // per key block the K/V/keep sources advance by 32 keys, bias sources by 32 f32
-  auto advance = [&](int rd, int k0) -> const f32x4* {
-    const int idx = rd * NT + threadIdx.x;
-    size_t step;
-    if (idx < Stage::K_CHUNKS) step = (size_t)k0 * 32;                  // K rows
-    else if (idx < 2 * Stage::K_CHUNKS) step = (size_t)k0 * 32;         // V blocks (1024/32 keys)
-    else if (idx < 2 * Stage::K_CHUNKS + Stage::KP_CHUNKS) step = (size_t)k0;
-    else step = (size_t)k0 * sizeof(float) / sizeof(CT);
-    return reinterpret_cast<const f32x4*>(src[rd] + step);
-  };
-  f32x4 stage_reg[ROUNDS];
-  auto fetch = [&](int k0) {
 #pragma unroll
-    for (int rd = 0; rd < ROUNDS; ++rd)
-      if (dst[rd] >= 0) stage_reg[rd] = *advance(rd, k0);
-  };
-  auto commit = [&](int buf) {
-    f32x4* base = reinterpret_cast<f32x4*>(&st[buf]);
+  for (int j = 0; j < BPW; ++j) {
+    const int p = (wu + j * NW) * 64 + l;
+    const int qq = p >> 3, ch = (p & 7) ^ (qq & 7);
+    const int qrow = min(min(wg_q0 + qq, n - 1), jp - 1);
+    ob[j] = (uint32_t)(((size_t)qrow * jp + ch * 4) * sizeof(float));
+  }
+  if (l < Stage::KP_CHUNKS) {
+    const int rr = l / KCH, ch = l % KCH;
+    const int lrow = min(wg_row0 + rr, a.rows - 1) - base_row;
+    okp = (uint32_t)(((size_t)lrow * jp + ch * VEC) * sizeof(CT));
+  }
+  // loads of key block t into stage buffer `buf`
+  auto issue = [&](int t, int buf) {
+    Stage& S = st[buf];
+    const uint32_t skv = (uint32_t)t * 32 * 32 * sizeof(CT);
 #pragma unroll
-    for (int rd = 0; rd < ROUNDS; ++rd)
-      if (dst[rd] >= 0) base[dst[rd]] = stage_reg[rd];
+    for (int j = 0; j < KPW; ++j) {
+      const int i = wu + j * NW;
+      if (i < NKI) {
+        buffer_load_lds16(kbase, kv_bytes, S.k + i * 64, ok[j], skv);
+        buffer_load_lds16(vbase, kv_bytes, S.v + i * 64, ov[j], skv);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+      const int i = wu + j * NW;
+      if (i < NBI) buffer_load_lds16(B, b_bytes, S.b + i * 64, ob[j], (uint32_t)t * 32 * sizeof(float));
+    }
+    if (wu == NW - 1 && l < Stage::KP_CHUNKS)
+      buffer_load_lds16(kpbase, kp_bytes, S.kp, okp, (uint32_t)t * 32 * sizeof(CT));
   };
 
   // ---- per-wave state ----
@@ -884,6 +911,7 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
 
   f32x4 o[R][2][QB];
   float lsum[R][QB];
+  f32x4 lacc[kMfmaSum ? R : 1][QB];  // bf16: row sums on the MFMA
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -891,15 +919,18 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
       o[r][0][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
       o[r][1][qb] = o[r][0][qb];
       lsum[r][qb] = 0.f;
+      if constexpr (kMfmaSum) lacc[r][qb] = o[r][0][qb];
     }
 
-  fetch(0);
-  commit(0);
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   const int nblk = jp >> 5;
   for (int t = 0; t < nblk; ++t) {
     const int buf = t & 1;
-    if (t + 1 < nblk) fetch((t + 1) * 32);
+    // buffer buf ^ 1 was last read in iteration t - 1, which every wave has
+    // left (barrier at its end)
+    if (t + 1 < nblk) issue(t + 1, buf ^ 1);
     if (!skip) {
       const Stage& S = st[buf];
       const CT* Ks = reinterpret_cast<const CT*>(S.k);
@@ -944,15 +975,22 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e]));
-          lsum[r][qb] = psum8(pf[qb], kpf, lsum[r][qb]);
+          if constexpr (!kMfmaSum) lsum[r][qb] = psum8(pf[qb], kpf, lsum[r][qb]);
         }
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+        if constexpr (kMfmaSum) {
+          // lane (g, r16) ends with the sum for query r16 in every slot
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) mma(lacc[r][qb], kpf, pf[qb]);
+        }
       }
     }
-    if (t + 1 < nblk) commit(buf ^ 1);
+    // this wave's loads of block t + 1 have landed; the barrier makes every
+    // wave's visible and ends all reads of buffer buf
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
   if (skip) return;
@@ -966,7 +1004,9 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
     bool ur = false;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const float lt = group_sum_fast(lsum[r][qb]);
+      float lt;
+      if constexpr (kMfmaSum) lt = lacc[r][qb][0];
+      else lt = group_sum_fast(lsum[r][qb]);
       ur = ur || !(lt >= kUnderflowSum);
       inv[r][qb] = 1.0f / lt;
     }
