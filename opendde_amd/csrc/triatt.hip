@@ -48,6 +48,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemm.hpp"
 #include "lnpass.hpp"
@@ -925,14 +927,18 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
   issue(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  // Two key blocks per trip with the stage buffer a compile-time constant, so
+  // every LDS fragment address is a lane base plus an immediate offset and
+  // the direct loads' LDS destinations are constants (no per-block address
+  // arithmetic); nblk is even because jp is a multiple of 64.
   const int nblk = jp >> 5;
-  for (int t = 0; t < nblk; ++t) {
-    const int buf = t & 1;
-    // buffer buf ^ 1 was last read in iteration t - 1, which every wave has
-    // left (barrier at its end)
-    if (t + 1 < nblk) issue(t + 1, buf ^ 1);
+  auto block = [&](auto buf_c, int t) {
+    constexpr int kBuf = decltype(buf_c)::value;
+    // buffer kBuf ^ 1 was last read in the previous block, which every wave
+    // has left (barrier at its end)
+    if (t + 1 < nblk) issue(t + 1, kBuf ^ 1);
     if (!skip) {
-      const Stage& S = st[buf];
+      const Stage& S = st[kBuf];
       const CT* Ks = reinterpret_cast<const CT*>(S.k);
       const CT* Vs = reinterpret_cast<const CT*>(S.v);
       const CT* KPs = reinterpret_cast<const CT*>(S.kp);
@@ -989,9 +995,13 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
       }
     }
     // this wave's loads of block t + 1 have landed; the barrier makes every
-    // wave's visible and ends all reads of buffer buf
+    // wave's visible and ends all reads of buffer kBuf
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+  for (int t = 0; t < nblk; t += 2) {
+    block(std::integral_constant<int, 0>{}, t);
+    block(std::integral_constant<int, 1>{}, t + 1);
   }
   if (skip) return;
 

@@ -3,8 +3,10 @@
 Mirrors opendde/model/layer_norm/layer_norm.py:
 * ``_FAST_LAYER_NORM_REQUIRED_SYMBOLS`` and the validation of a loaded
   extension (:31-58);
-* ``_load_fast_layer_norm()``: lazy, lock-protected, cached load, including a
-  cached failure logged once (:61-108).  Without a GPU it returns ``None`` and
+* ``_load_fast_layer_norm_cuda_v2()`` and the module global
+  ``fast_layer_norm_cuda_v2``: lazy, lock-protected, cached load, including a
+  cached failure logged once (:61-108); the reference's own names, which its
+  tests patch and reset.  Without a GPU it returns ``None`` and
   does not mark the load as attempted.  The extension here is
   ``opendde_amd.fast_layer_norm`` over ``libopendde_amd.so``; nothing is
   compiled at run time;
@@ -45,7 +47,7 @@ _FAST_LAYER_NORM_REQUIRED_SYMBOLS = (
     "backward_with_both_affine",
 )
 
-fast_layer_norm: Any = None
+fast_layer_norm_cuda_v2: Any = None  # the loaded extension (the reference's name)
 _fast_layer_norm_load_attempted = False
 _fast_layer_norm_load_error: Optional[BaseException] = None
 _fast_layer_norm_load_lock = threading.Lock()
@@ -60,16 +62,16 @@ def _validate_fast_layer_norm_extension(extension: Any) -> Any:
     return extension
 
 
-def _load_fast_layer_norm() -> Any:
+def _load_fast_layer_norm_cuda_v2() -> Any:
     """The validated extension module, or ``None`` (no GPU, or load failed)."""
-    global fast_layer_norm, _fast_layer_norm_load_attempted, _fast_layer_norm_load_error
+    global fast_layer_norm_cuda_v2, _fast_layer_norm_load_attempted, _fast_layer_norm_load_error
     if not torch.cuda.is_available():
         return None
     if _fast_layer_norm_load_attempted:
-        return fast_layer_norm
+        return fast_layer_norm_cuda_v2
     with _fast_layer_norm_load_lock:
         if _fast_layer_norm_load_attempted:
-            return fast_layer_norm
+            return fast_layer_norm_cuda_v2
         try:
             extension = importlib.import_module(".fast_layer_norm", package=__package__)
             extension = _validate_fast_layer_norm_extension(extension)
@@ -79,15 +81,15 @@ def _load_fast_layer_norm() -> Any:
             logger.warning("Fast LayerNorm HIP library is unavailable: %s", error)
             _fast_layer_norm_load_error = error
             extension = None
-        fast_layer_norm = extension
+        fast_layer_norm_cuda_v2 = extension
         _fast_layer_norm_load_attempted = True
         return extension
 
 
 def _reset_loader_for_tests() -> None:
-    global fast_layer_norm, _fast_layer_norm_load_attempted, _fast_layer_norm_load_error
+    global fast_layer_norm_cuda_v2, _fast_layer_norm_load_attempted, _fast_layer_norm_load_error
     with _fast_layer_norm_load_lock:
-        fast_layer_norm = None
+        fast_layer_norm_cuda_v2 = None
         _fast_layer_norm_load_attempted = False
         _fast_layer_norm_load_error = None
 
@@ -98,7 +100,7 @@ class FusedLayerNormAffineFunction(torch.autograd.Function):
                 bias: Optional[torch.Tensor], normalized_shape: torch.Size,
                 eps: float) -> torch.Tensor:
         d = input.dtype
-        ext = fast_layer_norm
+        ext = fast_layer_norm_cuda_v2
         ctx.normalized_shape = normalized_shape
         ctx.eps = eps
         input_ = input.contiguous()
@@ -121,7 +123,7 @@ class FusedLayerNormAffineFunction(torch.autograd.Function):
     def backward(ctx: Any, *grad_outputs: Any):
         (grad_output,) = grad_outputs
         d = grad_output.dtype
-        ext = fast_layer_norm
+        ext = fast_layer_norm_cuda_v2
         input_, weight_, bias_, mean, invvar = ctx.saved_tensors
         g = grad_output.contiguous()
         shape, eps = ctx.normalized_shape, ctx.eps
@@ -170,7 +172,7 @@ class FusedLayerNorm(torch.nn.Module):
     def forward(self, input: torch.Tensor) -> torch.Tensor:
         if not input.is_cuda:
             return F.layer_norm(input, self.normalized_shape, self.weight, self.bias, self.eps)
-        if _load_fast_layer_norm() is None:
+        if _load_fast_layer_norm_cuda_v2() is None:
             raise RuntimeError("fast LayerNorm was selected but the HIP library is unusable: "
                                f"{_fast_layer_norm_load_error}")
         return FusedLayerNormAffineFunction.apply(input, self.weight, self.bias,

@@ -35,7 +35,7 @@ def reset_loader():
 
 
 def test_fused_layer_norm_uses_torch_for_cpu(monkeypatch):
-    monkeypatch.setattr(layer_norm, "_load_fast_layer_norm",
+    monkeypatch.setattr(layer_norm, "_load_fast_layer_norm_cuda_v2",
                         lambda: pytest.fail("CPU LayerNorm loaded the HIP library"))
     for scale, offset in ((True, True), (True, False), (False, True), (False, False)):
         module = layer_norm.FusedLayerNorm(4, create_scale=scale, create_offset=offset)
@@ -64,15 +64,15 @@ def test_loaded_extension_is_cached(monkeypatch, reset_loader):
 
     monkeypatch.setattr(layer_norm.torch.cuda, "is_available", lambda: True)
     monkeypatch.setattr(layer_norm.importlib, "import_module", counting_import)
-    ext = layer_norm._load_fast_layer_norm()
+    ext = layer_norm._load_fast_layer_norm_cuda_v2()
     assert ext is fln
-    assert layer_norm._load_fast_layer_norm() is ext
+    assert layer_norm._load_fast_layer_norm_cuda_v2() is ext
     assert imports == [(".fast_layer_norm", layer_norm.__package__)]
 
 
 def test_loader_without_gpu_does_not_mark_attempted(monkeypatch, reset_loader):
     monkeypatch.setattr(layer_norm.torch.cuda, "is_available", lambda: False)
-    assert layer_norm._load_fast_layer_norm() is None
+    assert layer_norm._load_fast_layer_norm_cuda_v2() is None
     assert not layer_norm._fast_layer_norm_load_attempted
 
 
@@ -86,11 +86,11 @@ def test_load_failure_is_cached_and_logged_once(caplog, monkeypatch, reset_loade
     monkeypatch.setattr(layer_norm.torch.cuda, "is_available", lambda: True)
     monkeypatch.setattr(layer_norm.importlib, "import_module", broken_import)
     caplog.set_level(logging.WARNING, logger=layer_norm.__name__)
-    assert layer_norm._load_fast_layer_norm() is None
-    assert layer_norm._load_fast_layer_norm() is None
+    assert layer_norm._load_fast_layer_norm_cuda_v2() is None
+    assert layer_norm._load_fast_layer_norm_cuda_v2() is None
     assert len(calls) == 1
     assert layer_norm._fast_layer_norm_load_attempted
-    assert layer_norm.fast_layer_norm is None
+    assert layer_norm.fast_layer_norm_cuda_v2 is None
     assert "missing required symbols" in str(layer_norm._fast_layer_norm_load_error)
     assert sum("Fast LayerNorm HIP library is unavailable" in r.message
                for r in caplog.records) == 1
@@ -103,7 +103,7 @@ def test_backward_returns_one_gradient_per_input(monkeypatch):
         backward_with_both_affine=lambda g, mean, invvar, x, shape, w, b, eps: (
             g, torch.zeros_like(w), torch.zeros_like(b)),
     )
-    monkeypatch.setattr(layer_norm, "fast_layer_norm", extension)
+    monkeypatch.setattr(layer_norm, "fast_layer_norm_cuda_v2", extension)
     x = torch.randn(2, 4, requires_grad=True)
     w = torch.ones(4, requires_grad=True)
     b = torch.zeros(4, requires_grad=True)
@@ -124,7 +124,7 @@ def test_dispatch_picks_the_symbol_for_the_affine_variant(monkeypatch):
 
     ext = SimpleNamespace(**{s: fwd(s) for s in layer_norm._FAST_LAYER_NORM_REQUIRED_SYMBOLS
                              if s.startswith("forward")})
-    monkeypatch.setattr(layer_norm, "fast_layer_norm", ext)
+    monkeypatch.setattr(layer_norm, "fast_layer_norm_cuda_v2", ext)
     x = torch.randn(3, 4)
     w, b = torch.ones(4), torch.zeros(4)
     for wi, bi in ((None, None), (None, b), (w, None), (w, b)):
