@@ -95,6 +95,14 @@ typedef struct odde_triatt_args {
   float eps;          /* 1e-5 */
   void* workspace;
   uint64_t workspace_bytes;
+  /* Leading batch dims flattened to one count (the reference's modules take
+   * z [*, N, N, C], triangular.py:648-706).  batch = 0 or 1: one view.  With
+   * batch = B > 1, view b reads z + b*z_sb and mask + b*mask_sb and writes
+   * out + b*out_sb (strides in elements; mask_sb may be 0 for a broadcast
+   * mask).  One call runs the B views in order on the stream, sharing one
+   * workspace of the size odde_triatt_workspace_bytes reports. */
+  int32_t batch;
+  int64_t z_sb, mask_sb, out_sb;
 } odde_triatt_args;
 
 int odde_triatt_workspace_bytes(const odde_triatt_args* args, uint64_t* bytes);
@@ -174,6 +182,10 @@ typedef struct odde_trimul_args {
    * rounding after the LayerNorm.  W' is formed from this f32 copy when it
    * is given (one rounding), else from the bf16 p_out_weight. */
   const float* p_out_weight_f32;
+  /* Leading batch dims, with the meaning they have in odde_triatt_args; the
+   * reference's module takes z [*, N, N, C] (triangular.py:459-567). */
+  int32_t batch;
+  int64_t z_sb, mask_sb, out_sb;
 } odde_trimul_args;
 
 int odde_trimul_workspace_bytes(const odde_trimul_args* args, uint64_t* bytes);

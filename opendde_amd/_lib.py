@@ -52,6 +52,7 @@ class TriattArgs(ctypes.Structure):
         ("w_bias", _vp), ("w_q", _vp), ("w_k", _vp), ("w_v", _vp), ("w_g", _vp), ("w_o", _vp),
         ("inf", _f32), ("eps", _f32),
         ("workspace", _vp), ("workspace_bytes", _u64),
+        ("batch", _i32), ("z_sb", _i64), ("mask_sb", _i64), ("out_sb", _i64),
     ]
 
 
@@ -83,6 +84,7 @@ class TrimulArgs(ctypes.Structure):
         ("eps", _f32),
         ("workspace", _vp), ("workspace_bytes", _u64),
         ("p_out_weight_f32", _vp),
+        ("batch", _i32), ("z_sb", _i64), ("mask_sb", _i64), ("out_sb", _i64),
     ]
 
 

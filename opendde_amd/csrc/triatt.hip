@@ -1782,6 +1782,7 @@ int check_triatt(const odde_triatt_args* a) {
     return set_error(ODDE_EINVAL, "triatt: struct_size mismatch (ABI version skew)");
   if (a->n <= 0 || a->c <= 0 || a->heads <= 0)
     return set_error(ODDE_EINVAL, "triatt: n, c and heads must be positive");
+  if (a->batch < 0) return set_error(ODDE_EINVAL, "triatt: batch must be >= 0");
   if (a->head_dim != 32) return set_error(ODDE_EUNSUPPORTED, "triatt: head_dim must be 32");
   if (a->heads > 16) return set_error(ODDE_EUNSUPPORTED, "triatt: at most 16 heads");
   if (!valid_dtype(a->z_dtype) || !valid_dtype(a->compute_dtype))
@@ -2085,13 +2086,24 @@ int odde_triatt_fwd(const odde_triatt_args* a, void* stream) {
       (reinterpret_cast<uintptr_t>(a->workspace) & 255))
     return set_error(ODDE_EWORKSPACE, "triatt: workspace missing, too small or not 256-byte aligned");
   const int zes = dtype_size(a->z_dtype);
+  const int nb = a->batch > 1 ? a->batch : 1;
+  const int64_t sb = nb > 1 ? (a->z_sb | a->out_sb) : 0;
   if ((reinterpret_cast<uintptr_t>(a->z) | reinterpret_cast<uintptr_t>(a->out)) & 15 ||
-      ((a->z_s0 | a->z_s1 | a->out_s0 | a->out_s1) * zes) & 15)
+      ((a->z_s0 | a->z_s1 | a->out_s0 | a->out_s1 | sb) * zes) & 15)
     return set_error(ODDE_EINVAL, "triatt: z/out rows must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) return run_triatt<float, float>(a, st);
-  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_BF16) return run_triatt<float, bf16>(a, st);
-  return run_triatt<bf16, bf16>(a, st);
+  // The views of a batch run in order on the stream and share the workspace.
+  odde_triatt_args e = *a;
+  for (int b = 0; b < nb; ++b) {
+    e.z = static_cast<const char*>(a->z) + (int64_t)b * a->z_sb * zes;
+    e.out = static_cast<char*>(a->out) + (int64_t)b * a->out_sb * zes;
+    e.mask = a->mask ? a->mask + (int64_t)b * a->mask_sb : nullptr;
+    if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) rc = run_triatt<float, float>(&e, st);
+    else if (a->z_dtype == ODDE_F32) rc = run_triatt<float, bf16>(&e, st);
+    else rc = run_triatt<bf16, bf16>(&e, st);
+    if (rc) return rc;
+  }
+  return ODDE_OK;
 }
 
 }  // extern "C"

@@ -930,6 +930,7 @@ int check_trimul(const odde_trimul_args* a) {
     return set_error(ODDE_EINVAL, "trimul: struct_size mismatch (ABI version skew)");
   if (a->n <= 0 || a->c <= 0 || a->c_hidden <= 0)
     return set_error(ODDE_EINVAL, "trimul: n, c and c_hidden must be positive");
+  if (a->batch < 0) return set_error(ODDE_EINVAL, "trimul: batch must be >= 0");
   if (!kdim(a->c) || !kdim(a->c_hidden))
     return set_error(ODDE_EUNSUPPORTED, "trimul: c and c_hidden must be 64, 128, 256 or 384");
   if (!valid_dtype(a->z_dtype) || !valid_dtype(a->compute_dtype))
@@ -1118,13 +1119,24 @@ int odde_trimul_fwd(const odde_trimul_args* a, void* stream) {
       (reinterpret_cast<uintptr_t>(a->workspace) & 255))
     return set_error(ODDE_EWORKSPACE, "trimul: workspace missing, too small or not 256-byte aligned");
   const int zes = dtype_size(a->z_dtype);
+  const int nb = a->batch > 1 ? a->batch : 1;
+  const int64_t sb = nb > 1 ? (a->z_sb | a->out_sb) : 0;
   if ((reinterpret_cast<uintptr_t>(a->z) | reinterpret_cast<uintptr_t>(a->out)) & 15 ||
-      ((a->z_s0 | a->z_s1 | a->out_s0 | a->out_s1) * zes) & 15)
+      ((a->z_s0 | a->z_s1 | a->out_s0 | a->out_s1 | sb) * zes) & 15)
     return set_error(ODDE_EINVAL, "trimul: z/out rows must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) return run_trimul<float, float>(a, st);
-  if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_BF16) return run_trimul<float, bf16>(a, st);
-  return run_trimul<bf16, bf16>(a, st);
+  // The views of a batch run in order on the stream and share the workspace.
+  odde_trimul_args e = *a;
+  for (int b = 0; b < nb; ++b) {
+    e.z = static_cast<const char*>(a->z) + (int64_t)b * a->z_sb * zes;
+    e.out = static_cast<char*>(a->out) + (int64_t)b * a->out_sb * zes;
+    e.mask = a->mask ? a->mask + (int64_t)b * a->mask_sb : nullptr;
+    if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) rc = run_trimul<float, float>(&e, st);
+    else if (a->z_dtype == ODDE_F32) rc = run_trimul<float, bf16>(&e, st);
+    else rc = run_trimul<bf16, bf16>(&e, st);
+    if (rc) return rc;
+  }
+  return ODDE_OK;
 }
 
 }  // extern "C"

@@ -7,11 +7,15 @@ opendde/config/inference.py:23,83-170, opendde/utils/environment.py:84-97,
 kernels.  ``"hip"`` names it; ``"cuequivariance"`` is accepted as an alias so
 existing configs and call sites select the same accelerated slot unchanged.
 
-Module-level policy (as in the reference): an accelerated request on a GPU
-tensor runs the HIP kernels or raises; on a CPU tensor it runs the torch path
-(layers.py:455-459, triangular.py:482-486).  The reference's extra cuEq-only
-fallbacks (J <= 16 for attention, c_hidden != c_z for multiplication) do not
-apply: the HIP kernels take those shapes.
+Module-level policy (as in the reference): an accelerated request on a CPU
+tensor runs the torch path (layers.py:455-459, triangular.py:482-486); on a
+GPU tensor it runs the HIP kernels when they cover the call's shape and dtype
+and the torch path otherwise, logged once per module and reason, as the
+reference's slot falls back to torch for configurations its kernel lacks
+(layers.py:466-468).  A missing or unloadable library is never a reason to
+fall back: the call raises.  The reference's cuEq-only shape gates (J <= 16
+for attention, c_hidden != c_z for multiplication) are not carried over: the
+HIP kernels take those shapes.
 """
 
 from __future__ import annotations
@@ -31,6 +35,18 @@ TRIANGLE_KERNELS = ("auto",) + MODULE_KERNELS
 
 def is_accelerated(name: str) -> bool:
     return name in ACCELERATED
+
+
+_fallbacks_noted: set = set()
+
+
+def note_fallback(module: str, reason: str) -> None:
+    """Log, once per (module, reason), that an accelerated request on a GPU
+    tensor ran the torch path because the kernels do not cover the call."""
+    key = (module, reason)
+    if key not in _fallbacks_noted:
+        _fallbacks_noted.add(key)
+        logger.warning("%s: HIP kernels do not cover %s; running the torch path", module, reason)
 
 
 def check_attention_kernel(name: str) -> None:

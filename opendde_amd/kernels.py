@@ -4,7 +4,9 @@ PyTorch is used here only as plumbing: it owns device memory (outputs and the
 per-call workspace, via the caching allocator) and names the current stream.
 All arithmetic happens in the gfx950 kernels of ``libopendde_amd.so``.
 There is no fallback in this module: unsupported shapes, non-GPU tensors or a
-missing library raise.
+missing library raise.  The ``*_unsupported`` predicates name the shapes the
+kernels do not cover, so that the modules can route those calls to their
+torch path before reaching an entry point.
 """
 
 from __future__ import annotations
@@ -56,12 +58,27 @@ def _require_gpu(*ts: torch.Tensor) -> None:
 
 
 def _pair_view_ok(t: torch.Tensor, name: str) -> None:
-    if t.dim() != 3:
-        raise ValueError(f"{name} must be [N, N, C], got {tuple(t.shape)}")
+    if t.dim() < 3:
+        raise ValueError(f"{name} must be [*, N, N, C], got {tuple(t.shape)}")
     if t.stride(-1) != 1:
         raise ValueError(f"{name} must have a unit channel stride")
-    if t.shape[0] != t.shape[1]:
+    if t.shape[-3] != t.shape[-2]:
         raise ValueError(f"{name} must be square in its pair dims")
+
+
+def _batch_view(t: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
+    """``t`` [*, N, N, C] as a [B, N, N, C] view (never a copy: ``out`` is
+    written through it) with B and the batch stride in elements."""
+    _pair_view_ok(t, name)
+    if t.numel() == 0:
+        return t, 0, 0
+    if t.dim() == 3:
+        return t.unsqueeze(0), 1, 0
+    try:
+        v = t.view((-1,) + tuple(t.shape[-3:]))
+    except RuntimeError:
+        raise ValueError(f"{name}'s leading dims must collapse to one batch stride") from None
+    return v, v.shape[0], v.stride(0) if v.shape[0] > 1 else 0
 
 
 # Converted weights are cached per source tensor *object* (held by weak
@@ -95,16 +112,87 @@ def prepared_cat(ts, dtype: torch.dtype) -> torch.Tensor:
                    lambda: torch.cat([t.detach() for t in ts], 0).to(dtype).contiguous())
 
 
-def _mask_view(mask: Optional[torch.Tensor], n: int, device) -> Tuple[Optional[torch.Tensor], int, int]:
+def _mask_view(mask: Optional[torch.Tensor], lead: Tuple[int, ...], n: int,
+               device) -> Tuple[Optional[torch.Tensor], int, int, int]:
+    """The mask as float32 [B, N, N] for z's leading dims ``lead`` (a mask
+    without them broadcasts: batch stride 0); returns (mask, s0, s1, sb)."""
     if mask is None:
-        return None, 0, 0
-    if mask.dim() != 2 or tuple(mask.shape) != (n, n):
-        raise ValueError(f"mask must be [N, N] = [{n}, {n}], got {tuple(mask.shape)}")
-    if mask.dtype != torch.float32:
-        mask = mask.float()
+        return None, 0, 0, 0
+    if mask.dim() < 2 or tuple(mask.shape[-2:]) != (n, n) or mask.dim() > len(lead) + 2:
+        raise ValueError(f"mask must be [*, N, N] = [..., {n}, {n}] over z's leading dims, "
+                         f"got {tuple(mask.shape)}")
     if mask.device != device:
         raise ValueError("mask must be on the same device as z")
-    return mask, mask.stride(0), mask.stride(1)
+    if mask.dtype != torch.float32:
+        mask = mask.float()
+    try:
+        m = mask.expand(tuple(lead) + (n, n)).reshape(-1, n, n)
+    except RuntimeError:
+        raise ValueError(f"mask {tuple(mask.shape)} does not broadcast to z's leading dims "
+                         f"{tuple(lead)}") from None
+    return m, m.stride(1), m.stride(2), m.stride(0) if m.shape[0] > 1 else 0
+
+
+# ---------------------------------------------------------------------------
+# coverage: why a call is outside what the kernels take (None = covered).
+# The modules run their torch path for such calls, as the reference's
+# accelerated slot does for configurations its kernel lacks
+# (opendde/model/triangular/layers.py:455-468, triangular.py:482-486); the
+# entry points below raise for them.
+# ---------------------------------------------------------------------------
+
+
+def _dtype_reason(t: torch.Tensor, compute_dtype: Optional[torch.dtype]) -> Optional[str]:
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        return f"{t.dtype} tensors (the kernels take float32 and bfloat16)"
+    ct = compute_dtype or autocast_compute_dtype(t)
+    if t.dtype == torch.bfloat16 and ct == torch.float32:
+        return "bf16 storage with fp32 arithmetic"
+    return None
+
+
+def triangle_attention_unsupported(z: torch.Tensor, heads: int, head_dim: int,
+                                   compute_dtype: Optional[torch.dtype] = None) -> Optional[str]:
+    """Reason the fused triangle attention does not take z [*, N, N, C] with
+    ``heads`` x ``head_dim``, or None."""
+    if head_dim != HEAD_DIM:
+        return f"per-head dim {head_dim} (the kernels take {HEAD_DIM})"
+    c = z.shape[-1]
+    if c not in SUPPORTED_CHANNELS or heads * HEAD_DIM not in SUPPORTED_CHANNELS:
+        return f"c={c}, heads={heads} (c and heads*32 must be in {SUPPORTED_CHANNELS})"
+    return _dtype_reason(z, compute_dtype)
+
+
+def triangle_multiplication_unsupported(z: torch.Tensor, c_hidden: int,
+                                        compute_dtype: Optional[torch.dtype] = None
+                                        ) -> Optional[str]:
+    """Reason the fused triangle multiplication does not take z [*, N, N, C]
+    with ``c_hidden``, or None."""
+    c = z.shape[-1]
+    if c not in SUPPORTED_CHANNELS or c_hidden not in SUPPORTED_CHANNELS:
+        return f"c={c}, c_hidden={c_hidden} (both must be in {SUPPORTED_CHANNELS})"
+    return _dtype_reason(z, compute_dtype)
+
+
+def attention_core_unsupported(q: torch.Tensor) -> Optional[str]:
+    """Reason the triangle attention core does not take q [*, H, J, D], or
+    None."""
+    if q.shape[-1] != HEAD_DIM:
+        return f"per-head dim {q.shape[-1]} (the core takes {HEAD_DIM})"
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        return f"{q.dtype} tensors (the core takes float32 and bfloat16)"
+    return None
+
+
+def transition_unsupported(x: torch.Tensor, c: int, n: int,
+                           compute_dtype: Optional[torch.dtype] = None) -> Optional[str]:
+    """Reason the fused transition does not take rows x [*, c] with
+    intermediate factor ``n``, or None."""
+    if n != 4 or c not in TRANSITION_CHANNELS:
+        return f"c={c}, n={n} (the kernels take n=4, c in {TRANSITION_CHANNELS})"
+    if not x.is_contiguous():
+        return "non-contiguous rows"
+    return _dtype_reason(x, compute_dtype)
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
@@ -117,7 +205,8 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
                        out: Optional[torch.Tensor] = None, add_residual: bool = False,
                        compute_dtype: Optional[torch.dtype] = None, inf: float = 1e9,
                        eps: float = 1e-5) -> torch.Tensor:
-    """Fused triangle attention on one pair tensor z [N, N, C].
+    """Fused triangle attention on pair tensors z [*, N, N, C] (leading dims
+    run as one batch of views in one library call).
 
     starting=False runs the ending-node form by reading z, the mask and the
     output through transposed strides (no transposed copies).  With
@@ -126,8 +215,8 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     update.  Returns ``out``.
     """
     _require_gpu(z, mask)
-    _pair_view_ok(z, "z")
-    n, c = z.shape[0], z.shape[2]
+    zb, nbatch, z_sb = _batch_view(z, "z")
+    n, c = z.shape[-3], z.shape[-1]
     if c not in SUPPORTED_CHANNELS or heads * HEAD_DIM not in SUPPORTED_CHANNELS:
         raise NotImplementedError(
             f"HIP triangle attention supports c, heads*32 in {SUPPORTED_CHANNELS}; got c={c}, "
@@ -139,12 +228,14 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
         raise NotImplementedError("bf16 storage with fp32 compute is not provided")
     if out is None:
         out = torch.empty_like(z, memory_format=torch.contiguous_format)
-    _pair_view_ok(out, "out")
     if out.dtype != z.dtype or out.shape != z.shape:
         raise ValueError("out must match z in shape and dtype")
-    m, ms0, ms1 = _mask_view(mask, n, z.device)
-    zs0, zs1 = z.stride(0), z.stride(1)
-    os0, os1 = out.stride(0), out.stride(1)
+    ob, _, o_sb = _batch_view(out, "out")
+    m, ms0, ms1, m_sb = _mask_view(mask, z.shape[:-3], n, z.device)
+    if z.numel() == 0:
+        return out
+    zs0, zs1 = zb.stride(1), zb.stride(2)
+    os0, os1 = ob.stride(1), ob.stride(2)
     if not starting:
         zs0, zs1, ms0, ms1, os0, os1 = zs1, zs0, ms1, ms0, os1, os0
     lnw = prepared(ln_w, torch.float32)
@@ -161,6 +252,7 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     a.ln_w, a.ln_b = _ptr(lnw), _ptr(lnb)
     a.w_bias, a.w_q, a.w_k, a.w_v, a.w_g, a.w_o = (_ptr(w) for w in ws)
     a.inf, a.eps = float(inf), float(eps)
+    a.batch, a.z_sb, a.mask_sb, a.out_sb = nbatch, z_sb, m_sb, o_sb
     lib = _lib.load()
     nb = ctypes.c_uint64(0)
     _lib.check(lib.odde_triatt_workspace_bytes(ctypes.byref(a), ctypes.byref(nb)), "triatt workspace")
@@ -176,14 +268,15 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
                             out: Optional[torch.Tensor] = None, add_residual: bool = False,
                             compute_dtype: Optional[torch.dtype] = None,
                             eps: float = 1e-5, f32_out_weight: bool = True) -> torch.Tensor:
-    """Fused triangle multiplicative update on one pair tensor z [N, N, C];
+    """Fused triangle multiplicative update on z [*, N, N, C] (one library
+    call for the leading dims);
     same ``out`` / ``add_residual`` contract as :func:`triangle_attention`.
     ``p_in_weight``/``g_in_weight`` are [2*Ch, C] (a rows then b rows).
     ``f32_out_weight``: with bf16 compute, also hand the library linear_z in
     f32 (it folds LN_out into that weight with a single bf16 rounding)."""
     _require_gpu(z, mask)
-    _pair_view_ok(z, "z")
-    n, c = z.shape[0], z.shape[2]
+    zb, nbatch, z_sb = _batch_view(z, "z")
+    n, c = z.shape[-3], z.shape[-1]
     ch = p_in_weight.shape[0] // 2
     if c not in SUPPORTED_CHANNELS or ch not in SUPPORTED_CHANNELS:
         raise NotImplementedError(
@@ -194,10 +287,12 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
         raise NotImplementedError("bf16 storage with fp32 compute is not provided")
     if out is None:
         out = torch.empty_like(z, memory_format=torch.contiguous_format)
-    _pair_view_ok(out, "out")
     if out.dtype != z.dtype or out.shape != z.shape:
         raise ValueError("out must match z in shape and dtype")
-    m, ms0, ms1 = _mask_view(mask, n, z.device)
+    ob, _, o_sb = _batch_view(out, "out")
+    m, ms0, ms1, m_sb = _mask_view(mask, z.shape[:-3], n, z.device)
+    if z.numel() == 0:
+        return out
     f32 = torch.float32
     a = _lib.TrimulArgs()
     a.struct_size = ctypes.sizeof(_lib.TrimulArgs)
@@ -205,9 +300,10 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
     a.z_dtype, a.compute_dtype = dtype_code(z.dtype), dtype_code(ct)
     a.outgoing = 1 if outgoing else 0
     a.add_residual = 1 if add_residual else 0
-    a.z, a.z_s0, a.z_s1 = _ptr(z), z.stride(0), z.stride(1)
+    a.z, a.z_s0, a.z_s1 = _ptr(z), zb.stride(1), zb.stride(2)
     a.mask, a.mask_s0, a.mask_s1 = _ptr(m), ms0, ms1
-    a.out, a.out_s0, a.out_s1 = _ptr(out), out.stride(0), out.stride(1)
+    a.out, a.out_s0, a.out_s1 = _ptr(out), ob.stride(1), ob.stride(2)
+    a.batch, a.z_sb, a.mask_sb, a.out_sb = nbatch, z_sb, m_sb, o_sb
     keep = [prepared(norm_in_weight, f32), prepared(norm_in_bias, f32),
             prepared(norm_out_weight, f32), prepared(norm_out_bias, f32),
             prepared(p_in_weight, ct), prepared(g_in_weight, ct),

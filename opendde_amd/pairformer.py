@@ -51,9 +51,14 @@ class Transition(nn.Module):
         """The fused HIP kernels take n = 4 and c in ``K.TRANSITION_CHANNELS``,
         in bf16 arithmetic (bf16 inputs, or float32 inputs under bf16
         autocast, the reference's bf16 mode) or fp32 arithmetic (float32
-        inputs without autocast)."""
-        return (x.is_cuda and self.n == 4 and self.c_in in K.TRANSITION_CHANNELS
-                and x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous())
+        inputs without autocast).  A GPU call outside that is noted once and
+        runs the torch path."""
+        if not x.is_cuda:
+            return False
+        why = K.transition_unsupported(x, self.c_in, self.n)
+        if why is not None:
+            hook.note_fallback("Transition", why)
+        return why is None
 
     def hip_apply(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                   add_residual: bool = False, pair_bias: Optional[tuple] = None) -> torch.Tensor:
@@ -186,6 +191,13 @@ class AttentionPairBias(nn.Module):
         return self.attention(q_x=a, kv_x=a, attn_bias=bias, hip=hip)
 
 
+def _hip_covers(mod: nn.Module, z: torch.Tensor, name: str) -> bool:
+    why = mod.hip_unsupported(z)
+    if why is not None:
+        hook.note_fallback(name, why)
+    return why is None
+
+
 class PairformerBlock(nn.Module):
     """Algorithm 17 block (pairformer.py:59-273)."""
 
@@ -218,6 +230,10 @@ class PairformerBlock(nn.Module):
         hook.check_attention_kernel(triangle_attention)
         hip_mul = hook.is_accelerated(triangle_multiplicative) and z.is_cuda
         hip_att = hook.is_accelerated(triangle_attention) and z.is_cuda
+        accel = hip_mul or hip_att  # the transitions and the single track follow
+        # shapes or dtypes the kernels do not cover run the torch path
+        hip_mul = hip_mul and _hip_covers(self.tri_mul_out, z, "TriangleMultiplicativeUpdate")
+        hip_att = hip_att and _hip_covers(self.tri_att_start, z, "TriangleAttention")
 
         # triangle multiplications: z + update, in place when allowed
         for mod in (self.tri_mul_out, self.tri_mul_in):
@@ -246,7 +262,7 @@ class PairformerBlock(nn.Module):
             z = zt.transpose(-2, -3).contiguous()
 
         z_bias = None
-        if (hip_mul or hip_att) and self.pair_transition.hip_supported(z):
+        if accel and self.pair_transition.hip_supported(z):
             pb = None
             if self.c_s > 0 and z.dim() == 3 and self.attention_pair_bias.hip_pair_bias_ok():
                 z_bias = torch.empty((16, z.shape[0], z.shape[1]), dtype=torch.float32,
@@ -259,8 +275,8 @@ class PairformerBlock(nn.Module):
             z = z.add_(upd) if inplace_safe else z + upd
         if self.c_s > 0:
             s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias,
-                                             z_bias=z_bias, hip=hip_mul or hip_att)
-            if (hip_mul or hip_att) and self.single_transition.hip_supported(s):
+                                             z_bias=z_bias, hip=accel)
+            if accel and self.single_transition.hip_supported(s):
                 s = self.single_transition.hip_apply(s.contiguous(), add_residual=True)
             else:
                 s = s + self.single_transition(s)

@@ -5,8 +5,9 @@ opendde/model/triangular/layers.py:325-494).
 Same constructor and ``forward`` signatures, parameter names and
 kernel-selection kwarg.  ``"torch"`` runs plain PyTorch ops; ``"hip"`` (alias
 ``"cuequivariance"``) on a GPU tensor runs the fused gfx950 kernels of
-``libopendde_amd.so`` and never falls back; on a CPU tensor it runs the torch
-ops, as the reference does.
+``libopendde_amd.so`` when they cover the call's shape and dtype, and the
+torch ops otherwise (logged once), as the reference's accelerated slot does;
+on a CPU tensor it runs the torch ops.  A missing library raises.
 """
 
 from __future__ import annotations
@@ -131,6 +132,12 @@ class Attention(nn.Module):
         use_hip = _use_hip(triangle_attention, q_x)
         q, k, v = self._prep_qkv(q_x, kv_x, apply_scale=not use_hip)
         if use_hip:
+            why = K.attention_core_unsupported(q)
+            if why is not None:
+                hook.note_fallback("Attention", why)
+                use_hip = False
+                q = q / math.sqrt(self.c_hidden)
+        if use_hip:
             if len(biases) != 2:
                 raise ValueError("the accelerated slot takes [mask_bias, triangle_bias]")
             scale = 1.0 / math.sqrt(self.c_hidden)
@@ -165,31 +172,23 @@ class TriangleAttention(nn.Module):
     def hip_apply(self, z: torch.Tensor, mask: Optional[torch.Tensor], *, transpose: bool = False,
                   out: Optional[torch.Tensor] = None, add_residual: bool = False,
                   compute_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-        """Fused HIP forward on z [*, N, N, C] (leading dims looped).  With
-        ``transpose`` the module acts on the transposed pair view (the
-        ending-node form the Pairformer builds around a starting-node module)
-        without copying z.  ``add_residual`` writes z + update into ``out``."""
-        starting = self.starting != transpose
-        lead = z.shape[:-3]
-        zf = z.reshape((-1,) + tuple(z.shape[-3:]))
-        mf = None
-        if mask is not None:
-            mf = mask.expand(lead + tuple(z.shape[-3:-1])).reshape((-1,) + tuple(z.shape[-3:-1]))
-        if out is None:
-            out = torch.empty_like(zf, memory_format=torch.contiguous_format)
-            of = out
-        else:
-            of = out.reshape((-1,) + tuple(out.shape[-3:]))
+        """Fused HIP forward on z [*, N, N, C] (the leading dims in one library
+        call).  With ``transpose`` the module acts on the transposed pair view
+        (the ending-node form the Pairformer builds around a starting-node
+        module) without copying z.  ``add_residual`` writes z + update into
+        ``out``."""
         mha = self.mha
-        for b in range(zf.shape[0]):
-            K.triangle_attention(
-                zf[b], None if mf is None else mf[b],
-                ln_w=self.layer_norm.weight, ln_b=self.layer_norm.bias,
-                w_bias=self.linear.weight, w_q=mha.linear_q.weight, w_k=mha.linear_k.weight,
-                w_v=mha.linear_v.weight, w_g=mha.linear_g.weight, w_o=mha.linear_o.weight,
-                heads=self.no_heads, starting=starting, out=of[b], add_residual=add_residual,
-                compute_dtype=compute_dtype, inf=self.inf, eps=self.layer_norm.eps)
-        return of.reshape(z.shape) if out is of else out
+        return K.triangle_attention(
+            z, mask, ln_w=self.layer_norm.weight, ln_b=self.layer_norm.bias,
+            w_bias=self.linear.weight, w_q=mha.linear_q.weight, w_k=mha.linear_k.weight,
+            w_v=mha.linear_v.weight, w_g=mha.linear_g.weight, w_o=mha.linear_o.weight,
+            heads=self.no_heads, starting=self.starting != transpose, out=out,
+            add_residual=add_residual, compute_dtype=compute_dtype, inf=self.inf,
+            eps=self.layer_norm.eps)
+
+    def hip_unsupported(self, z: torch.Tensor) -> Optional[str]:
+        """Reason the fused kernels do not take this module on z, or None."""
+        return K.triangle_attention_unsupported(z, self.no_heads, self.c_hidden)
 
     # -- torch path ----------------------------------------------------------
     def _chunk(self, x, biases, chunk_size, triangle_attention="torch"):
@@ -215,9 +214,12 @@ class TriangleAttention(nn.Module):
                 inplace_safe: bool = False) -> torch.Tensor:
         hook.check_attention_kernel(triangle_attention)
         if _use_hip(triangle_attention, x):
-            # chunk_size only bounds memory in the torch path; the fused HIP
-            # path never materialises the logits.
-            return self.hip_apply(x, mask)
+            why = self.hip_unsupported(x)
+            if why is None:
+                # chunk_size only bounds memory in the torch path; the fused
+                # HIP path never materialises the logits.
+                return self.hip_apply(x, mask)
+            hook.note_fallback("TriangleAttention", why)
         if mask is None:
             mask = x.new_ones(x.shape[:-1])
         if not self.starting:
@@ -271,33 +273,24 @@ class TriangleMultiplicativeUpdate(nn.Module):
     def hip_apply(self, z: torch.Tensor, mask: Optional[torch.Tensor], *,
                   out: Optional[torch.Tensor] = None, add_residual: bool = False,
                   compute_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-        """Fused HIP forward on z [*, N, N, C]; ``add_residual`` writes
-        z + update into ``out`` (which may be z: the in-place inference form)."""
-        lead = z.shape[:-3]
-        zf = z.reshape((-1,) + tuple(z.shape[-3:]))
-        mf = None
-        if mask is not None:
-            mf = mask.expand(lead + tuple(z.shape[-3:-1])).reshape((-1,) + tuple(z.shape[-3:-1]))
-        if out is None:
-            out = torch.empty_like(zf, memory_format=torch.contiguous_format)
-            of = out
-        else:
-            of = out.reshape((-1,) + tuple(out.shape[-3:]))
-        p_in = K.prepared_cat([self.linear_a_p.weight, self.linear_b_p.weight],
-                              compute_dtype or K.autocast_compute_dtype(z))
-        g_in = K.prepared_cat([self.linear_a_g.weight, self.linear_b_g.weight],
-                              compute_dtype or K.autocast_compute_dtype(z))
-        for b in range(zf.shape[0]):
-            K.triangle_multiplication(
-                zf[b], None if mf is None else mf[b], outgoing=self._outgoing,
-                norm_in_weight=self.layer_norm_in.weight, norm_in_bias=self.layer_norm_in.bias,
-                p_in_weight=p_in, g_in_weight=g_in,
-                norm_out_weight=self.layer_norm_out.weight,
-                norm_out_bias=self.layer_norm_out.bias,
-                p_out_weight=self.linear_z.weight, g_out_weight=self.linear_g.weight,
-                out=of[b], add_residual=add_residual, compute_dtype=compute_dtype,
-                eps=self.layer_norm_in.eps)
-        return of.reshape(z.shape) if out is of else out
+        """Fused HIP forward on z [*, N, N, C] (the leading dims in one library
+        call); ``add_residual`` writes z + update into ``out`` (which may be
+        z: the in-place inference form)."""
+        ct = compute_dtype or K.autocast_compute_dtype(z)
+        p_in = K.prepared_cat([self.linear_a_p.weight, self.linear_b_p.weight], ct)
+        g_in = K.prepared_cat([self.linear_a_g.weight, self.linear_b_g.weight], ct)
+        return K.triangle_multiplication(
+            z, mask, outgoing=self._outgoing,
+            norm_in_weight=self.layer_norm_in.weight, norm_in_bias=self.layer_norm_in.bias,
+            p_in_weight=p_in, g_in_weight=g_in,
+            norm_out_weight=self.layer_norm_out.weight, norm_out_bias=self.layer_norm_out.bias,
+            p_out_weight=self.linear_z.weight, g_out_weight=self.linear_g.weight,
+            out=out, add_residual=add_residual, compute_dtype=compute_dtype,
+            eps=self.layer_norm_in.eps)
+
+    def hip_unsupported(self, z: torch.Tensor) -> Optional[str]:
+        """Reason the fused kernels do not take this module on z, or None."""
+        return K.triangle_multiplication_unsupported(z, self.c_hidden)
 
     def forward(self, z: torch.Tensor, mask: Optional[torch.Tensor] = None,
                 inplace_safe: bool = False, _add_with_inplace: bool = False,
@@ -306,10 +299,13 @@ class TriangleMultiplicativeUpdate(nn.Module):
         hook.check_multiplicative_kernel(triangle_multiplicative)
         add = inplace_safe is True and _add_with_inplace
         if _use_hip(triangle_multiplicative, z):
-            if add:
-                # in-place inference form: z <- z + update, one fused pass
-                return self.hip_apply(z, mask, out=z, add_residual=True)
-            return self.hip_apply(z, mask)
+            why = self.hip_unsupported(z)
+            if why is None:
+                if add:
+                    # in-place inference form: z <- z + update, one fused pass
+                    return self.hip_apply(z, mask, out=z, add_residual=True)
+                return self.hip_apply(z, mask)
+            hook.note_fallback("TriangleMultiplicativeUpdate", why)
         if mask is None:
             mask = z.new_ones(z.shape[:-1])
         m = mask.unsqueeze(-1)

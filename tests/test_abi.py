@@ -78,6 +78,10 @@ def test_bad_arguments_return_status_and_message():
     a.z_dtype = a.compute_dtype = 0
     rc, msg = _status("odde_triatt_fwd", a)
     assert rc == -1 and "null" in msg
+    a.batch = -1
+    rc, msg = _status("odde_triatt_fwd", a)
+    assert rc == -1 and "batch" in msg
+    a.batch = 0
     t = _lib.TrimulArgs()
     t.struct_size = ctypes.sizeof(t)
     t.n, t.c, t.c_hidden = 32, 100, 128
