@@ -28,6 +28,8 @@
 //                      values = A rows x0 + .. + 16 i + 4 (lane/16) + e.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace odde {
@@ -153,6 +155,113 @@ __device__ __forceinline__ void gemm_nt_mainloop(
         }
   }
   // the stage buffers may be refilled by the caller's next mainloop
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  barrier_nofence();
+}
+
+// Software-pipelined form for KC = 64 and two stage buffers (whole 128-byte
+// lines per row and stage), used where one workgroup of 8 waves owns the CU
+// (the triangle contraction): the two K32 halves of stage s are multiplied in
+// turn; the fragments of half 1 are read under half 0's MFMAs, and those of
+// stage s+1's half 0 under half 1's.  The one barrier per stage sits between
+// the halves, when every wave holds all of stage s in registers: it frees
+// buffer s % 2 for stage s+2 and publishes stage s+1.
+template <int TX, int TY, int WX, bool kPairCols, typename ARow, typename BRow>
+__device__ __forceinline__ void gemm_nt_mainloop_pipe64(
+    ARow arow, BRow brow, int K, bf16* sm,
+    f32x4 (&acc)[GemmShape<TX, TY, WX, 64>::MX][GemmShape<TX, TY, WX, 64>::MY]) {
+  constexpr int KC = 64, NS = 2;
+  using S = GemmShape<TX, TY, WX, KC>;
+  constexpr int MX = S::MX, MY = S::MY, OPS_A = S::OPS_A, OPS = S::OPS;
+  constexpr int CPR = S::CPR, RPO = S::RPO;
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % WX, wy = w / WX;
+
+  const bf16* src0[OPS];
+#pragma unroll
+  for (int op = 0; op < OPS; ++op) {
+    const bool isb = op >= OPS_A;
+    const int blk = isb ? w * S::OPS_B + (op - OPS_A) : w * OPS_A + op;
+    const int row = blk * RPO + l / CPR;
+    src0[op] = (isb ? brow(row) : arow(row)) + gemm_swz<KC>(row, l % CPR) * 8;
+  }
+  auto issue = [&](int st) {
+    bf16* base = sm + (st % NS) * S::STAGE_ELEMS;
+#pragma unroll
+    for (int op = 0; op < OPS; ++op) {
+      const bool isb = op >= OPS_A;
+      const int blk = isb ? w * S::OPS_B + (op - OPS_A) : w * OPS_A + op;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(src0[op] + st * KC),
+          (__attribute__((address_space(3))) void*)(base + (isb ? TX * KC : 0) + blk * 512),
+          16, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < MX; ++i)
+#pragma unroll
+    for (int j = 0; j < MY; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int arow0 = (wx * (TX / WX) + r16) * KC;
+  const int brow0 = TX * KC + (wy * (TY / S::WY) + r16) * KC;
+  const int fsw0 = gemm_swz<KC>(r16, g) * 8, fsw1 = gemm_swz<KC>(r16, 4 + g) * 8;
+  Frag<bf16> fa[2][MX], fb[2][MY];
+  auto read_half = [&](auto set_c, int st, int fsw) {
+    constexpr int set = decltype(set_c)::value;
+    const bf16* base = sm + (st % NS) * S::STAGE_ELEMS;
+#pragma unroll
+    for (int j = 0; j < MY; ++j) fb[set][j].load(base + brow0 + j * 16 * KC + fsw);
+#pragma unroll
+    for (int i = 0; i < MX; ++i) fa[set][i].load(base + arow0 + i * 16 * KC + fsw);
+  };
+  auto mult = [&](auto set_c) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int i = 0; i < MX; ++i)
+#pragma unroll
+      for (int j = 0; j < MY; ++j) {
+        if constexpr (kPairCols) {
+          mma(acc[i][j], fb[set][j], fa[set][i]);
+        } else {
+          mma(acc[i][j], fa[set][i], fb[set][j]);
+        }
+      }
+    // one LDS read after each MFMA pair (reads requested just before)
+#pragma unroll
+    for (int k = 0; k < MX + MY; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, MX * MY - 2 * (MX + MY), 0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  const int nst = K / KC;
+  issue(0);
+  if (nst > 1) {
+    issue(1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  barrier_nofence();
+  read_half(I0{}, 0, fsw0);
+  for (int st = 0; st < nst; ++st) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // half 0 of stage st in registers
+    read_half(I1{}, st, fsw1);
+    mult(I0{});
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // all of stage st in registers
+    if (st + 1 < nst) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage st+1
+      barrier_nofence();  // every wave's; buffer st % 2 is free
+      if (st + 2 < nst) issue(st + 2);
+    }
+    // stage st+1's half 0 (after the last stage: an unused re-read)
+    read_half(I0{}, st + 1, fsw0);
+    mult(I1{});
+  }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   barrier_nofence();
 }

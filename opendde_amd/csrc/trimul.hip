@@ -184,9 +184,10 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(ContractArgs<CT> a
 
 // Large-tile form (bf16, Np a multiple of 256): TX x TY tiles per workgroup
 // of 8 waves, the shared NT mainloop (gemm.hpp) over k = 0..Np.
-template <int TX, int TY, int WX, int NS, int KC>
+template <int TX, int TY, int WX, int NS, int KC, bool kPipe = false>
 __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<bf16> a) {
   using S = GemmShape<TX, TY, WX, KC>;
+  static_assert(!kPipe || (KC == 64 && NS == 2), "the pipelined mainloop: two 64-k stages");
   __shared__ __attribute__((aligned(16))) bf16 sm[NS * S::STAGE_ELEMS];
   const int TXn = a.np / TX, TYn = a.np / TY;
   const int tiles = TXn * TYn;
@@ -208,13 +209,15 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
   // each 32 rows, row block 2p + b, MFMA row m is column 8 (m >> 2) + 4 b +
   // (m & 3), so a lane's results of row blocks 2p and 2p + 1 are 8
   // consecutive columns (one 16-byte store)
-  gemm_nt_mainloop<TX, TY, WX, NS, true, KC>(
-      [&](int r) { return Ab + (size_t)r * a.np; },
-      [&](int r) {
-        const int m = r & 15;
-        return Bb + (size_t)((r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * a.np;
-      },
-      a.np, sm, acc);
+  auto arow = [&](int r) { return Ab + (size_t)r * a.np; };
+  auto brow = [&](int r) {
+    const int m = r & 15;
+    return Bb + (size_t)((r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * a.np;
+  };
+  if constexpr (kPipe)
+    gemm_nt_mainloop_pipe64<TX, TY, WX, true>(arow, brow, a.np, sm, acc);
+  else
+    gemm_nt_mainloop<TX, TY, WX, NS, true, KC>(arow, brow, a.np, sm, acc);
   // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16); rows = columns
   // y0 + wy*TY/WY + 16 (j & ~1) + 8g + 4 (j & 1) + r
   static_assert(S::MY % 2 == 0 && (TY / S::WY) % 32 == 0, "row blocks pair up");
@@ -238,14 +241,17 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
 }
 
 // Np >= 1024: 256 x 256 tiles staged 64 k at a time (whole 128-byte lines of
-// each row; 128 KiB of LDS, one workgroup per CU); smaller Np: 256 x 128
-// tiles staged 32 k at a time (two workgroups per CU), which keeps more
-// workgroups per channel.  Both measured on MI355X.
+// each row; 128 KiB of LDS, one workgroup per CU), software-pipelined, each
+// wave a 64 x 128 block; smaller Np: 256 x 128 tiles staged 32 k at a time
+// (two workgroups per CU), which keeps more workgroups per channel.  Chosen
+// by measurement on MI355X (N = 1024: the pipelined loop 0.311 / 0.281 ms
+// outgoing / incoming against 0.317 / 0.290 ms for the plain one; deeper
+// 32-k staging, with or without a k-blocked operand layout, was slower).
 inline void launch_contract_big(const ContractArgs<bf16>& k, int np, int ch, hipStream_t st) {
   if (np >= 1024) {
     const int tiles = (np / 256) * (np / 256);
-    hipLaunchKernelGGL((trimul_contract_big_kernel<256, 256, 2, 2, 64>), dim3(tiles * ch), dim3(512),
-                       0, st, k);
+    hipLaunchKernelGGL((trimul_contract_big_kernel<256, 256, 4, 2, 64, true>), dim3(tiles * ch),
+                       dim3(512), 0, st, k);
   } else {
     const int tiles = (np / 256) * (np / 128);
     hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3, 32>), dim3(tiles * ch), dim3(512),
