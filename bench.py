@@ -181,7 +181,8 @@ def kernel_avg_ms(fn, kid, reps: int = 5):
 
 def probe_machine(dev):
     """Sustained MFMA rates (bf16 16x16x32, f32 16x16x4; 2 workgroups of 4
-    waves per CU, 8 independent chains per wave) and HBM copy bandwidth
+    waves per CU, 8 independent chains per wave), the attention core's
+    instruction mix as a ceiling (odde_probe_mix) and HBM copy bandwidth
     (2 GiB device copy, bytes read + written) on this GPU."""
     lib = _lib.load()
     sink = torch.zeros(256, device=dev)
@@ -199,6 +200,18 @@ def probe_machine(dev):
         out[f"mfma_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
     out["mfma_bf16_tflops_spec"] = PEAK_BF16_TFLOPS
     out["mfma_f32_tflops_spec"] = PEAK_F32_TFLOPS
+    # the attention core's per-key-block mix (40 MFMA, 64 exp, 32 bf16 packs)
+    # with no memory traffic: its ceiling in attention TF/s on this GPU, and
+    # the MFMA and exponential parts alone
+    for name, parts in (("mfma_only", 1), ("exp_only", 2), ("mix", 3)):
+        fl = ctypes.c_double(0.0)
+        call = lambda it: _lib.check(lib.odde_probe_mix(parts, it, 2 * cus,  # noqa: E731
+                                                        ctypes.c_void_p(sink.data_ptr()),
+                                                        ctypes.byref(fl), stream),
+                                     "odde_probe_mix")
+        call(50)
+        ms = kernel_avg_ms(lambda: call(2000), _lib.K_PROBE, reps=3)
+        out[f"core_mix_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
     src = torch.empty(1 << 29, device=dev)
     dst = torch.empty_like(src)
     ms = gpu_median_ms(lambda: dst.copy_(src), warm=2, iters=5)

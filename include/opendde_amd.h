@@ -408,6 +408,17 @@ int odde_timing_query(int kernel_id, double* total_ms, int64_t* launches);
 int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flops,
                     void* hip_stream);
 
+/* Co-issue probe (no counterpart in the reference): the triangle-attention
+ * core's per-key-block instruction mix at its tile -- 40 MFMA 16x16x32 bf16,
+ * 64 v_exp_f32, 32 v_cvt_pk_bf16_f32 per iteration, no memory traffic -- on
+ * `grid` workgroups of 4 waves.  parts: 1 = the MFMAs alone, 2 = the
+ * exponentials alone, 3 = the whole mix.  *flops: the attention flops the
+ * iterations stand for (QK^T and PV of 2 rows x 64 queries x 32 keys x head
+ * dim 32 per wave and iteration), so flops / time is the core's ceiling on
+ * this GPU.  Timed like odde_probe_mfma (kernel id ODDE_K_PROBE). */
+int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
+                   void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

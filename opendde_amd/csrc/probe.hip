@@ -39,6 +39,54 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(float* __restrict__ sin
   if (s == 1234.5f) sink[threadIdx.x] = s;  // practically never; keeps the chains live
 }
 
+// The attention core's per-key-block instruction mix at its tile (two rows x
+// 64 queries per wave, 32 keys per block, head dim 32): 40 MFMA 16x16x32
+// bf16 (QK^T 16, PV 16, row sums 8), 64 v_exp_f32 (2 x 64 x 32 scores / 64
+// lanes) and 32 v_cvt_pk_bf16_f32 (the bf16 P operand), with no memory
+// traffic.  kParts: 1 = the MFMAs alone, 2 = the exponentials alone (the
+// packs have no consumer there and are dropped), 3 = the whole mix.  The exponentials are 64
+// independent chains x <- exp2(-x) (bounded, fixed point ~0.64); the packed
+// results feed the next iteration's MFMA A operands, as P feeds PV.
+template <int kParts>
+__global__ __launch_bounds__(256) void mix_probe_kernel(float* __restrict__ sink, int64_t iters) {
+  constexpr bool kM = kParts & 1, kV = kParts & 2;
+  f32x4 acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float seed = 1e-3f * (float)(threadIdx.x & 63);
+  float e[64];
+#pragma unroll
+  for (int k = 0; k < 64; ++k) e[k] = seed + 0.01f * k;
+  bf16x8 p[8], b;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p[k][t] = (bf16)(seed + t);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) b[t] = (bf16)(seed - t);
+  for (int64_t it = 0; it < iters; ++it) {
+    if constexpr (kM) {
+#pragma unroll
+      for (int k = 0; k < 40; ++k)
+        acc[k & 7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p[k & 7], b, acc[k & 7], 0, 0, 0);
+    }
+    if constexpr (kV) {
+#pragma unroll
+      for (int k = 0; k < 64; ++k) e[k] = __builtin_amdgcn_exp2f(-e[k]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) p[k][t] = (bf16)e[8 * k + t];  // v_cvt_pk_bf16_f32 pairs
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s += acc[k][0] + (float)p[k][0];
+#pragma unroll
+  for (int k = 0; k < 64; ++k) s += e[k];
+  if (s == 1234.5f) sink[threadIdx.x] = s;  // practically never; keeps the work live
+}
+
 }  // namespace odde
 
 using namespace odde;
@@ -61,6 +109,24 @@ int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flo
   else
     hipLaunchKernelGGL(mfma_probe_kernel<false>, dim3(grid), dim3(256), 0, st, sink, iters);
   return check_launch("probe_mfma");
+}
+
+int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
+                   void* stream) {
+  if (!sink || !flops || iters <= 0 || grid <= 0)
+    return set_error(ODDE_EINVAL, "probe_mix: bad argument");
+  if (parts < 1 || parts > 3) return set_error(ODDE_EINVAL, "probe_mix: parts must be 1, 2 or 3");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LaunchScope ls(ODDE_K_PROBE, st);
+  // the attention flops one iteration stands for: QK^T and PV of 2 rows x 64
+  // queries x 32 keys x head dim 32 (2 * 2 * 2 * 64 * 32 * 32), per wave
+  *flops = 524288.0 * (double)iters * 4.0 * (double)grid;
+  switch (parts) {
+    case 1: hipLaunchKernelGGL(mix_probe_kernel<1>, dim3(grid), dim3(256), 0, st, sink, iters); break;
+    case 2: hipLaunchKernelGGL(mix_probe_kernel<2>, dim3(grid), dim3(256), 0, st, sink, iters); break;
+    default: hipLaunchKernelGGL(mix_probe_kernel<3>, dim3(grid), dim3(256), 0, st, sink, iters);
+  }
+  return check_launch("probe_mix");
 }
 
 }  // extern "C"
