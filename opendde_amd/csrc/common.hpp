@@ -163,6 +163,24 @@ __device__ __forceinline__ float sigmoidf_(float x) {
 }
 __device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
 
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes
+// land at lds + 16 l.  `base` / `bytes` describe a raw buffer (offsets at or
+// past `bytes` read as zero); voff is the lane's byte offset, soff a uniform
+// one.  Against global_load_lds this keeps one 32-bit offset per lane
+// instead of a 64-bit address.
+__device__ __forceinline__ void buffer_load_lds16(const void* base, uint32_t bytes, void* lds,
+                                                  uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voff, soff, 0, 0);
+#endif
+}
+__host__ __device__ __forceinline__ uint32_t clamp_bytes(uint64_t b) {
+  return b > 0xffffffffull ? 0xffffffffu : (uint32_t)b;
+}
+
 // Workgroup barrier without the memory fence __syncthreads() carries (that
 // fence waits for every outstanding global load, which would drain loads
 // issued ahead of time).  Callers first wait for what they need themselves

@@ -108,22 +108,28 @@ __device__ __forceinline__ void raw_tile_issue(const ZT* base, int64_t s1, int r
   constexpr int RPO = T::ROWS_PER_OP, OPS = T::OPS_PER_WAVE;
   constexpr int P = RPO >= 8 ? 1 : 8 / RPO;  // ops per period of the row swizzle
   static_assert(OPS % P == 0 && (OPS * RPO) % 8 == 0, "swizzle period");
-  const int w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  int l = lane_id();
+  // the lane offsets below are recomputed per call (a few VALU) rather than
+  // hoisted out of the caller's tile loop and kept in registers, which the
+  // weight-stationary kernels cannot spare
+  asm volatile("" : "+v"(l));
   const int rl = l / T::CHUNKS, cl = l % T::CHUNKS;
   const int first = w * OPS * RPO;  // a multiple of 8: r & 7 = (op * RPO + rl) & 7
   unsigned char* dst = raw + w * OPS * 1024;
   if (r0 + first + OPS * RPO <= n) {
-    const unsigned char* lrow =
-        reinterpret_cast<const unsigned char*>(base + (int64_t)(r0 + first + rl) * s1);
-    const int64_t step = (int64_t)RPO * s1 * (int64_t)sizeof(ZT);  // bytes per op
-    const unsigned char* lp[P];
+    // buffer loads based at the wave's first row: per lane one 32-bit offset
+    // per swizzle phase (row rl, chunk), per op a uniform row step; the
+    // wave's rows span less than 4 GiB
+    const ZT* wbase = base + (int64_t)(r0 + first) * s1;
+    const uint32_t rowb = (uint32_t)((int64_t)rl * s1 * (int64_t)sizeof(ZT));
+    const uint32_t step = (uint32_t)((int64_t)RPO * s1 * (int64_t)sizeof(ZT));  // bytes per op
+    uint32_t lo[P];
 #pragma unroll
-    for (int k = 0; k < P; ++k) lp[k] = lrow + (cl ^ ((k * RPO + rl) & 7)) * 16;
+    for (int k = 0; k < P; ++k) lo[k] = rowb + (cl ^ ((k * RPO + rl) & 7)) * 16;
 #pragma unroll
     for (int op = 0; op < OPS; ++op)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(lp[op % P] + op * step),
-          (__attribute__((address_space(3))) void*)(dst + op * 1024), 16, 0, 0);
+      buffer_load_lds16(wbase, 0xffffffffu, dst + op * 1024, lo[op % P], op * step);
   } else {
 #pragma unroll 1
     for (int op = 0; op < OPS; ++op) {  // one address live at a time

@@ -783,23 +783,6 @@ __device__ __forceinline__ void xcd_group_map(int L, int nx, int ngroups, int& x
   x = s % nx;
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes
-// land at lds + 16 l.  `base` / `bytes` describe a raw buffer (offsets at or
-// past `bytes` read as zero); voff is the lane's byte offset, soff a uniform
-// one.
-__device__ __forceinline__ void buffer_load_lds16(const void* base, uint32_t bytes, void* lds,
-                                                  uint32_t voff, uint32_t soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
-                                           voff, soff, 0, 0);
-#endif
-}
-__host__ __device__ __forceinline__ uint32_t clamp_bytes(uint64_t b) {
-  return b > 0xffffffffull ? 0xffffffffu : (uint32_t)b;
-}
-
 template <typename CT, int R, int QB, int RG, int QS>
 __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a, int nx,
                                                                         int ny) {
