@@ -56,7 +56,9 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>&
                                                    bool valid, const float* pb_ln_w,
                                                    const float* pb_ln_b, const CT* pb_w) {
   constexpr int C = kC * 32, NCB = C / 16;
-  const int l = lane_id(), g = l >> 4, r16 = l & 15;
+  int l = lane_id();
+  asm volatile("" : "+v"(l));  // lane addresses recomputed per call, not kept live by callers
+  const int g = l >> 4, r16 = l & 15;
   float zv[NCB][4];
   float s = 0.f;
 #pragma unroll
@@ -337,11 +339,19 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     return tile * kTpRows + (kRB * w + rb) * 16 + r16;
   };
   RowSlots<ZT> xr[kRB];  // the rows of the tile about to start
+  // per-lane row addresses are recomputed at each use (an opaque lane id)
+  // rather than hoisted out of the tile loop, where they would be spilled
+  auto lane_g = [&]() {
+    int ll = lane_id();
+    asm volatile("" : "+v"(ll));
+    return ll >> 4;
+  };
   auto load_rows = [&](int64_t tile) {
+    const int gg = lane_g();
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = min(row_of(tile, rb), a.rows - 1);  // pad rows read a real row
-      xr[rb].load(a.x + row * C, g);
+      xr[rb].load(a.x + row * C, gg);
     }
   };
   load_rows(blockIdx.x);
@@ -477,6 +487,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     const int64_t next = tile + gridDim.x;
     // residual rows one row block at a time; the first block's loads and the
     // wait below also cover this wave's chunk loads for the next tile
+    const int gb = lane_g();
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
@@ -485,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       if (a.add) {
         const int64_t rr = min(row, a.rows - 1);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * g);
+        for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
       }
       if (rb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[cb].get(e);
         if (valid)
-          store4(a.out + row * C + cb * 16 + 4 * g, acc[rb][cb][0], acc[rb][cb][1],
+          store4(a.out + row * C + cb * 16 + 4 * gb, acc[rb][cb][0], acc[rb][cb][1],
                  acc[rb][cb][2], acc[rb][cb][3]);
       }
     }
