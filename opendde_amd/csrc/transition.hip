@@ -235,7 +235,9 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 // workgroup overlap the other workgroup's MFMA work.
 // LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
 // bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
-// (4 slots; slot t of row r holds chunk t ^ ((r >> 1) & 3)).
+// (4 slots; slot t of row r holds chunk t ^ ((r >> 2) & 3): the 16 rows of a
+// fragment read then cover 16 distinct (row position, slot) pairs of a
+// 256-byte bank period, free of bank conflicts).
 constexpr int kRB = 3;                   // 16-row blocks per wave
 constexpr int kTpRows = 64 * kRB;
 constexpr int kTpStages = 3;
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   // holds channels 16 bi + (l >> 2).
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int lane_ab = (l >> 4) * C + ((l & 15) ^ (4 * w + (l >> 4))) * 8;
-  const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((l >> 3) & 3)) * 8;
+  const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((l >> 4) & 3)) * 8;
   auto issue = [&](int q) {
     const int h0 = (q % NCHUNK) * kTrHid;
     bf16* base = ws[q % kTpStages];
@@ -358,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const int sa_off = r16 * C;                  // + hb*16*C + slot*8
-  const int so_sw = (r16 >> 1) & 3;
+  const int so_sw = (r16 >> 2) & 3;
   const float* ln_w = lnp;
   const float* ln_b = lnp + C;
   int q = 0;
