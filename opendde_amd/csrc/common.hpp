@@ -23,6 +23,9 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -31,9 +34,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 // ----------------------------------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
 // x rounded to T's precision and widened back
 template <typename T> __device__ __forceinline__ float round_to(float x) { return (float)from_f32<T>(x); }
 
@@ -68,9 +73,22 @@ template <> struct Frag<float> {
   __device__ __forceinline__ float get(int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
 };
 
+template <> struct Frag<f16> {
+  f16x8 v;
+  __device__ __forceinline__ void zero() {
+    for (int e = 0; e < 8; ++e) v[e] = (f16)0.0f;
+  }
+  __device__ __forceinline__ void load(const f16* p) { v = *reinterpret_cast<const f16x8*>(p); }
+  __device__ __forceinline__ void set(int e, float x) { v[e] = (f16)x; }
+  __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
+};
+
 // acc += A * B over one 32-deep slot set.
 __device__ __forceinline__ void mma(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<f16>& a, const Frag<f16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, b.v, acc, 0, 0, 0);
 }
 __device__ __forceinline__ void mma(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[0], b.lo[0], acc, 0, 0, 0);
@@ -93,6 +111,11 @@ __device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float
   bf16x4 v;
   v[0] = (bf16)a; v[1] = (bf16)b; v[2] = (bf16)c; v[3] = (bf16)d;
   *reinterpret_cast<bf16x4*>(p) = v;
+}
+__device__ __forceinline__ void store4(f16* p, float a, float b, float c, float d) {
+  f16x4 v;
+  v[0] = (f16)a; v[1] = (f16)b; v[2] = (f16)c; v[3] = (f16)d;
+  *reinterpret_cast<f16x4*>(p) = v;
 }
 __device__ __forceinline__ void load4(const float* p, float* o) {
   f32x4 v = *reinterpret_cast<const f32x4*>(p);
@@ -258,6 +281,15 @@ __device__ __forceinline__ void load_w_frag(const CT* __restrict__ w, int ld, in
   const int g = lane_id() >> 4;
   if (o < n_out) f.load(w + (size_t)o * ld + 32 * t + 8 * g);
   else f.zero();
+}
+// bf16 weights as fp16 fragments (exact: fp16 holds every bf16 value of the
+// weights' range, |w| >= 2^-14, to more mantissa bits than bf16 has)
+__device__ __forceinline__ void load_w_frag(const bf16* __restrict__ w, int ld, int o0, int n_out,
+                                            int t, Frag<f16>& f) {
+  Frag<bf16> b;
+  load_w_frag(w, ld, o0, n_out, t, b);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f.v[e] = (f16)(float)b.v[e];
 }
 
 }  // namespace odde

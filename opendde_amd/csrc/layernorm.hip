@@ -34,12 +34,7 @@
 
 namespace odde {
 
-typedef _Float16 f16;
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
-template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
 
 namespace {
 

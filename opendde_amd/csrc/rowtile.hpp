@@ -234,9 +234,9 @@ __device__ __forceinline__ void tile_frags(const CT* lds, int rb, Frag<CT> (&f)[
 
 // Weight fragments kept in registers: NB column blocks of 16 output rows of
 // W[out][K] starting at output o0 (rows >= n_out are zero).
-template <typename CT, int NB, int KS>
-__device__ __forceinline__ void load_w_slice(const CT* __restrict__ w, int ld, int o0, int n_out,
-                                             Frag<CT> (&f)[NB][KS]) {
+template <typename WT, typename FT, int NB, int KS>
+__device__ __forceinline__ void load_w_slice(const WT* __restrict__ w, int ld, int o0, int n_out,
+                                             Frag<FT> (&f)[NB][KS]) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll

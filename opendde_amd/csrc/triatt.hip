@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
   // wave 3 only helps stage the tile: the gate is computed in the output kernel
   const CT* W = w == 0 ? a.wq : w == 1 ? a.wk : a.wv;
   Frag<CT> wf[NB][kC];
-  load_w_slice<CT, NB, kC>(W, C, 0, HD, wf);
+  load_w_slice(W, C, 0, HD, wf);
   Frag<CT> wbf[kC];
 #pragma unroll
   for (int t = 0; t < kC; ++t) {
@@ -1267,9 +1267,9 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
     lnp[C + t] = a.ln_b[t];
   }
   Frag<CT> wof[NBO][kHD];
-  load_w_slice<CT, NBO, kHD>(a.wo, HD, w * (C / 4), C, wof);
+  load_w_slice(a.wo, HD, w * (C / 4), C, wof);
   Frag<CT> wgf[NBG][kC];
-  load_w_slice<CT, NBG, kC>(a.wg, C, w * (HD / 4), HD, wgf);
+  load_w_slice(a.wg, C, w * (HD / 4), HD, wgf);
   const int jp = a.jp, n = a.n, tiles_per_row = jp / kTileRows;
 
   // The next tile's z rows (into LDS) and o rows (into registers) are loaded

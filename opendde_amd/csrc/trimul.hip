@@ -389,10 +389,11 @@ template <typename ZT, typename CT, int kC, int kCH>
 __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<ZT, CT> a,
                                                                 int ntiles) {
   constexpr int C = kC * 32, CH = kCH * 32, NB = kCH;  // NB blocks of 16 = Ch/2 channels
-  // bf16: the value projections also take the rounding remainder of LN(z)
-  constexpr bool kSplit = sizeof(CT) == 2;
-  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
-  __shared__ __attribute__((aligned(16))) CT xs_lo[kSplit ? kTileRows * TileLD<CT, C>::value : 8];
+  // bf16 arithmetic multiplies in fp16 here: LN(z) rounded to fp16 (11
+  // mantissa bits against bf16's 8, well inside fp16's range) times the bf16
+  // weights, which fp16 holds exactly; same MFMA rate, fp32 accumulation
+  using XT = typename std::conditional<sizeof(CT) == 2, f16, CT>::type;
+  __shared__ __attribute__((aligned(16))) XT xs[kTileRows * TileLD<XT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ float mk_s[kTileRows];
   __shared__ float lnp[2 * C];  // LayerNorm weight, bias
@@ -403,9 +404,9 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   }
   const int which = w >> 1, half = w & 1;
   const int o0 = which * CH + half * (CH / 2);
-  Frag<CT> wpf[NB][kC], wgf[NB][kC];
-  load_w_slice<CT, NB, kC>(a.wp, C, o0, 2 * CH, wpf);
-  load_w_slice<CT, NB, kC>(a.wg, C, o0, 2 * CH, wgf);
+  Frag<XT> wpf[NB][kC], wgf[NB][kC];
+  load_w_slice(a.wp, C, o0, 2 * CH, wpf);
+  load_w_slice(a.wg, C, o0, 2 * CH, wgf);
   CT* dst = which ? a.B : a.A;
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   // the next tile's z rows stream into LDS while a tile is computed; rows
@@ -438,8 +439,8 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
     const int x = tile / tiles_per_row;
     const int y0 = (tile % tiles_per_row) * kTileRows;
     const float mcur = mnext;
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, lnp, lnp + C,
-                           a.eps, xs, kSplit ? xs_lo : nullptr);
+    raw_tile_ln<ZT, XT, C>(raw, [&](int r) { return x < n && y0 + r < n; }, lnp, lnp + C,
+                           a.eps, xs);
     if (w == 0) mk_s[l] = mcur;
     lds_barrier();  // xs and mk_s ready; raw consumed
     if (tile + (int)gridDim.x < ntiles) {
@@ -453,15 +454,12 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
       const int rbase = 32 * (rb >> 1) + 4 * (rb & 1);
-      Frag<CT> xf[kC], xl[kSplit ? kC : 1];
+      Frag<XT> xf[kC];
       {
-        constexpr int LD = TileLD<CT, C>::value;
+        constexpr int LD = TileLD<XT, C>::value;
         const int off = (rbase + 8 * (r16 >> 2) + (r16 & 3)) * LD + 8 * g;
 #pragma unroll
-        for (int t = 0; t < kC; ++t) {
-          xf[t].load(xs + off + 32 * t);
-          if constexpr (kSplit) xl[t].load(xs_lo + off + 32 * t);
-        }
+        for (int t = 0; t < kC; ++t) xf[t].load(xs + off + 32 * t);
       }
       float mk[4];
 #pragma unroll
@@ -471,7 +469,6 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
         f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap;
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-          if constexpr (kSplit) mma(ap, xl[t], wpf[cb][t]);
           mma(ap, xf[t], wpf[cb][t]);
           mma(ag, xf[t], wgf[cb][t]);
         }
@@ -523,8 +520,8 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
     lnp[3 * C + t] = a.wz_bias[t];
   }
   Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
-  load_w_slice<CT, NBO, kCH>(a.wz, CH, w * (C / 4), C, wzf);
-  load_w_slice<CT, NBO, kC>(a.wg, C, w * (C / 4), C, wgf);
+  load_w_slice(a.wz, CH, w * (C / 4), C, wzf);
+  load_w_slice(a.wg, C, w * (C / 4), C, wgf);
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   auto issue = [&](int tl) {  // the next tile's z rows (for LN_in), as in the projection
     const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;

@@ -435,14 +435,15 @@ def test_pairformer_block_bf16_autocast():
 # ------------------------------------------------- bf16 accuracy of tri-mul
 @pytest.mark.parametrize("outgoing", [True, False])
 def test_triangle_multiplication_bf16_rounding_budget(outgoing):
-    """The bf16 multiplication keeps the rounding remainder of LN_in(z) for
-    the value projections (hi + lo bf16) and folds LN_out into W_z, so p
-    enters the output projection as stored.  Without those the relative error
-    of the update against the fp32 oracle is about 5.0e-3 at this size (one
-    bf16 rounding each of x, the weights, a and b, p and LN_out(p)); with
-    them about 4.1e-3.  Over the 48-block trunk that margin is what keeps the
-    accumulated update within max-abs 5e-2.  Also: without the f32 copy of
-    linear_z the fold rounds the weight twice and stays within the tier."""
+    """The bf16 multiplication's input projections multiply LN_in(z) rounded
+    to fp16 (11 mantissa bits) by the bf16 weights (exact in fp16), and
+    LN_out is folded into W_z, so p enters the output projection as stored.
+    With LN_in(z) rounded to bf16 and LN_out(p) rounded again, the relative
+    error of the update against the fp32 oracle is about 5.0e-3 at this size;
+    with them about 4.1e-3.  Over the 48-block trunk that margin is what
+    keeps the accumulated update within max-abs 5e-2.  Also: without the f32
+    copy of linear_z the fold rounds the weight twice and stays within the
+    tier."""
     n = 192
     cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
     mod = seeded(cls(128, 128), 900 + outgoing, 0.02)  # the workload's weight scale
