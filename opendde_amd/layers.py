@@ -17,6 +17,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .kernels import prepared
+
 # LayerNorm selection, read once at import as the reference does
 # (layers.py:24-29).
 _use_fast_layer_norm = os.getenv("LAYERNORM_TYPE", "torch") == "fast_layernorm"
@@ -152,7 +154,21 @@ class Linear(nn.Linear):
             with torch.amp.autocast("cuda", enabled=False):
                 b = self.bias.to(self.precision) if self.bias is not None else None
                 return F.linear(x.to(self.precision), self.weight.to(self.precision), b).to(d)
+        if x.is_cuda and _bf16_autocast(x):
+            # what bf16 autocast does for F.linear (input, weight and bias in
+            # bf16, bf16 result), with the weight and bias cast once per
+            # version instead of on every call
+            bf = torch.bfloat16
+            with torch.amp.autocast("cuda", enabled=False):
+                b = prepared(self.bias, bf) if self.bias is not None else None
+                return F.linear(x.to(bf), prepared(self.weight, bf), b)
         return F.linear(x, self.weight, self.bias)
 
 
 LinearNoBias = partial(Linear, bias=False)
+
+
+def _bf16_autocast(x: torch.Tensor) -> bool:
+    """CUDA autocast to bf16 is on and would cast this floating input."""
+    return (x.dtype in (torch.float32, torch.bfloat16) and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.bfloat16)

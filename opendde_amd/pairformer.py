@@ -25,7 +25,7 @@ import torch.nn.functional as F
 
 from . import hook
 from . import kernels as K
-from .layers import LayerNorm, Linear, LinearNoBias
+from .layers import LayerNorm, Linear, LinearNoBias, _bf16_autocast
 from .triangular import (TriangleAttention, TriangleMultiplicationIncoming,
                          TriangleMultiplicationOutgoing)
 
@@ -126,6 +126,11 @@ class SingleAttention(nn.Module):
         sequence [N, c], GPU tensors, supported head dim)."""
         def heads(t):
             return t.view(t.shape[:-1] + (self.num_heads, -1)).transpose(-2, -3)
+        if q_x.is_cuda and _bf16_autocast(q_x):
+            # the bf16 cast autocast gives each of the four projections, once
+            same = kv_x is q_x
+            q_x = q_x.to(torch.bfloat16)
+            kv_x = q_x if same else kv_x
         q = heads(self.linear_q(q_x)) / math.sqrt(self.c_hidden)
         k = heads(self.linear_k(kv_x))
         v = heads(self.linear_v(kv_x))
