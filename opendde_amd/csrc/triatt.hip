@@ -852,7 +852,9 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
 #pragma unroll
     for (int j = 0; j < KPW; ++j) {
       const int i = wu + j * NW;
-      if (i < NKI) {
+      // (always true when the instructions divide evenly over the waves:
+      // then no branch is emitted)
+      if (NKI % NW == 0 || i < NKI) {
         buffer_load_lds16(kbase, kv_bytes, S.k + i * 64, ok[j], skv);
         buffer_load_lds16(vbase, kv_bytes, S.v + i * 64, ov[j], skv);
       }
@@ -860,7 +862,8 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int i = wu + j * NW;
-      if (i < NBI) buffer_load_lds16(B, b_bytes, S.b + i * 64, ob[j], (uint32_t)t * 32 * sizeof(float));
+      if (NBI % NW == 0 || i < NBI)
+        buffer_load_lds16(B, b_bytes, S.b + i * 64, ob[j], (uint32_t)t * 32 * sizeof(float));
     }
     if (wu == NW - 1 && l < Stage::KP_CHUNKS)
       buffer_load_lds16(kpbase, kp_bytes, S.kp, okp, (uint32_t)t * 32 * sizeof(CT));
@@ -893,6 +896,9 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
     if (l < R && row0 + l < a.rows) a.rowflag[row0 + l] = 1;
     skip = true;
   }
+  // the same for every lane of the wave (its rows and their flags): made
+  // provably uniform so that `if (!skip)` is a scalar branch, not an exec mask
+  skip = __builtin_amdgcn_readfirstlane((int)skip) != 0;
 
   f32x4 o[R][2][QB];
   float lsum[R][QB];
