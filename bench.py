@@ -66,7 +66,9 @@ def flops(n, c_z=128, c_s=384, h=4, d=32, ch=128, n_heads=16):
     single = (2.0 * n * n * c_z * n_heads + 8.0 * n * c_s * c_s + 4.0 * n * n * c_s
               + 2.0 * n * c_s * c_s + 2.0 * n * (2 * c_s * 4 * c_s + 4 * c_s * c_s))
     block = 2 * (core + att_lin) + 2 * (contract + mul_lin) + trans + (single if c_s else 0)
-    return dict(core=core, att_lin=att_lin, contract=contract, mul_lin=mul_lin, block=block)
+    single_trans = 2.0 * n * (2 * c_s * 4 * c_s + 4 * c_s * c_s)
+    return dict(core=core, att_lin=att_lin, contract=contract, mul_lin=mul_lin, trans=trans,
+                single_trans=single_trans, block=block)
 
 
 def kernel_bytes(n, c_z=128, h=4, ch=128, z_bytes=4, ct_bytes=2):
@@ -589,11 +591,20 @@ def main():
         elif name == "trimul_contract":
             t = f["contract"] / (avg * 1e-3) / 1e12
             ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
+        elif name == "transition":
+            # the pair transition and, with a single track, the single one:
+            # their flops over their launches
+            per_block = cnt / args.blocks
+            fl = f["trans"] + (f["single_trans"] if per_block > 1 else 0.0)
+            t = fl / per_block / (avg * 1e-3) / 1e12
+            ent.update(tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2))
         elif name in kb:
             gbs = kb[name] / (avg * 1e-3) / 1e9
             ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_HBM_GBS, 2))
         kernels[name] = ent
-    dom = max(kernels, key=lambda k: kernels[k]["total_ms_per_step"])
+    # the dominant kernel among those with a rate (flops or compulsory bytes)
+    rated = [k for k in kernels if "tflops" in kernels[k] or "gbs" in kernels[k]]
+    dom = max(rated, key=lambda k: kernels[k]["total_ms_per_step"])
     d = kernels[dom]
     traffic = None if v1 else load_traffic(n).get(dom)
     if "tflops" in d:
