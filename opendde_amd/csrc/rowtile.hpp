@@ -11,6 +11,8 @@
 
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace odde {
 
 constexpr int kTileRows = 64;
@@ -94,14 +96,15 @@ struct RawTile {
 // Issue the tile's loads.  Tile row r is row min(r0 + r, n - 1) of a view
 // whose row 0 starts at `base` with rows `s1` elements apart (rows past the
 // end re-read the last real row; raw_tile_ln masks them).  Completion is
-// awaited by raw_tile_wait().
+// awaited by raw_tile_wait().  kPolicy is the loads' cache policy (kStream for
+// a tile the kernel reads once).
 //
 // Wave w loads tile rows [w R, (w + 1) R), R = kTileRows / 4, one op of
 // ROWS_PER_OP rows at a time.  Where all of them exist the addresses are
 // affine in the op: the lane's row pointer is formed once and each op adds a
 // uniform step; the row swizzle (r & 7) repeats every 8 / ROWS_PER_OP ops,
 // so that many lane pointers (chunk offset folded in) cover every op.
-template <typename ZT, int C>
+template <typename ZT, int C, int kPolicy = 0>
 __device__ __forceinline__ void raw_tile_issue(const ZT* base, int64_t s1, int r0, int n,
                                                unsigned char* raw) {
   using T = RawTile<ZT, C>;
@@ -129,7 +132,7 @@ __device__ __forceinline__ void raw_tile_issue(const ZT* base, int64_t s1, int r
     for (int k = 0; k < P; ++k) lo[k] = rowb + (cl ^ ((k * RPO + rl) & 7)) * 16;
 #pragma unroll
     for (int op = 0; op < OPS; ++op)
-      buffer_load_lds16(wbase, 0xffffffffu, dst + op * 1024, lo[op % P], op * step);
+      buffer_load_lds16<kPolicy>(wbase, 0xffffffffu, dst + op * 1024, lo[op % P], op * step);
   } else {
 #pragma unroll 1
     for (int op = 0; op < OPS; ++op) {  // one address live at a time
@@ -140,7 +143,7 @@ __device__ __forceinline__ void raw_tile_issue(const ZT* base, int64_t s1, int r
           chunk * 16;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)src,
-          (__attribute__((address_space(3))) void*)(dst + op * 1024), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(dst + op * 1024), 16, 0, kPolicy);
     }
   }
 }
@@ -241,6 +244,35 @@ __device__ __forceinline__ void load_w_slice(const WT* __restrict__ w, int ld, i
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int t = 0; t < KS; ++t) load_w_frag(w, ld, o0 + 16 * b, n_out, t, f[b][t]);
+}
+
+// Output rows of a row-tile kernel: lane (g, r16) holds, for its row, NB
+// blocks of 4 consecutive outputs r[cb] (float[4] or f32x4) at channels
+// c_base + 16 cb + 4 g.
+// With fp32 rows and NB even, blocks 2L and 2L + 1 are slots g and 4 + g of
+// one 128-byte line, stored with the streaming policy as whole lines together
+// with the row of lane r16 ^ 1 (store_line_pair; `partner_row`, and ok /
+// partner_ok, say which rows exist).  Otherwise the blocks are stored one by
+// one.  Every lane of the wave must be active.
+template <typename ZT, int NB, typename Block>
+__device__ __forceinline__ void store_row_blocks(ZT* row, ZT* partner_row, int c_base,
+                                                 const Block (&r)[NB], bool ok, bool partner_ok) {
+  const int g = lane_id() >> 4;
+  if constexpr (std::is_same<ZT, float>::value && NB % 2 == 0) {
+#pragma unroll
+    for (int L = 0; L < NB / 2; ++L) {
+      const f32x4 lo = {r[2 * L][0], r[2 * L][1], r[2 * L][2], r[2 * L][3]};
+      const f32x4 hi = {r[2 * L + 1][0], r[2 * L + 1][1], r[2 * L + 1][2], r[2 * L + 1][3]};
+      store_line_pair(reinterpret_cast<f32x4*>(row + c_base + 32 * L),
+                      reinterpret_cast<f32x4*>(partner_row + c_base + 32 * L), g, lo, hi, ok,
+                      partner_ok);
+    }
+  } else {
+    if (!ok) return;
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb)
+      store4(row + c_base + 16 * cb + 4 * g, r[cb][0], r[cb][1], r[cb][2], r[cb][3]);
+  }
 }
 
 }  // namespace odde

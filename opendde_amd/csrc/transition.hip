@@ -501,15 +501,13 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
         for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
       }
       if (rb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (a.add)
 #pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        if (a.add)
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[cb].get(e);
-        if (valid)
-          store4(a.out + row * C + cb * 16 + 4 * gb, acc[rb][cb][0], acc[rb][cb][1],
-                 acc[rb][cb][2], acc[rb][cb][3]);
-      }
+      store_row_blocks<ZT>(a.out + row * C, a.out + (row ^ 1) * C, 0, acc[rb], valid,
+                           (row ^ 1) < a.rows);
     }
     if (a.pb_out)
 #pragma unroll

@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws_kernel(TriattProjArgs<Z
   // rows past n read row n-1 (always present) and are masked in the LN pass
   auto issue = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
+    raw_tile_issue<ZT, C, kStream>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
   };
   // the next tile's mask value (wave 0, lane = key) and row flag are loaded
   // with its z rows, so no global load latency sits inside a tile
@@ -503,8 +503,8 @@ __device__ __forceinline__ void proj_ws4_role(const TriattProjArgs<ZT, CT>& a, c
           v8[e] = out[rb][ob][e];
           v8[4 + e] = out[rb + 1][ob][e];
         }
-        *reinterpret_cast<bf16x8*>(a.v + vperm_offset(i, o >> 5, H, jp, j0 + rb * 16 + 4 * g,
-                                                      o & 31)) = v8;
+        store_stream(reinterpret_cast<bf16x8*>(a.v + vperm_offset(i, o >> 5, H, jp, j0 + rb * 16 + 4 * g,
+                                                                  o & 31)), v8);
       } else {
         if (ch & 16) continue;  // stored with the head's first block
 #pragma unroll
@@ -512,14 +512,14 @@ __device__ __forceinline__ void proj_ws4_role(const TriattProjArgs<ZT, CT>& a, c
           v8[e] = out[rb][ob][e];
           v8[4 + e] = out[rb][ob + 1][e];
         }
-        *reinterpret_cast<bf16x8*>((mat ? a.k : a.q) +
-                                   (((size_t)i * H + (ch >> 5)) * jp + j0 + rb * 16 + r16) * 32 +
-                                   8 * g) = v8;
+        store_stream(reinterpret_cast<bf16x8*>((mat ? a.k : a.q) +
+                                               (((size_t)i * H + (ch >> 5)) * jp + j0 + rb * 16 + r16) * 32 +
+                                               8 * g), v8);
       }
     }
     if (W == 0 && r16 < H)
-      *reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g) =
-          bo[rb];
+      store_stream(reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g),
+                   bo[rb]);
   }
   if (W == 1 || W == 2) {
 #pragma unroll
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256, 2) void triatt_proj_ws4_kernel(TriattProjArgs<
   const int tiles_per_row = jp / kTileRows;
   auto issue = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
+    raw_tile_issue<ZT, C, kStream>(a.z + (int64_t)ti * a.z_s0, a.z_s1, tj0, n, raw);
   };
   // the next tile's mask value (wave 0, lane = key) and row flag are loaded
   // with its z rows
@@ -719,7 +719,7 @@ __device__ __forceinline__ void core_store(const TriattCoreArgs<CT>& a, int row0
           bf16x8 v8;
 #pragma unroll
           for (int e = 0; e < 8; ++e) v8[e] = (bf16)ov[e];
-          *reinterpret_cast<bf16x8*>(dst) = v8;
+          store_stream(reinterpret_cast<bf16x8*>(dst), v8);
           continue;
         }
       }
@@ -1284,12 +1284,12 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
   f32x4 opre[OCH];
   auto fetch = [&](int tl) {
     const int ti = tl / tiles_per_row, tj0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(a.res + (int64_t)ti * a.r_s0, a.r_s1, tj0, n, raw);
+    raw_tile_issue<ZT, C, kStream>(a.res + (int64_t)ti * a.r_s0, a.r_s1, tj0, n, raw);
     const CT* src = a.o + ((size_t)ti * jp + tj0) * HD;
 #pragma unroll
     for (int k = 0; k < OCH; ++k) {
       const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
-      opre[k] = *reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc);
+      opre[k] = load_stream(reinterpret_cast<const f32x4*>(src + (size_t)r * HD + cc));
     }
   };
   if ((int)blockIdx.x < ntiles) fetch(blockIdx.x);
@@ -1343,16 +1343,18 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
       Frag<CT> xf[kHD];
       tile_frags<CT, HD>(xo, rb, xf);
       const int jr = j0 + rb * 16 + r16;
+      float r[NBO][4];
 #pragma unroll
       for (int cb = 0; cb < NBO; ++cb) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < kHD; ++t) mma(acc, wof[cb][t], xf[t]);
-        if (jr >= n) continue;
-        const int c0 = w * (C / 4) + cb * 16 + 4 * g;
-        store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jr * a.o_s1 + c0, res[rb][cb][0] + acc[0],
-               res[rb][cb][1] + acc[1], res[rb][cb][2] + acc[2], res[rb][cb][3] + acc[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[cb][e] = res[rb][cb][e] + acc[e];
       }
+      ZT* orow = a.out + (int64_t)i * a.o_s0;
+      store_row_blocks<ZT>(orow + (int64_t)jr * a.o_s1, orow + (int64_t)(jr ^ 1) * a.o_s1,
+                                w * (C / 4), r, jr < n, (jr ^ 1) < n);
     }
     // xs and xo are rewritten only after the barrier in raw_tile_wait()
   }

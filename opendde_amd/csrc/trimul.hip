@@ -477,20 +477,25 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next raw tile (own part) landed
+    // a lane holds rows y0 + 8 g .. + 7 (row blocks 0, 1) and y0 + 32 + 8 g ..
+    // + 7 (row blocks 2, 3) of channel c: slots g and 4 + g of the channel's
+    // 128-byte line of this tile; lanes r16 and r16 ^ 1 (channels c, c ^ 1)
+    // complete each other's lines
+    static_assert(kTileRows == 64, "one 128-byte line of bf16 per channel and tile");
 #pragma unroll
-    for (int p = 0; p < kTileRows / 32; ++p) {
-      const int yb = y0 + 32 * p + 8 * g;
+    for (int cb = 0; cb < NB; ++cb) {
+      const int c = half * (CH / 2) + cb * 16 + r16;
+      bf16x8 lo, hi;
 #pragma unroll
-      for (int cb = 0; cb < NB; ++cb) {
-        const int c = half * (CH / 2) + cb * 16 + r16;
-        bf16x8 v8;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v8[e] = ov[2 * p][cb][e];
-          v8[4 + e] = ov[2 * p + 1][cb][e];
-        }
-        *reinterpret_cast<bf16x8*>(dst + ((size_t)c * np + x) * np + yb) = v8;
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = ov[0][cb][e];
+        lo[4 + e] = ov[1][cb][e];
+        hi[e] = ov[2][cb][e];
+        hi[4 + e] = ov[3][cb][e];
       }
+      store_line_pair(reinterpret_cast<bf16x8*>(dst + ((size_t)c * np + x) * np + y0),
+                      reinterpret_cast<bf16x8*>(dst + ((size_t)(c ^ 1) * np + x) * np + y0), g, lo,
+                      hi);
     }
     lds_barrier();  // every wave's part of the next raw tile landed; xs, mk_s free
   }
@@ -525,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   auto issue = [&](int tl) {  // the next tile's z rows (for LN_in), as in the projection
     const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
+    raw_tile_issue<ZT, C, kStream>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
   };
   // P[:, x, y0:y0+64] of the next tile is loaded into registers while the
   // current tile is computed, then written transposed to xp[y][c]: thread t
@@ -540,7 +545,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
     const CT* src = a.P + (size_t)tx * np + ty0 + 8 * pyb;
 #pragma unroll
     for (int k = 0; k < PCH; ++k)
-      ppre[k] = *reinterpret_cast<const f32x4*>(src + (size_t)(PCH * pcg + k) * np * np);
+      ppre[k] = load_stream(reinterpret_cast<const f32x4*>(src + (size_t)(PCH * pcg + k) * np * np));
   };
   if ((int)blockIdx.x < ntiles) {
     issue(blockIdx.x);
@@ -623,6 +628,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       tile_frags<CT, C>(xz, rb, zf);
       const int yr = y0 + rb * 16 + r16;
       const float pmean = pst[rb * 16 + r16], prstd = pst[kTileRows + rb * 16 + r16];
+      float r[NBO][4];
 #pragma unroll
       for (int cb = 0; cb < NBO; ++cb) {
         f32x4 ay = {0.f, 0.f, 0.f, 0.f}, ag = ay;
@@ -630,19 +636,19 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
         for (int t = 0; t < kCH; ++t) mma(ay, wzf[cb][t], pf[t]);
 #pragma unroll
         for (int t = 0; t < kC; ++t) mma(ag, wgf[cb][t], zf[t]);
-        if (yr >= n) continue;
         const int c0 = w * (C / 4) + cb * 16 + 4 * g;
         float sw[4], cw[4];
         load4(lnp + 2 * C + c0, sw);
         load4(lnp + 3 * C + c0, cw);
-        float r[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float y = prstd * (ay[e] - pmean * sw[e]) + cw[e];
-          r[e] = res[rb][cb][e] + y * sigmoidf_(ag[e]);
+          r[cb][e] = res[rb][cb][e] + y * sigmoidf_(ag[e]);
         }
-        store4(a.out + (int64_t)x * a.o_s0 + (int64_t)yr * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
       }
+      ZT* orow = a.out + (int64_t)x * a.o_s0;
+      store_row_blocks<ZT>(orow + (int64_t)yr * a.o_s1, orow + (int64_t)(yr ^ 1) * a.o_s1,
+                                w * (C / 4), r, yr < n, (yr ^ 1) < n);
     }
     lds_barrier();  // xp and xz are rewritten for the next tile
   }
