@@ -277,7 +277,10 @@ struct RowSlots {
 template <typename ZT> struct Quad;
 template <> struct Quad<float> {
   f32x4 v;
-  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const f32x4*>(p); }
+  // the residual re-read of a row the kernel read once already: streamed
+  __device__ __forceinline__ void load(const float* p) {
+    v = load_stream(reinterpret_cast<const f32x4*>(p));
+  }
   __device__ __forceinline__ float get(int e) const { return v[e]; }
 };
 template <> struct Quad<bf16> {

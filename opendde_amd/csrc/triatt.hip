@@ -518,8 +518,8 @@ __device__ __forceinline__ void proj_ws4_role(const TriattProjArgs<ZT, CT>& a, c
       }
     }
     if (W == 0 && r16 < H)
-      store_stream(reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g),
-                   bo[rb]);
+      *reinterpret_cast<f32x4*>(a.bias + ((size_t)r16 * jp + i) * jp + j0 + rb * 16 + 4 * g) =
+          bo[rb];  // half lines: the default policy (the core re-reads the bias through L2)
   }
   if (W == 1 || W == 2) {
 #pragma unroll

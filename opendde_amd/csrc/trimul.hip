@@ -220,23 +220,30 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
     gemm_nt_mainloop<TX, TY, WX, NS, true, KC>(arow, brow, a.np, sm, acc);
   // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16); rows = columns
   // y0 + wy*TY/WY + 16 (j & ~1) + 8g + 4 (j & 1) + r
-  static_assert(S::MY % 2 == 0 && (TY / S::WY) % 32 == 0, "row blocks pair up");
+  // Row blocks j, j + 1 give a lane 8 consecutive columns (slot g of a 64-
+  // column, 128-byte line of its row), row blocks j + 2, j + 3 slot 4 + g of
+  // the same line; lanes r16 and r16 ^ 1 (rows xx, xx ^ 1) complete each
+  // other's lines, stored whole with the streaming policy (store_line_pair).
+  static_assert(S::MY % 4 == 0 && (TY / S::WY) % 64 == 0, "row blocks form whole lines");
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % WX, wy = w / WX;
   bf16* Pb = a.P + c * plane;
 #pragma unroll
   for (int i = 0; i < S::MX; ++i)
 #pragma unroll
-    for (int j = 0; j < S::MY; j += 2) {
+    for (int j = 0; j < S::MY; j += 4) {
       const int xx = x0 + wx * (TX / WX) + i * 16 + r16;
-      const int yy = y0 + wy * (TY / S::WY) + j * 16 + 8 * g;
-      bf16x8 v8;
+      const int y = y0 + wy * (TY / S::WY) + j * 16;
+      bf16x8 lo, hi;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v8[e] = (bf16)acc[i][j][e];
-        v8[4 + e] = (bf16)acc[i][j + 1][e];
+        lo[e] = (bf16)acc[i][j][e];
+        lo[4 + e] = (bf16)acc[i][j + 1][e];
+        hi[e] = (bf16)acc[i][j + 2][e];
+        hi[4 + e] = (bf16)acc[i][j + 3][e];
       }
-      *reinterpret_cast<bf16x8*>(Pb + (size_t)xx * a.np + yy) = v8;
+      store_line_pair(reinterpret_cast<bf16x8*>(Pb + (size_t)xx * a.np + y),
+                      reinterpret_cast<bf16x8*>(Pb + (size_t)(xx ^ 1) * a.np + y), g, lo, hi);
     }
 }
 
@@ -413,7 +420,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   // outside n x n read a real row and are masked in the LN pass
   auto issue = [&](int tl) {
     const int tx = min(tl / tiles_per_row, n - 1), ty0 = (tl % tiles_per_row) * kTileRows;
-    raw_tile_issue<ZT, C>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
+    raw_tile_issue<ZT, C, kStream>(a.z + (int64_t)tx * a.z_s0, a.z_s1, ty0, n, raw);
   };
   // wave 0 loads the next tile's mask values (lane = column) with its z rows
   float mnext = 0.f;
