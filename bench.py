@@ -184,8 +184,9 @@ def kernel_avg_ms(fn, kid, reps: int = 5):
 def probe_machine(dev):
     """Sustained MFMA rates (bf16 16x16x32, f32 16x16x4; 2 workgroups of 4
     waves per CU, 8 independent chains per wave), the attention core's
-    instruction mix as a ceiling (odde_probe_mix) and HBM copy bandwidth
-    (2 GiB device copy, bytes read + written) on this GPU."""
+    instruction mix as a ceiling (odde_probe_mix) and HBM bandwidth on this
+    GPU: the library's streaming probe over 2 GiB (read; copy and in-place
+    rewrite, bytes read + written) and torch's device copy beside it."""
     lib = _lib.load()
     sink = torch.zeros(256, device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
@@ -214,10 +215,22 @@ def probe_machine(dev):
         call(50)
         ms = kernel_avg_ms(lambda: call(2000), _lib.K_PROBE, reps=3)
         out[f"core_mix_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
-    src = torch.empty(1 << 29, device=dev)
-    dst = torch.empty_like(src)
+    src = torch.zeros(1 << 29, device=dev)
+    dst = torch.zeros_like(src)
+    nbytes = src.numel() * 4
+    # the library's streaming probe (non-temporal loads and stores, as the
+    # row-tile kernels stream pair data): read, copy, in-place rewrite
+    for name, mode, traffic in (("read", 0, nbytes), ("copy", 1, 2 * nbytes),
+                                ("inplace", 2, 2 * nbytes)):
+        call = lambda m=mode: _lib.check(lib.odde_probe_stream(  # noqa: E731
+            m, ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes, stream),
+            "odde_probe_stream")
+        call()
+        ms = kernel_avg_ms(call, _lib.K_PROBE, reps=5)
+        out[f"hbm_{name}_gbs"] = round(traffic / (ms * 1e-3) / 1e9, 1)
+    # torch's device copy of the same 2 GiB, for comparison
     ms = gpu_median_ms(lambda: dst.copy_(src), warm=2, iters=5)
-    out["hbm_copy_gbs"] = round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)
+    out["hbm_torch_copy_gbs"] = round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
     out["hbm_gbs_spec"] = PEAK_HBM_GBS
     del src, dst
     torch.cuda.empty_cache()

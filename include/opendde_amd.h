@@ -419,6 +419,16 @@ int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flo
 int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
                    void* hip_stream);
 
+/* Streaming-bandwidth probe (no counterpart in the reference): the HBM rate a
+ * kernel that touches its data once can reach with the non-temporal cache
+ * policy the row-tile kernels use.  mode 0 reads `bytes` of src (dst: at
+ * least 256 floats, practically never written); mode 1 copies src to dst;
+ * mode 2 rewrites dst in place with its own contents (src unused).  bytes: a
+ * positive multiple of 16; 16-byte aligned buffers.  Time it with
+ * odde_timing_* (kernel id ODDE_K_PROBE); the traffic is `bytes` for mode 0
+ * and 2 * bytes otherwise. */
+int odde_probe_stream(int mode, const void* src, void* dst, uint64_t bytes, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

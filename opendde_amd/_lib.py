@@ -163,6 +163,7 @@ SYMBOLS = {
     "odde_timing_query": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
     "odde_probe_mfma": (_i32, [_i32, _i64, _i32, _vp, ctypes.POINTER(ctypes.c_double), _vp]),
     "odde_probe_mix": (_i32, [_i32, _i64, _i32, _vp, ctypes.POINTER(ctypes.c_double), _vp]),
+    "odde_probe_stream": (_i32, [_i32, _vp, _vp, _u64, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

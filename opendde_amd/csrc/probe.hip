@@ -87,6 +87,38 @@ __global__ __launch_bounds__(256) void mix_probe_kernel(float* __restrict__ sink
   if (s == 1234.5f) sink[threadIdx.x] = s;  // practically never; keeps the work live
 }
 
+// Streaming bandwidth: each thread moves 4 x 16 bytes per trip of a grid-
+// stride loop with the non-temporal policy (kStream), as the row-tile kernels
+// stream pair data.  kMode 0: read only (a practically-never-taken store keeps
+// the loads live); 1: copy; 2: rewrite dst in place with its own bits.
+template <int kMode>
+__global__ __launch_bounds__(256) void stream_probe_kernel(const f32x4* __restrict__ src,
+                                                           f32x4* __restrict__ dst, uint64_t n16) {
+  constexpr int U = 4;
+  const uint64_t stride = (uint64_t)gridDim.x * 256 * U;
+  typedef int i32x4_t __attribute__((ext_vector_type(4)));
+  i32x4_t acc = {0, 0, 0, 0};
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 * U + threadIdx.x; i < n16; i += stride) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * 256 < n16) v[u] = load_stream((kMode == 2 ? dst : src) + i + u * 256);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i + u * 256 >= n16) continue;
+      if constexpr (kMode == 0) {
+        acc ^= __builtin_bit_cast(i32x4_t, v[u]);
+      } else {
+        asm volatile("" : "+v"(v[u]));  // the in-place rewrite is not elided
+        store_stream(dst + i + u * 256, v[u]);
+      }
+    }
+  }
+  if constexpr (kMode == 0)
+    if ((acc[0] & acc[1] & acc[2] & acc[3]) == 0x7f7f7f7f)
+      reinterpret_cast<float*>(dst)[threadIdx.x] = 1.f;  // practically never
+}
+
 }  // namespace odde
 
 using namespace odde;
@@ -109,6 +141,27 @@ int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flo
   else
     hipLaunchKernelGGL(mfma_probe_kernel<false>, dim3(grid), dim3(256), 0, st, sink, iters);
   return check_launch("probe_mfma");
+}
+
+int odde_probe_stream(int mode, const void* src, void* dst, uint64_t bytes, void* stream) {
+  if (mode < 0 || mode > 2) return set_error(ODDE_EINVAL, "probe_stream: mode must be 0, 1 or 2");
+  if (!dst || (mode != 2 && !src) || bytes == 0 || bytes % 16 != 0)
+    return set_error(ODDE_EINVAL, "probe_stream: bad argument (bytes: a positive multiple of 16)");
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0)
+    return set_error(ODDE_EINVAL, "probe_stream: buffers must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LaunchScope ls(ODDE_K_PROBE, st);
+  const uint64_t n16 = bytes / 16;
+  const uint64_t want = (n16 + 1023) / 1024;  // 4 chunks per thread per trip
+  const int grid = (int)(want < 8192 ? want : 8192);
+  const f32x4* s4 = static_cast<const f32x4*>(src);
+  f32x4* d4 = static_cast<f32x4*>(dst);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(stream_probe_kernel<0>, dim3(grid), dim3(256), 0, st, s4, d4, n16); break;
+    case 1: hipLaunchKernelGGL(stream_probe_kernel<1>, dim3(grid), dim3(256), 0, st, s4, d4, n16); break;
+    default: hipLaunchKernelGGL(stream_probe_kernel<2>, dim3(grid), dim3(256), 0, st, s4, d4, n16);
+  }
+  return check_launch("probe_stream");
 }
 
 int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
