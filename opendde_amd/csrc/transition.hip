@@ -362,7 +362,18 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   load_rows(blockIdx.x);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const int sa_off = r16 * C;                  // + hb*16*C + slot*8
+  // GEMM1's output row m of half hb is hidden unit 8 (m >> 2) + 4 hb + (m & 3)
+  // of the chunk: the W_a / W_b fragment row a lane reads (staged row `row`,
+  // chunks swizzled by row & 15).  A lane's accumulator rows 4g..4g+3 of the
+  // two halves are then the consecutive hidden units 8g..8g+7, so GEMM2's
+  // W_o fragment is one 16-byte read.
+  int sa_off[2], sa_key[2];
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb) {
+    const int row = 8 * (r16 >> 2) + 4 * hb + (r16 & 3);
+    sa_off[hb] = row * C;
+    sa_key[hb] = row & 15;
+  }
   const int so_sw = (r16 >> 2) & 3;
   const float* ln_w = lnp;
   const float* ln_b = lnp + C;
@@ -440,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       // LDS reads are in flight while step s multiplies
       Frag<bf16> fa[2], fb[2];
       auto load_ab = [&](int s, int buf) {
-        const int off = sa_off + (s >> 2) * 16 * C + ((4 * (s & 3) + g) ^ r16) * 8;
+        const int off = sa_off[s >> 2] + ((4 * (s & 3) + g) ^ sa_key[s >> 2]) * 8;
         fa[buf].load(wa + off);
         fb[buf].load(wb + off);
       };
@@ -467,19 +478,12 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
           for (int e = 0; e < 4; ++e) hf[rb].set(4 * hb + e, siluf_(sa[rb][e]) * sb[rb][e]);
       }
-      // GEMM2: W_o[c][h0 + slot] fragments (hidden 4g..4g+3 and 16+4g..16+4g+3)
-      // one 16-channel block at a time, both row blocks
+      // GEMM2: W_o[c][h0 + 8g .. + 7] fragments (staged chunk g, swizzled by
+      // (c >> 2) & 3), one 16-channel block at a time, all row blocks
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const bf16* row = wo + (cb * 16 + r16) * kTrHid + 4 * (g & 1);
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + (((g >> 1)) ^ so_sw) * 8);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + ((2 + (g >> 1)) ^ so_sw) * 8);
         Frag<bf16> fo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          fo.v[e] = lo[e];
-          fo.v[4 + e] = hi[e];
-        }
+        fo.load(wo + (cb * 16 + r16) * kTrHid + (g ^ so_sw) * 8);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb) mma(acc[rb][cb], fo, hf[rb]);
       }
