@@ -240,6 +240,11 @@ __device__ __forceinline__ float sigmoidf_(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 __device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
+// sigmoid(x) from xs = -x log2(e), for products whose weights carry the factor
+constexpr float kNegLog2e = -1.4426950408889634f;
+__device__ __forceinline__ float sigmoid_nl2e(float xs) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(xs));
+}
 
 // 16 bytes per lane from global memory straight into LDS: lane l's bytes
 // land at lds + 16 l.  `base` / `bytes` describe a raw buffer (offsets at or
@@ -347,6 +352,15 @@ __device__ __forceinline__ void load_w_frag(const bf16* __restrict__ w, int ld, 
   load_w_frag(w, ld, o0, n_out, t, b);
 #pragma unroll
   for (int e = 0; e < 8; ++e) f.v[e] = (f16)(float)b.v[e];
+}
+// ... scaled by `scale` on the way (one rounding of scale * w to fp16, 11
+// significant bits): folds a constant factor of the product into the weights
+__device__ __forceinline__ void load_w_frag_scaled(const bf16* __restrict__ w, int ld, int o0,
+                                                   int n_out, int t, float scale, Frag<f16>& f) {
+  Frag<bf16> b;
+  load_w_frag(w, ld, o0, n_out, t, b);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f.v[e] = (f16)(scale * (float)b.v[e]);
 }
 
 }  // namespace odde

@@ -245,6 +245,16 @@ __device__ __forceinline__ void load_w_slice(const WT* __restrict__ w, int ld, i
 #pragma unroll
     for (int t = 0; t < KS; ++t) load_w_frag(w, ld, o0 + 16 * b, n_out, t, f[b][t]);
 }
+// The same as fp16 fragments of scale * w (load_w_frag_scaled).
+template <int NB, int KS>
+__device__ __forceinline__ void load_w_slice_scaled(const bf16* __restrict__ w, int ld, int o0,
+                                                    int n_out, float scale,
+                                                    Frag<f16> (&f)[NB][KS]) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int t = 0; t < KS; ++t) load_w_frag_scaled(w, ld, o0 + 16 * b, n_out, t, scale, f[b][t]);
+}
 
 // Output rows of a row-tile kernel: lane (g, r16) holds, for its row, NB
 // blocks of 4 consecutive outputs r[cb] (float[4] or f32x4) at channels

@@ -1264,7 +1264,10 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
   static_assert(kTileRows * PER_ROW % 256 == 0, "o tile chunks");
   static_assert(sizeof(CT) == 2, "gate scaling in LDS takes 4 x 16-bit o values");
   __shared__ __attribute__((aligned(16))) CT xo[kTileRows * LD];
-  __shared__ __attribute__((aligned(16))) CT xs[kTileRows * TileLD<CT, C>::value];
+  // the gate multiplies in fp16 (LN(z) rounded to fp16, 11 significant bits;
+  // the bf16 weights carry -log2(e) in fp16, so the gate's accumulator feeds
+  // exp2 directly)
+  __shared__ __attribute__((aligned(16))) f16 xs[kTileRows * TileLD<f16, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[Raw::BYTES];
   __shared__ float lnp[2 * C];  // LayerNorm weight, bias
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
@@ -1274,8 +1277,8 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
   }
   Frag<CT> wof[NBO][kHD];
   load_w_slice(a.wo, HD, w * (C / 4), C, wof);
-  Frag<CT> wgf[NBG][kC];
-  load_w_slice(a.wg, C, w * (HD / 4), HD, wgf);
+  Frag<f16> wgf[NBG][kC];
+  load_w_slice_scaled(a.wg, C, w * (HD / 4), HD, kNegLog2e, wgf);
   const int jp = a.jp, n = a.n, tiles_per_row = jp / kTileRows;
 
   // The next tile's z rows (into LDS) and o rows (into registers) are loaded
@@ -1302,7 +1305,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
       const int ci = threadIdx.x + k * 256, r = ci / PER_ROW, cc = (ci % PER_ROW) * VEC;
       *reinterpret_cast<f32x4*>(xo + r * LD + cc) = opre[k];
     }
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return j0 + r < n; }, lnp, lnp + C, a.eps, xs);
+    raw_tile_ln<ZT, f16, C>(raw, [&](int r) { return j0 + r < n; }, lnp, lnp + C, a.eps, xs);
     // this lane's residual values: rows rb*16 + r16, channels c0..c0+3
     float res[RB][NBO][4];
 #pragma unroll
@@ -1322,8 +1325,8 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
     // gate: lane holds row rb*16 + r16, gate channels o..o+3 of its slice
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      Frag<CT> xf[kC];
-      tile_frags<CT, C>(xs, rb, xf);
+      Frag<f16> xf[kC];
+      tile_frags<f16, C>(xs, rb, xf);
 #pragma unroll
       for (int gb = 0; gb < NBG; ++gb) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1333,7 +1336,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
         bf16x4* p = reinterpret_cast<bf16x4*>(xo + (rb * 16 + r16) * LD + o);
         bf16x4 ov = *p;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (bf16)((float)ov[e] * sigmoidf_(acc[e]));
+        for (int e = 0; e < 4; ++e) ov[e] = (bf16)((float)ov[e] * sigmoid_nl2e(acc[e]));
         *p = ov;
       }
     }
@@ -1354,7 +1357,7 @@ __global__ __launch_bounds__(256, 2) void triatt_out_ws_kernel(TriattOutArgs<ZT,
       }
       ZT* orow = a.out + (int64_t)i * a.o_s0;
       store_row_blocks<ZT>(orow + (int64_t)jr * a.o_s1, orow + (int64_t)(jr ^ 1) * a.o_s1,
-                                w * (C / 4), r, jr < n, (jr ^ 1) < n);
+                           w * (C / 4), r, jr < n, (jr ^ 1) < n);
     }
     // xs and xo are rewritten only after the barrier in raw_tile_wait()
   }

@@ -411,9 +411,13 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
   }
   const int which = w >> 1, half = w & 1;
   const int o0 = which * CH + half * (CH / 2);
+  // with fp16 operands the gate weights carry -log2(e), so the gate's
+  // accumulator feeds exp2 directly (sigmoid_nl2e)
+  constexpr bool kFold = std::is_same<XT, f16>::value;
   Frag<XT> wpf[NB][kC], wgf[NB][kC];
   load_w_slice(a.wp, C, o0, 2 * CH, wpf);
-  load_w_slice(a.wg, C, o0, 2 * CH, wgf);
+  if constexpr (kFold) load_w_slice_scaled(a.wg, C, o0, 2 * CH, kNegLog2e, wgf);
+  else load_w_slice(a.wg, C, o0, 2 * CH, wgf);
   CT* dst = which ? a.B : a.A;
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   // the next tile's z rows stream into LDS while a tile is computed; rows
@@ -480,7 +484,9 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_ws_kernel(TrimulProjArgs<Z
           mma(ag, xf[t], wgf[cb][t]);
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[rb][cb][e] = (bf16)(mk[e] * sigmoidf_(ag[e]) * ap[e]);
+        for (int e = 0; e < 4; ++e)
+          ov[rb][cb][e] =
+              (bf16)(mk[e] * (kFold ? sigmoid_nl2e(ag[e]) : sigmoidf_(ag[e])) * ap[e]);
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next raw tile (own part) landed
@@ -520,7 +526,11 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
   constexpr int C = kC * 32, CH = kCH * 32, NBO = C / 64;
   constexpr int LDP = TileLD<CT, CH>::value;
   __shared__ __attribute__((aligned(16))) CT xp[kTileRows * LDP];
-  __shared__ __attribute__((aligned(16))) CT xz[kTileRows * TileLD<CT, C>::value];
+  // the gate multiplies in fp16 with bf16 arithmetic (LN_in(z) rounded to
+  // fp16, the weights carrying -log2(e); see the projection)
+  using GT = typename std::conditional<sizeof(CT) == 2, f16, CT>::type;
+  constexpr bool kFold = std::is_same<GT, f16>::value;
+  __shared__ __attribute__((aligned(16))) GT xz[kTileRows * TileLD<GT, C>::value];
   __shared__ __attribute__((aligned(16))) unsigned char raw[RawTile<ZT, C>::BYTES];
   __shared__ __attribute__((aligned(16))) float lnp[4 * C];  // LN_in weight, bias; s; c
   __shared__ float pst[2 * kTileRows];                      // LN_out mean, rstd per row
@@ -531,9 +541,11 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
     lnp[2 * C + t] = a.wz_sum[t];
     lnp[3 * C + t] = a.wz_bias[t];
   }
-  Frag<CT> wzf[NBO][kCH], wgf[NBO][kC];
+  Frag<CT> wzf[NBO][kCH];
+  Frag<GT> wgf[NBO][kC];
   load_w_slice(a.wz, CH, w * (C / 4), C, wzf);
-  load_w_slice(a.wg, C, w * (C / 4), C, wgf);
+  if constexpr (kFold) load_w_slice_scaled(a.wg, C, w * (C / 4), C, kNegLog2e, wgf);
+  else load_w_slice(a.wg, C, w * (C / 4), C, wgf);
   const int np = a.np, n = a.n, tiles_per_row = np / kTileRows;
   auto issue = [&](int tl) {  // the next tile's z rows (for LN_in), as in the projection
     const int tx = tl / tiles_per_row, ty0 = (tl % tiles_per_row) * kTileRows;
@@ -579,7 +591,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
       }
     }
     raw_tile_wait();  // z rows landed; every wave is done with the previous tile
-    raw_tile_ln<ZT, CT, C>(raw, [&](int r) { return y0 + r < n; }, lnp, lnp + C, a.eps, xz);
+    raw_tile_ln<ZT, GT, C>(raw, [&](int r) { return y0 + r < n; }, lnp, lnp + C, a.eps, xz);
     {  // LN_out statistics of each staged P row (the row itself stays as stored)
       constexpr int Q = CH / 4;
       const int r = threadIdx.x >> 2, quarter = threadIdx.x & 3;
@@ -630,9 +642,10 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
     }
 #pragma unroll
     for (int rb = 0; rb < kTileRows / 16; ++rb) {
-      Frag<CT> pf[kCH], zf[kC];
+      Frag<CT> pf[kCH];
+      Frag<GT> zf[kC];
       tile_frags<CT, CH>(xp, rb, pf);
-      tile_frags<CT, C>(xz, rb, zf);
+      tile_frags<GT, C>(xz, rb, zf);
       const int yr = y0 + rb * 16 + r16;
       const float pmean = pst[rb * 16 + r16], prstd = pst[kTileRows + rb * 16 + r16];
       float r[NBO][4];
@@ -650,12 +663,12 @@ __global__ __launch_bounds__(256, 2) void trimul_out_ws_kernel(TrimulOutArgs<ZT,
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float y = prstd * (ay[e] - pmean * sw[e]) + cw[e];
-          r[cb][e] = res[rb][cb][e] + y * sigmoidf_(ag[e]);
+          r[cb][e] = res[rb][cb][e] + y * (kFold ? sigmoid_nl2e(ag[e]) : sigmoidf_(ag[e]));
         }
       }
       ZT* orow = a.out + (int64_t)x * a.o_s0;
       store_row_blocks<ZT>(orow + (int64_t)yr * a.o_s1, orow + (int64_t)(yr ^ 1) * a.o_s1,
-                                w * (C / 4), r, yr < n, (yr ^ 1) < n);
+                           w * (C / 4), r, yr < n, (yr ^ 1) < n);
     }
     lds_barrier();  // xp and xz are rewritten for the next tile
   }
