@@ -317,12 +317,17 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   const int Q = my_tiles * NCHUNK;
   // A chunk is 24 blocks of 1 KiB (8 per region: W_a, W_b, W_o); wave w's op
   // `op` loads block bi = 4 (op & 1) + w of region op >> 1, so the region is
-  // known at compile time and the lane's part of the source offset is fixed
-  // per wave: W_a / W_b block bi holds rows 4 bi + (l >> 4) (whose swizzle
-  // key, row & 15 = 4 w + (l >> 4), does not depend on op), W_o block bi
-  // holds channels 16 bi + (l >> 2).
+  // known at compile time and the lane's part of the source offset depends
+  // only on op & 1: W_a / W_b block bi holds rows 4 bi + (l >> 4), whose
+  // 16-byte chunks are swizzled by key(row) = (4 (row >> 3) + (row & 3)) & 15
+  // = 8 (op & 1) + 4 (w >> 1) + (l >> 4) (the 16 rows one GEMM1 fragment read
+  // touches, 8 (m >> 2) + 4 hb + (m & 3), have the distinct keys m); W_o
+  // block bi holds channels 16 bi + (l >> 2).
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  const int lane_ab = (l >> 4) * C + ((l & 15) ^ (4 * w + (l >> 4))) * 8;
+  int lane_ab[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+    lane_ab[p] = (l >> 4) * C + ((l & 15) ^ (8 * p + 4 * (w >> 1) + (l >> 4))) * 8;
   const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((l >> 4) & 3)) * 8;
   auto issue = [&](int q) {
     const int h0 = (q % NCHUNK) * kTrHid;
@@ -331,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     for (int op = 0; op < kTpOps; ++op) {
       const int region = op >> 1, bi = 4 * (op & 1) + wu;
       const bf16* src = region == 2 ? a.wo + bi * 16 * HID + h0 + lane_o
-                                    : (region ? a.wb : a.wa) + (h0 + bi * 4) * C + lane_ab;
+                                    : (region ? a.wb : a.wa) + (h0 + bi * 4) * C + lane_ab[op & 1];
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)src,
           (__attribute__((address_space(3))) void*)(base + region * 4096 + bi * 512), 16, 0, 0);
@@ -364,16 +369,12 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 
   // GEMM1's output row m of half hb is hidden unit 8 (m >> 2) + 4 hb + (m & 3)
   // of the chunk: the W_a / W_b fragment row a lane reads (staged row `row`,
-  // chunks swizzled by row & 15).  A lane's accumulator rows 4g..4g+3 of the
-  // two halves are then the consecutive hidden units 8g..8g+7, so GEMM2's
-  // W_o fragment is one 16-byte read.
-  int sa_off[2], sa_key[2];
+  // whose chunks are swizzled by key(row) = r16).  A lane's accumulator rows
+  // 4g..4g+3 of the two halves are then the consecutive hidden units
+  // 8g..8g+7, so GEMM2's W_o fragment is one 16-byte read.
+  int sa_off[2];
 #pragma unroll
-  for (int hb = 0; hb < 2; ++hb) {
-    const int row = 8 * (r16 >> 2) + 4 * hb + (r16 & 3);
-    sa_off[hb] = row * C;
-    sa_key[hb] = row & 15;
-  }
+  for (int hb = 0; hb < 2; ++hb) sa_off[hb] = (8 * (r16 >> 2) + 4 * hb + (r16 & 3)) * C;
   const int so_sw = (r16 >> 2) & 3;
   const float* ln_w = lnp;
   const float* ln_b = lnp + C;
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       // LDS reads are in flight while step s multiplies
       Frag<bf16> fa[2], fb[2];
       auto load_ab = [&](int s, int buf) {
-        const int off = sa_off[s >> 2] + ((4 * (s & 3) + g) ^ sa_key[s >> 2]) * 8;
+        const int off = sa_off[s >> 2] + ((4 * (s & 3) + g) ^ r16) * 8;
         fa[buf].load(wa + off);
         fb[buf].load(wb + off);
       };
