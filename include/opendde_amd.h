@@ -319,11 +319,17 @@ int odde_layer_norm_bwd_noalloc(const odde_layer_norm_bwd_args* args, void* hip_
  * AttentionPairBias (replaces primitives._attention, opendde/model/modules/
  * primitives.py:220-258, which upcasts q, k, v and the bias to fp32 and runs
  * SDPA with scale 1; called from Attention.forward, :800-857):
- *   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
+ *   out[h][i][:] = sum_j softmax_j(s q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
+ *                  (* sigmoid(gate[h][i][:]) when gate is given)
  * q, k, v, out: element (h, i, d) at base + h*s_h + i*s_n + d (head_dim
  * contiguous), dtype f32 or bf16 (out in the same dtype); k and v rows
  * 16-byte aligned; bias: f32 [heads][n_q][n_k] contiguous, or NULL.
  * head_dim in {8, 16, 24, 32, 48, 64}.  No workspace.
+ * Optional: q_scale s (0 is read as 1; Attention._prep_qkv's q / sqrt(c_hidden),
+ * primitives.py:755-756, applied in fp32), and gate (NULL = none; same dtype
+ * and layout rules as q, strides g_sh, g_sn): the output gating
+ * o * sigmoid(linear_g(q_x)) of Attention._wrap_up (primitives.py:772-776)
+ * fused into the store.
  */
 typedef struct odde_bias_attn_args {
   uint32_t struct_size;
@@ -341,6 +347,9 @@ typedef struct odde_bias_attn_args {
   const float* bias;
   void* out;
   int64_t o_sh, o_sn;
+  const void* gate;
+  int64_t g_sh, g_sn;
+  float q_scale;
 } odde_bias_attn_args;
 
 int odde_bias_attn_fwd(const odde_bias_attn_args* args, void* hip_stream);

@@ -132,7 +132,8 @@ class BiasAttnArgs(ctypes.Structure):
         ("head_dim", _i32), ("dtype", _i32),
         ("q", _vp), ("q_sh", _i64), ("q_sn", _i64), ("k", _vp), ("k_sh", _i64), ("k_sn", _i64),
         ("v", _vp), ("v_sh", _i64), ("v_sn", _i64), ("bias", _vp), ("out", _vp),
-        ("o_sh", _i64), ("o_sn", _i64),
+        ("o_sh", _i64), ("o_sn", _i64), ("gate", _vp), ("g_sh", _i64), ("g_sn", _i64),
+        ("q_scale", _f32),
     ]
 
 

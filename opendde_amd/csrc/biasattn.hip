@@ -2,7 +2,11 @@
 // AttentionPairBias core: primitives._attention, opendde/model/modules/
 // primitives.py:220-258, which upcasts q, k, v and the bias to fp32 and runs
 // SDPA with scale 1):
-//   out[h][i][:] = sum_j softmax_j(q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
+//   out[h][i][:] = sum_j softmax_j(s q[h][i] . k[h][j] + bias[h][i][j]) v[h][j][:]
+// with the query scale s (Attention._prep_qkv's 1 / sqrt(c_hidden),
+// primitives.py:755-756) and, optionally, the output gate of
+// Attention._wrap_up (primitives.py:772-776), out *= sigmoid(gate), applied
+// at the store.
 //
 // One workgroup per (head, 64 queries); within it, KS groups of 4 waves
 // (KS = 4 for head dims up to 32, else 1) take disjoint ranges of key blocks
@@ -33,6 +37,9 @@ struct BiasAttnArgs {
   const float* bias;                          // [H][Nq][Nk] or null
   void* out;
   int64_t o_sh, o_sn;
+  const void* gate;  // [H][Nq][D] strides g_sh, g_sn, or null: out *= sigmoid(gate)
+  int64_t g_sh, g_sn;
+  float q_scale;     // multiplies q . k
   int nq, nk;
 };
 
@@ -68,7 +75,7 @@ __global__ __launch_bounds__(256 * BaSplit<D>::KS) void bias_attn_kernel(BiasAtt
   const T* qp = static_cast<const T*>(a.q) + h * a.q_sh + (int64_t)(qvalid ? qi : 0) * a.q_sn;
   float qf[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) qf[s] = qvalid ? to_f32(qp[4 * s + g]) * kLog2e : 0.f;
+  for (int s = 0; s < NS; ++s) qf[s] = qvalid ? to_f32(qp[4 * s + g]) * (a.q_scale * kLog2e) : 0.f;
   const T* kb = static_cast<const T*>(a.k) + h * a.k_sh;
   const T* vb = static_cast<const T*>(a.v) + h * a.v_sh;
   const float* brow = a.bias ? a.bias + ((int64_t)h * a.nq + (qvalid ? qi : 0)) * a.nk : nullptr;
@@ -206,12 +213,16 @@ __global__ __launch_bounds__(256 * BaSplit<D>::KS) void bias_attn_kernel(BiasAtt
   if (!qvalid) return;
   const float inv = 1.0f / lsum;
   T* op = static_cast<T*>(a.out) + h * a.o_sh + (int64_t)qi * a.o_sn;
+  const T* gp = a.gate ? static_cast<const T*>(a.gate) + h * a.g_sh + (int64_t)qi * a.g_sn : nullptr;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int d = 16 * t + 4 * g + r;
-      if (d < D) op[d] = from_f32<T>(o[t][r] * inv);
+      if (d >= D) continue;
+      float y = o[t][r] * inv;
+      if (gp) y *= sigmoidf_(to_f32(gp[d]));
+      op[d] = from_f32<T>(y);
     }
 }
 
@@ -224,6 +235,8 @@ int launch_bias_attn(const odde_bias_attn_args* x, hipStream_t st) {
   a.q_sh = x->q_sh; a.q_sn = x->q_sn; a.k_sh = x->k_sh; a.k_sn = x->k_sn;
   a.v_sh = x->v_sh; a.v_sn = x->v_sn;
   a.bias = x->bias; a.out = x->out; a.o_sh = x->o_sh; a.o_sn = x->o_sn;
+  a.gate = x->gate; a.g_sh = x->g_sh; a.g_sn = x->g_sn;
+  a.q_scale = x->q_scale == 0.f ? 1.f : x->q_scale;
   a.nq = x->n_q; a.nk = x->n_k;
   LaunchScope ls(ODDE_K_BIAS_ATTN, st);
   dim3 grid((x->n_q + 63) / 64, x->heads);

@@ -518,11 +518,17 @@ BIAS_ATTN_HEAD_DIMS = (8, 16, 24, 32, 48, 64)
 
 
 def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                   bias: Optional[torch.Tensor]) -> torch.Tensor:
+                   bias: Optional[torch.Tensor], scale: float = 1.0,
+                   gate: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """fp32 attention with an additive bias, the single track's attention
     core (primitives._attention with scale 1): q, k, v [H, N, D] (any head
     and row strides, D contiguous; f32 or bf16), bias [H, Nq, Nk] or None.
-    Returns [H, Nq, D] in q's dtype."""
+    ``scale`` multiplies q . k (the caller's q / sqrt(c_hidden)); ``gate``
+    [H, Nq, D] (q's dtype, D contiguous) multiplies the output by
+    sigmoid(gate) (Attention._wrap_up's gating). ``out`` [H, Nq, D] (any
+    head and row strides, D contiguous) receives the result; by default a
+    new contiguous tensor. Returns the output in q's dtype."""
     _require_gpu(q, k, v, bias)
     if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
         raise ValueError("q, k, v must be [H, N, D] with matching k and v")
@@ -547,7 +553,14 @@ def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     b = None
     if bias is not None:
         b = bias.to(torch.float32).expand(h, nq, nk).contiguous()
-    out = torch.empty((h, nq, d), dtype=q.dtype, device=q.device)
+    if gate is not None and (tuple(gate.shape) != (h, nq, d) or gate.dtype != q.dtype
+                             or gate.stride(-1) != 1 or gate.device != q.device):
+        raise ValueError("gate must be [H, Nq, D] in q's dtype with D contiguous")
+    if out is None:
+        out = torch.empty((h, nq, d), dtype=q.dtype, device=q.device)
+    elif (tuple(out.shape) != (h, nq, d) or out.dtype != q.dtype or out.stride(-1) != 1
+          or out.device != q.device):
+        raise ValueError("out must be [H, Nq, D] in q's dtype with D contiguous")
     a = _lib.BiasAttnArgs()
     a.struct_size = ctypes.sizeof(_lib.BiasAttnArgs)
     a.n_q, a.n_k, a.heads, a.head_dim, a.dtype = nq, nk, h, d, dtype_code(q.dtype)
@@ -556,6 +569,9 @@ def bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     a.v, a.v_sh, a.v_sn = _ptr(v), v.stride(0), v.stride(1)
     a.bias = _ptr(b)
     a.out, a.o_sh, a.o_sn = _ptr(out), out.stride(0), out.stride(1)
+    if gate is not None:
+        a.gate, a.g_sh, a.g_sn = _ptr(gate), gate.stride(0), gate.stride(1)
+    a.q_scale = float(scale)
     _lib.check(_lib.load().odde_bias_attn_fwd(ctypes.byref(a), _stream(q.device)),
                "odde_bias_attn_fwd")
     return out

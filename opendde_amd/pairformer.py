@@ -121,11 +121,42 @@ class SingleAttention(nn.Module):
         if zero_init:
             nn.init.zeros_(self.linear_o.weight)
 
+    def _hip_fused(self, x: torch.Tensor, attn_bias: Optional[torch.Tensor]) -> torch.Tensor:
+        """Self-attention of one sequence x [N, c] under bf16 autocast on the
+        HIP core: q, k, v and g from one GEMM (the four weights row-
+        concatenated, the q bias padded with zeros; cached per version), the
+        1 / sqrt(c_hidden) scale and the sigmoid gate applied inside the core,
+        whose output is written token-major, so linear_o reads it in place."""
+        bf = torch.bfloat16
+        hd = self.c_hidden * self.num_heads
+        w = K.prepared_cat((self.linear_q.weight, self.linear_k.weight, self.linear_v.weight,
+                            self.linear_g.weight), bf)
+        if self.linear_q.bias is not None:
+            if getattr(self, "_zero_bias", None) is None or self._zero_bias.device != x.device:
+                self._zero_bias = torch.zeros(3 * hd, device=x.device)
+            b = K.prepared_cat((self.linear_q.bias, self._zero_bias), bf)
+        else:
+            b = None
+        n = x.shape[0]
+        with torch.autocast(device_type="cuda", enabled=False):
+            y = F.linear(x.to(bf), w, b)  # [N, 4 hd]: q | k | v | g
+            parts = [y[:, i * hd:(i + 1) * hd].view(n, self.num_heads, self.c_hidden)
+                     .transpose(0, 1) for i in range(4)]
+            o = torch.empty((n, self.num_heads, self.c_hidden), dtype=bf, device=x.device)
+            K.bias_attention(parts[0], parts[1], parts[2], attn_bias,
+                             scale=1.0 / math.sqrt(self.c_hidden), gate=parts[3],
+                             out=o.transpose(0, 1))
+        return self.linear_o(o.view(n, hd))
+
     def forward(self, q_x, kv_x, attn_bias=None, hip: bool = False):
         """``hip``: run the fp32 attention core on the HIP kernel (one
         sequence [N, c], GPU tensors, supported head dim)."""
         def heads(t):
             return t.view(t.shape[:-1] + (self.num_heads, -1)).transpose(-2, -3)
+        if (hip and q_x.is_cuda and kv_x is q_x and q_x.dim() == 2 and _bf16_autocast(q_x)
+                and self.linear_g is not None and self.c_hidden in K.BIAS_ATTN_HEAD_DIMS
+                and (attn_bias is None or attn_bias.dim() == 3)):
+            return self._hip_fused(q_x, attn_bias)
         if q_x.is_cuda and _bf16_autocast(q_x):
             # the bf16 cast autocast gives each of the four projections, once
             same = kv_x is q_x

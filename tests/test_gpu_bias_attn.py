@@ -99,3 +99,47 @@ def test_bias_attention_contiguous_but_misaligned_kv():
     assert kd.is_contiguous() and kd.data_ptr() % 16 == 4
     got = K.bias_attention(q.to(DEV), kd, vd, b.to(DEV)).cpu()
     torch.testing.assert_close(got, exp, rtol=0, atol=1e-4)
+
+
+def test_bias_attention_scale_gate_and_token_major_out():
+    """The query scale applied inside the core, the output gate
+    sigmoid(gate) (Attention._wrap_up, primitives.py:772-776) at the store,
+    and the output written through strides into a token-major [N, H, D]
+    buffer: against the oracle's float64 attention of the scaled queries,
+    times the float64 sigmoid of the gate."""
+    say("[gpu] bias attn scale + gate + token-major out")
+    h, nq, nk, d = 3, 70, 130, 24
+    q, k, v, b = _inputs(h, nq, nk, d, 21)
+    q = q * d ** 0.5  # unscaled queries; the kernel applies 1 / sqrt(d)
+    gate = torch.randn(h, nq, d, generator=torch.Generator().manual_seed(22)) * 2.0
+    exp = (_expected(q / d ** 0.5, k, v, b).double() * torch.sigmoid(gate.double())).float()
+    buf = torch.full((nq, h, d), float("nan"), device=DEV)
+    K.bias_attention(q.to(DEV), k.to(DEV), v.to(DEV), b.to(DEV), scale=1.0 / d ** 0.5,
+                     gate=gate.to(DEV), out=buf.transpose(0, 1))
+    torch.testing.assert_close(buf.transpose(0, 1).cpu(), exp, rtol=0, atol=1e-4)
+
+
+def test_single_attention_fused_path_matches_its_torch_path():
+    """SingleAttention under bf16 autocast with hip=True (one GEMM for q, k,
+    v and g, scale and gate inside the core, token-major output) against
+    the same module's torch path (hip=False: separate bf16 projections,
+    fp32 SDPA, gating in bf16). The two round differently in bf16, so the
+    tolerance is bf16's on O(1) outputs; one core launch."""
+    from opendde_amd.pairformer import SingleAttention
+    say("[gpu] single attention fused path")
+    n, c, heads = 300, 384, 16
+    g = torch.Generator().manual_seed(31)
+    m = SingleAttention(c, c, c, c // heads, heads, gating=True, q_linear_bias=True)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * (0.05 if p.dim() > 1 else 0.5))
+    m = m.to(DEV)
+    x = torch.randn(n, c, generator=g).to(DEV)
+    bias = (torch.randn(heads, n, n, generator=g) * 2.0).to(DEV)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        before = _lib.launch_count(_lib.K_BIAS_ATTN)
+        got = m(x, x, bias, hip=True)
+        assert _lib.launch_count(_lib.K_BIAS_ATTN) == before + 1
+        exp = m(x, x, bias, hip=False)
+    assert got.dtype == exp.dtype == torch.bfloat16
+    torch.testing.assert_close(got.float(), exp.float(), rtol=2e-2, atol=2e-2)
