@@ -657,18 +657,20 @@ __device__ __forceinline__ void tw_tile_map(int L, int ncol, int& rt, int& ct) {
   ct = s % ncol;
 }
 
+template <int TX>
 __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* __restrict__ yn,
                                                                    const bf16* __restrict__ wa,
                                                                    const bf16* __restrict__ wb,
                                                                    bf16* __restrict__ h, int C,
                                                                    int ncol) {
+  using TwShape = GemmShape<TX, kTwTY, kTwWX, kTwKC>;
   __shared__ __attribute__((aligned(16))) bf16 sm[kTwNS * TwShape::STAGE_ELEMS];
   int rt, ct;
   tw_tile_map(blockIdx.x, ncol, rt, ct);
-  const int64_t x0 = (int64_t)rt * kTwTX;
+  const int64_t x0 = (int64_t)rt * TX;
   const int y0 = ct * kTwTY, HID = 4 * C;
   f32x4 acc[TwShape::MX][TwShape::MY];
-  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
+  gemm_nt_mainloop<TX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
       [&](int r) { return yn + (x0 + r) * C; },
       [&](int r) {
         const int R = y0 + r, t = R & 31;
@@ -679,7 +681,7 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
   const int wx = w % kTwWX, wy = w / kTwWX;
 #pragma unroll
   for (int i = 0; i < TwShape::MX; ++i) {
-    const int64_t m = x0 + wx * (kTwTX / kTwWX) + 16 * i + r16;
+    const int64_t m = x0 + wx * (TX / kTwWX) + 16 * i + r16;
 #pragma unroll
     for (int j = 0; j < TwShape::MY; j += 2) {
       const int hid = ((y0 + wy * (kTwTY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
@@ -691,36 +693,69 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
   }
 }
 
-template <typename ZT>
+// kSplit > 1: workgroup column ks of the grid (blockIdx.y) takes hidden
+// units [ks HID / kSplit, (ks + 1) HID / kSplit) and writes its fp32 partial
+// sums to part[ks][m][c] (rows of the padded tile range); the residual is
+// added by transition_wide_reduce_kernel, which sums the partials in order.
+template <typename ZT, int TX, int kSplit>
 __global__ __launch_bounds__(512) void transition_wide_out_kernel(const bf16* __restrict__ h,
                                                                   const bf16* __restrict__ wo,
                                                                   const ZT* x, ZT* out,
-                                                                  int64_t rows, int C, int add,
-                                                                  int ncol) {
+                                                                  float* __restrict__ part,
+                                                                  int64_t rows, int64_t mp,
+                                                                  int C, int add, int ncol) {
+  using TwShape = GemmShape<TX, kTwTY, kTwWX, kTwKC>;
   __shared__ __attribute__((aligned(16))) bf16 sm[kTwNS * TwShape::STAGE_ELEMS];
   int rt, ct;
   tw_tile_map(blockIdx.x, ncol, rt, ct);
-  const int64_t x0 = (int64_t)rt * kTwTX;
-  const int y0 = ct * kTwTY, HID = 4 * C;
+  const int64_t x0 = (int64_t)rt * TX;
+  const int y0 = ct * kTwTY, HID = 4 * C, KS = HID / kSplit, k0 = (int)blockIdx.y * KS;
   f32x4 acc[TwShape::MX][TwShape::MY];
-  gemm_nt_mainloop<kTwTX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
-      [&](int r) { return h + (x0 + r) * HID; },
-      [&](int r) { return wo + (size_t)(y0 + r) * HID; }, HID, sm, acc);
+  gemm_nt_mainloop<TX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
+      [&](int r) { return h + (x0 + r) * HID + k0; },
+      [&](int r) { return wo + (size_t)(y0 + r) * HID + k0; }, KS, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % kTwWX, wy = w / kTwWX;
 #pragma unroll
   for (int i = 0; i < TwShape::MX; ++i) {
-    const int64_t m = x0 + wx * (kTwTX / kTwWX) + 16 * i + r16;
+    const int64_t m = x0 + wx * (TX / kTwWX) + 16 * i + r16;
     if (m >= rows) continue;
 #pragma unroll
     for (int j = 0; j < TwShape::MY; ++j) {
       const int c0 = y0 + wy * (kTwTY / TwShape::WY) + 16 * j + 4 * g;
-      float r[4] = {0.f, 0.f, 0.f, 0.f};
-      if (add) load4(x + m * C + c0, r);
+      if constexpr (kSplit > 1) {
+        store4(part + ((int64_t)blockIdx.y * mp + m) * C + c0, acc[i][j][0], acc[i][j][1],
+               acc[i][j][2], acc[i][j][3]);
+      } else {
+        float r[4] = {0.f, 0.f, 0.f, 0.f};
+        if (add) load4(x + m * C + c0, r);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] += acc[i][j][e];
-      store4(out + m * C + c0, r[0], r[1], r[2], r[3]);
+        for (int e = 0; e < 4; ++e) r[e] += acc[i][j][e];
+        store4(out + m * C + c0, r[0], r[1], r[2], r[3]);
+      }
     }
+  }
+}
+
+// out = (add ? x : 0) + sum over ks of part[ks] (in ks order: deterministic),
+// four channels per thread.
+template <typename ZT, int kSplit>
+__global__ __launch_bounds__(256) void transition_wide_reduce_kernel(const float* __restrict__ part,
+                                                                     const ZT* x, ZT* out,
+                                                                     int64_t rows, int64_t mp,
+                                                                     int C, int add) {
+  const int64_t n4 = rows * C / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * 256) {
+    float r[4] = {0.f, 0.f, 0.f, 0.f};
+    if (add) load4(x + 4 * i, r);
+#pragma unroll
+    for (int ks = 0; ks < kSplit; ++ks) {
+      const f32x4 p = *reinterpret_cast<const f32x4*>(part + ks * mp * C + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += p[e];
+    }
+    store4(out + 4 * i, r[0], r[1], r[2], r[3]);
   }
 }
 
@@ -738,11 +773,24 @@ void launch_tr(const TransitionArgs<ZT, CT>& p, hipStream_t st) {
 }
 
 bool transition_wide(int c, int nf, int dt) { return dt == ODDE_BF16 && c == 384 && nf == 4; }
-int64_t transition_wide_rows(int64_t rows) { return (rows + 2047) / 2048 * 2048; }
+// Up to kTwSmallRows rows (the single track) the GEMMs take 128-row tiles
+// and the output GEMM splits the hidden dimension kTwSplit ways, so that a
+// few hundred rows still fill the GPU; tile rows are padded to whole groups
+// of 8 row tiles (tw_tile_map).
+constexpr int64_t kTwSmallRows = 16384;
+constexpr int kTwSplit = 4;
+bool transition_wide_small(int64_t rows) { return rows <= kTwSmallRows; }
+int64_t transition_wide_rows(int64_t rows) {
+  const int64_t q = transition_wide_small(rows) ? 8 * 128 : 8 * kTwTX;
+  return (rows + q - 1) / q * q;
+}
 uint64_t transition_ws_bytes(const odde_transition_args* a) {
   if (!transition_wide(a->c, a->n_factor, a->compute_dtype)) return 0;
-  // normalised rows [Mp][C] and hidden activations [Mp][4C], bf16
-  return (uint64_t)transition_wide_rows(a->rows) * 5 * a->c * 2 + 256;
+  // normalised rows [Mp][C] and hidden activations [Mp][4C], bf16; with the
+  // split output GEMM its fp32 partial sums [kTwSplit][Mp][C]
+  const uint64_t mp = (uint64_t)transition_wide_rows(a->rows);
+  const uint64_t part = transition_wide_small(a->rows) ? (uint64_t)kTwSplit * mp * a->c * 4 : 0;
+  return mp * 5 * a->c * 2 + part + 256;
 }
 
 template <typename ZT>
@@ -757,14 +805,31 @@ int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
   hipLaunchKernelGGL((ln_view_bf16_kernel<ZT, 384>), dim3(lg), dim3(256), 0, st,
                      static_cast<const ZT*>(a->x), (int64_t)0, (int64_t)C, (int)rows, 1,
                      (int)rows, a->ln_w, a->ln_b, a->eps, yn);
-  const int row_tiles = (int)(mp / kTwTX);
   const int ncol1 = 8 * C / kTwTY, ncol2 = C / kTwTY;
-  hipLaunchKernelGGL(transition_wide_gate_kernel, dim3(row_tiles * ncol1), dim3(512), 0, st, yn,
-                     static_cast<const bf16*>(a->w_a), static_cast<const bf16*>(a->w_b), h, C,
-                     ncol1);
-  hipLaunchKernelGGL((transition_wide_out_kernel<ZT>), dim3(row_tiles * ncol2), dim3(512), 0, st,
-                     h, static_cast<const bf16*>(a->w_o), static_cast<const ZT*>(a->x),
-                     static_cast<ZT*>(a->out), rows, C, a->add_residual, ncol2);
+  const bf16* wa = static_cast<const bf16*>(a->w_a);
+  const bf16* wb = static_cast<const bf16*>(a->w_b);
+  const bf16* wo = static_cast<const bf16*>(a->w_o);
+  const ZT* x = static_cast<const ZT*>(a->x);
+  ZT* out = static_cast<ZT*>(a->out);
+  if (transition_wide_small(rows)) {
+    const int row_tiles = (int)(mp / 128);
+    float* part = reinterpret_cast<float*>(h + mp * 4 * C);
+    hipLaunchKernelGGL(transition_wide_gate_kernel<128>, dim3(row_tiles * ncol1), dim3(512), 0, st,
+                       yn, wa, wb, h, C, ncol1);
+    hipLaunchKernelGGL((transition_wide_out_kernel<ZT, 128, kTwSplit>),
+                       dim3(row_tiles * ncol2, kTwSplit), dim3(512), 0, st, h, wo, x, out, part,
+                       rows, mp, C, a->add_residual, ncol2);
+    const int rg = (int)std::min<int64_t>((rows * C / 4 + 255) / 256, 2048);
+    hipLaunchKernelGGL((transition_wide_reduce_kernel<ZT, kTwSplit>), dim3(rg), dim3(256), 0, st,
+                       part, x, out, rows, mp, C, a->add_residual);
+  } else {
+    const int row_tiles = (int)(mp / kTwTX);
+    hipLaunchKernelGGL(transition_wide_gate_kernel<kTwTX>, dim3(row_tiles * ncol1), dim3(512), 0,
+                       st, yn, wa, wb, h, C, ncol1);
+    hipLaunchKernelGGL((transition_wide_out_kernel<ZT, kTwTX, 1>), dim3(row_tiles * ncol2),
+                       dim3(512), 0, st, h, wo, x, out, nullptr, rows, mp, C, a->add_residual,
+                       ncol2);
+  }
   if (a->pb_heads) {
     TransitionArgs<ZT, bf16> p;
     p.out = static_cast<ZT*>(a->out);

@@ -306,7 +306,10 @@ def test_triangle_attention_fully_masked_rows_are_mean_of_v(n_pad):
 # -------------------------------------------------------------- transition
 
 
-@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 1000), (384, 130)])
+# c = 384 takes 128-row tiles with a split output GEMM up to 16384 rows (the
+# single track) and 256-row tiles above: both sides of that boundary
+@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 1000), (384, 130),
+                                    (384, 16384), (384, 20000)])
 def test_transition_bf16(c, rows):
     from opendde_amd.pairformer import Transition
     # weights scaled so the output stays O(1) at every width (std ~0.6, max
