@@ -103,19 +103,41 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
   __shared__ __attribute__((aligned(16))) bf16 t[64 * LD];
   const int x = blockIdx.y, y0 = blockIdx.x * 64;
   const bf16* src = P + (size_t)x * np + y0;
-  constexpr int NL = CH * 8 / 256;  // 16-byte chunks per thread (8 per channel row)
-  bf16x8 ld[NL];
+  // unit u: channels 4 (u >> 3) .. + 3 at columns 8 (u & 7) .. + 7, four
+  // 16-byte loads (eight lanes read a channel's whole 128-byte line),
+  // transposed in registers into eight 8-byte LDS stores (one per column).
+  // Channel c of column yy sits at c ^ (8 (yy >> 3)): 4-channel groups stay
+  // contiguous under the swizzle.
+  constexpr int NU = CH * 2;                 // units
+  constexpr int UPT = (NU + 255) / 256;      // units per thread
+  uint32_t ld[UPT][4][4];                    // [unit][channel][column pair]
 #pragma unroll
-  for (int k = 0; k < NL; ++k) {  // all loads in flight before the first LDS store
-    const int ci = threadIdx.x + 256 * k, c = ci >> 3, yy = (ci & 7) * 8;
-    ld[k] = *reinterpret_cast<const bf16x8*>(src + (size_t)c * np * np + yy);
+  for (int k = 0; k < UPT; ++k) {  // all loads in flight before the first LDS store
+    const int u = threadIdx.x + 256 * k, c4 = (u >> 3) * 4, yy = (u & 7) * 8;
+    if (NU % 256 == 0 || u < NU) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + (size_t)(c4 + i) * np * np + yy);
+        ld[k][i][0] = v.x; ld[k][i][1] = v.y; ld[k][i][2] = v.z; ld[k][i][3] = v.w;
+      }
+    }
   }
 #pragma unroll
-  for (int k = 0; k < NL; ++k) {
-    const int ci = threadIdx.x + 256 * k, c = ci >> 3, yy = (ci & 7) * 8;
-    const int cs = c ^ (8 * ((yy >> 3) & 7));
+  for (int k = 0; k < UPT; ++k) {
+    const int u = threadIdx.x + 256 * k, c4 = (u >> 3) * 4, yy = (u & 7) * 8;
+    if (!(NU % 256 == 0 || u < NU)) continue;
+    const int cs = c4 ^ (8 * ((yy >> 3) & 7));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) t[(yy + e) * LD + cs] = ld[k][e];
+    for (int p = 0; p < 4; ++p) {
+      // columns yy + 2p (low halves) and yy + 2p + 1 (high halves) of the
+      // four channels: byte permutes pair channel i with i + 1
+      const uint32_t lo01 = __builtin_amdgcn_perm(ld[k][1][p], ld[k][0][p], 0x05040100u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(ld[k][3][p], ld[k][2][p], 0x05040100u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(ld[k][1][p], ld[k][0][p], 0x07060302u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(ld[k][3][p], ld[k][2][p], 0x07060302u);
+      *reinterpret_cast<uint2*>(t + (yy + 2 * p) * LD + cs) = make_uint2(lo01, lo23);
+      *reinterpret_cast<uint2*>(t + (yy + 2 * p + 1) * LD + cs) = make_uint2(hi01, hi23);
+    }
   }
   __syncthreads();
   const int yl = threadIdx.x >> 2, part = threadIdx.x & 3;
@@ -148,12 +170,16 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
   bf16* dst = out + ((size_t)x * np + y) * CH + part * Q;
 #pragma unroll
   for (int k = 0; k < Q / 8; ++k) {
+    const int c0 = part * Q + 8 * k;  // LayerNorm parameters as 16-byte vectors
+    float lw[8], lb[8];
+    load4(ln_w + c0, lw);
+    load4(ln_w + c0 + 4, lw + 4);
+    load4(ln_b + c0, lb);
+    load4(ln_b + c0 + 4, lb + 4);
     bf16x8 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = part * Q + 8 * k + e;
-      h[e] = (bf16)(valid ? (v[8 * k + e] - mean) * rstd * ln_w[c] + ln_b[c] : 0.f);
-    }
+    for (int e = 0; e < 8; ++e)
+      h[e] = (bf16)(valid ? (v[8 * k + e] - mean) * rstd * lw[e] + lb[e] : 0.f);
     reinterpret_cast<bf16x8*>(dst)[k] = h;
   }
 }
