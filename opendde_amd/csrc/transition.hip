@@ -719,20 +719,29 @@ __global__ __launch_bounds__(512) void transition_wide_out_kernel(const bf16* __
 #pragma unroll
   for (int i = 0; i < TwShape::MX; ++i) {
     const int64_t m = x0 + wx * (TX / kTwWX) + 16 * i + r16;
-    if (m >= rows) continue;
+    if constexpr (kSplit > 1) {
+      if (m >= rows) continue;
 #pragma unroll
-    for (int j = 0; j < TwShape::MY; ++j) {
-      const int c0 = y0 + wy * (kTwTY / TwShape::WY) + 16 * j + 4 * g;
-      if constexpr (kSplit > 1) {
+      for (int j = 0; j < TwShape::MY; ++j) {
+        const int c0 = y0 + wy * (kTwTY / TwShape::WY) + 16 * j + 4 * g;
         store4(part + ((int64_t)blockIdx.y * mp + m) * C + c0, acc[i][j][0], acc[i][j][1],
                acc[i][j][2], acc[i][j][3]);
-      } else {
-        float r[4] = {0.f, 0.f, 0.f, 0.f};
-        if (add) load4(x + m * C + c0, r);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] += acc[i][j][e];
-        store4(out + m * C + c0, r[0], r[1], r[2], r[3]);
       }
+    } else {
+      // rows m and m ^ 1 (lanes r16, r16 ^ 1) complete each other's lines
+      const bool ok = m < rows, pok = (m ^ 1) < rows;
+      float r[TwShape::MY][4];
+#pragma unroll
+      for (int j = 0; j < TwShape::MY; ++j) {
+        const int c0 = y0 + wy * (kTwTY / TwShape::WY) + 16 * j + 4 * g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[j][e] = 0.f;
+        if (add && ok) load4(x + m * C + c0, r[j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[j][e] += acc[i][j][e];
+      }
+      store_row_blocks<ZT>(out + m * C, out + (m ^ 1) * C, y0 + wy * (kTwTY / TwShape::WY), r,
+                           ok, pok);
     }
   }
 }

@@ -803,17 +803,21 @@ __global__ __launch_bounds__(512) void trimul_out_wide_kernel(TrimulWideOutArgs<
 #pragma unroll
   for (int i = 0; i < WideShape::MX; ++i) {
     const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + r16;
-    const int x = (int)(m / np), y = (int)(m % np);
-    if (x >= a.n || y >= a.n) continue;
+    const int x = (int)(m / np), y = (int)(m % np);  // np is even: lane r16 ^ 1 has y ^ 1
+    const bool ok = x < a.n && y < a.n, pok = x < a.n && (y ^ 1) < a.n;
+    float r[WideShape::MY][4];
 #pragma unroll
     for (int j = 0; j < WideShape::MY; ++j) {
       const int c0 = y0 + wy * (kWTY / WideShape::WY) + 16 * j + 4 * g;
-      float r[4] = {0.f, 0.f, 0.f, 0.f};
-      if (a.add) load4(a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 + c0, r);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] += sigmoidf_(accg[i][j][e]) * accy[i][j][e];
-      store4(a.out + (int64_t)x * a.o_s0 + (int64_t)y * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+      for (int e = 0; e < 4; ++e) r[j][e] = 0.f;
+      if (a.add && ok) load4(a.z + (int64_t)x * a.z_s0 + (int64_t)y * a.z_s1 + c0, r[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[j][e] += sigmoidf_(accg[i][j][e]) * accy[i][j][e];
     }
+    ZT* orow = a.out + (int64_t)x * a.o_s0;
+    store_row_blocks<ZT>(orow + (int64_t)y * a.o_s1, orow + (int64_t)(y ^ 1) * a.o_s1,
+                         y0 + wy * (kWTY / WideShape::WY), r, ok, pok);
   }
 }
 
