@@ -657,26 +657,29 @@ __device__ __forceinline__ void tw_tile_map(int L, int ncol, int& rt, int& ct) {
   ct = s % ncol;
 }
 
-template <int TX>
+template <int TX, int TY = kTwTY, int KC = kTwKC>
 __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* __restrict__ yn,
                                                                    const bf16* __restrict__ wa,
                                                                    const bf16* __restrict__ wb,
                                                                    bf16* __restrict__ h, int C,
                                                                    int ncol) {
-  using TwShape = GemmShape<TX, kTwTY, kTwWX, kTwKC>;
-  __shared__ __attribute__((aligned(16))) bf16 sm[kTwNS * TwShape::STAGE_ELEMS];
+  using TwShape = GemmShape<TX, TY, kTwWX, KC>;
+  constexpr int NS = KC == 64 ? 2 : kTwNS;
+  __shared__ __attribute__((aligned(16))) bf16 sm[NS * TwShape::STAGE_ELEMS];
   int rt, ct;
   tw_tile_map(blockIdx.x, ncol, rt, ct);
   const int64_t x0 = (int64_t)rt * TX;
-  const int y0 = ct * kTwTY, HID = 4 * C;
+  const int y0 = ct * TY, HID = 4 * C;
   f32x4 acc[TwShape::MX][TwShape::MY];
-  gemm_nt_mainloop<TX, kTwTY, kTwWX, kTwNS, true, kTwKC>(
-      [&](int r) { return yn + (x0 + r) * C; },
-      [&](int r) {
-        const int R = y0 + r, t = R & 31;
-        return (t < 16 ? wa : wb) + (size_t)((R >> 5) * 16 + (t & 15)) * C;
-      },
-      C, sm, acc);
+  auto arow = [&](int r) { return yn + (x0 + r) * C; };
+  auto brow = [&](int r) {
+    const int R = y0 + r, t = R & 31;
+    return (t < 16 ? wa : wb) + (size_t)((R >> 5) * 16 + (t & 15)) * C;
+  };
+  if constexpr (KC == 64)
+    gemm_nt_mainloop_pipe64<TX, TY, kTwWX, true>(arow, brow, C, sm, acc);
+  else
+    gemm_nt_mainloop<TX, TY, kTwWX, NS, true, KC>(arow, brow, C, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % kTwWX, wy = w / kTwWX;
 #pragma unroll
@@ -684,7 +687,7 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
     const int64_t m = x0 + wx * (TX / kTwWX) + 16 * i + r16;
 #pragma unroll
     for (int j = 0; j < TwShape::MY; j += 2) {
-      const int hid = ((y0 + wy * (kTwTY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
+      const int hid = ((y0 + wy * (TY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
       bf16x4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = (bf16)(siluf_(acc[i][j][e]) * acc[i][j + 1][e]);
@@ -832,9 +835,11 @@ int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
     hipLaunchKernelGGL((transition_wide_reduce_kernel<ZT, kTwSplit>), dim3(rg), dim3(256), 0, st,
                        part, x, out, rows, mp, C, a->add_residual);
   } else {
-    const int row_tiles = (int)(mp / kTwTX);
-    hipLaunchKernelGGL(transition_wide_gate_kernel<kTwTX>, dim3(row_tiles * ncol1), dim3(512), 0,
-                       st, yn, wa, wb, h, C, ncol1);
+    // the gate GEMM (N = 8C): 256 x 256 tiles, 64-k pipelined stages (each
+    // wave 64 x 128, fewer LDS bytes per MFMA than 256 x 128 tiles)
+    const int row_tiles = (int)(mp / kTwTX), ncol1w = 8 * C / 256;
+    hipLaunchKernelGGL((transition_wide_gate_kernel<kTwTX, 256, 64>), dim3(row_tiles * ncol1w),
+                       dim3(512), 0, st, yn, wa, wb, h, C, ncol1w);
     hipLaunchKernelGGL((transition_wide_out_kernel<ZT, kTwTX, 1>), dim3(row_tiles * ncol2),
                        dim3(512), 0, st, h, wo, x, out, nullptr, rows, mp, C, a->add_residual,
                        ncol2);
