@@ -1640,18 +1640,18 @@ __global__ __launch_bounds__(512) void triatt_qkvg_wide_kernel(TriattProjArgs<ZT
       if (type == 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v8[e] = (bf16)(v[e] * a.q_scale);
-        *reinterpret_cast<bf16x8*>(a.q + off) = v8;
+        store_stream(reinterpret_cast<bf16x8*>(a.q + off), v8);
       } else if (type == 1) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           v8[e] = (bf16)v[e];
           ss[j >> 1] += v[e] * v[e];
         }
-        *reinterpret_cast<bf16x8*>(a.k + off) = v8;
+        store_stream(reinterpret_cast<bf16x8*>(a.k + off), v8);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v8[e] = (bf16)sigmoidf_(v[e]);
-        *reinterpret_cast<bf16x8*>(a.gate + off) = v8;
+        store_stream(reinterpret_cast<bf16x8*>(a.gate + off), v8);
       }
     }
     if (type == 1) {

@@ -736,30 +736,41 @@ __global__ __launch_bounds__(512) void trimul_proj_wide_kernel(TrimulWideProjArg
       C, sm, acc);
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % kWWX, wy = w / kWWX;
-  static_assert(WideShape::MX % 2 == 0 && (kWTX / kWWX) % 32 == 0, "row blocks pair up");
+  // The wave's 64 pairs lie in one row x (np is a multiple of 64): row blocks
+  // 0, 1 give a lane pairs y + 8g .. + 7 (slot g of the channel's 128-byte
+  // line of this row), row blocks 2, 3 the pairs 32 further (slot 4 + g);
+  // lanes r16 and r16 ^ 1 (channels chan, chan ^ 1) complete each other's
+  // lines, stored whole with the streaming policy (store_line_pair).
+  static_assert(WideShape::MX == 4 && kWTX / kWWX == 64, "one 64-pair line per channel and wave");
+  const int64_t mw = x0 + wx * (kWTX / kWWX);
+  const int x = (int)(mw / np), yw = (int)(mw % np);
+  float mk[2][8];
 #pragma unroll
-  for (int i = 0; i < WideShape::MX; i += 2) {
-    // pairs m .. m+7 (one row x): row blocks i (m..m+3) and i + 1 (m+4..m+7)
-    const int64_t m = x0 + wx * (kWTX / kWWX) + 16 * i + 8 * g;
-    const int x = (int)(m / np), y = (int)(m % np);
-    float mk[8];
+  for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      mk[e] = (x < a.n && y + e < a.n)
-                  ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)(y + e) * a.m_s1] : 1.0f)
-                  : 0.f;
+    for (int e = 0; e < 8; ++e) {
+      const int y = yw + 32 * hh + 8 * g + e;
+      mk[hh][e] = (x < a.n && y < a.n)
+                      ? (a.mask ? a.mask[(int64_t)x * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
+                      : 0.f;
+    }
 #pragma unroll
-    for (int j = 0; j < WideShape::MY; j += 2) {
-      const int R = y0 + wy * (kWTY / WideShape::WY) + 16 * j;  // first row of the value block
-      const int side = R / (2 * CH), chan = ((R % (2 * CH)) >> 5) * 16 + r16;
-      bf16x8 v;
+  for (int j = 0; j < WideShape::MY; j += 2) {
+    const int R = y0 + wy * (kWTY / WideShape::WY) + 16 * j;  // first row of the value block
+    const int side = R / (2 * CH), chan = ((R % (2 * CH)) >> 5) * 16 + r16;
+    bf16x8 v[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[e] = (bf16)(mk[e] * sigmoidf_(acc[i][j + 1][e]) * acc[i][j][e]);
-        v[4 + e] = (bf16)(mk[4 + e] * sigmoidf_(acc[i + 1][j + 1][e]) * acc[i + 1][j][e]);
+        const int i = 2 * hh;
+        v[hh][e] = (bf16)(mk[hh][e] * sigmoidf_(acc[i][j + 1][e]) * acc[i][j][e]);
+        v[hh][4 + e] = (bf16)(mk[hh][4 + e] * sigmoidf_(acc[i + 1][j + 1][e]) * acc[i + 1][j][e]);
       }
-      *reinterpret_cast<bf16x8*>((side ? a.B : a.A) + ((size_t)chan * np + x) * np + y) = v;
-    }
+    bf16* dst = side ? a.B : a.A;
+    store_line_pair(reinterpret_cast<bf16x8*>(dst + ((size_t)chan * np + x) * np + yw),
+                    reinterpret_cast<bf16x8*>(dst + ((size_t)(chan ^ 1) * np + x) * np + yw), g,
+                    v[0], v[1]);
   }
 }
 
