@@ -672,9 +672,19 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
   const int y0 = ct * TY, HID = 4 * C;
   f32x4 acc[TwShape::MX][TwShape::MY];
   auto arow = [&](int r) { return yn + (x0 + r) * C; };
+  // Columns come in 32-wide groups q = R >> 5: 16 of W_a then the same 16
+  // hidden units of W_b.  With 256-wide tiles (a wave's 128 columns = 64
+  // hidden units, one 128-byte line of h per row) group q's column n is
+  // hidden unit 64 (q >> 2) + 32 ((q >> 1) & 1) + 8 (n >> 2) + 4 (q & 1) +
+  // (n & 3), so that a lane's groups 2k and 2k + 1 are 8 consecutive units;
+  // otherwise 16 (q) + n.
+  constexpr bool kLines = TY == 256;
   auto brow = [&](int r) {
-    const int R = y0 + r, t = R & 31;
-    return (t < 16 ? wa : wb) + (size_t)((R >> 5) * 16 + (t & 15)) * C;
+    const int R = y0 + r, t = R & 31, q = R >> 5, nn = t & 15;
+    const int hid = kLines ? 64 * (q >> 2) + 32 * ((q >> 1) & 1) + 8 * (nn >> 2) + 4 * (q & 1) +
+                                 (nn & 3)
+                           : q * 16 + nn;
+    return (t < 16 ? wa : wb) + (size_t)hid * C;
   };
   if constexpr (KC == 64)
     gemm_nt_mainloop_pipe64<TX, TY, kTwWX, true>(arow, brow, C, sm, acc);
@@ -685,13 +695,32 @@ __global__ __launch_bounds__(512) void transition_wide_gate_kernel(const bf16* _
 #pragma unroll
   for (int i = 0; i < TwShape::MX; ++i) {
     const int64_t m = x0 + wx * (TX / kTwWX) + 16 * i + r16;
+    if constexpr (kLines) {
+      // hidden units 64 (2 ct + wy) + 8g .. + 7 (slot g of row m's line) from
+      // groups 0, 1 of the wave, the same + 32 (slot 4 + g) from groups 2, 3;
+      // rows m and m ^ 1 (lanes r16, r16 ^ 1) complete each other's lines
+      static_assert(TwShape::MY == 8, "four column groups per wave");
+      bf16x8 v[2];
 #pragma unroll
-    for (int j = 0; j < TwShape::MY; j += 2) {
-      const int hid = ((y0 + wy * (TY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
-      bf16x4 v;
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (bf16)(siluf_(acc[i][j][e]) * acc[i][j + 1][e]);
-      *reinterpret_cast<bf16x4*>(h + m * HID + hid) = v;
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * hh;
+          v[hh][e] = (bf16)(siluf_(acc[i][j][e]) * acc[i][j + 1][e]);
+          v[hh][4 + e] = (bf16)(siluf_(acc[i][j + 2][e]) * acc[i][j + 3][e]);
+        }
+      const int hb = (y0 + wy * (TY / TwShape::WY)) / 2;  // the wave's first hidden unit
+      store_line_pair(reinterpret_cast<bf16x8*>(h + m * HID + hb),
+                      reinterpret_cast<bf16x8*>(h + (m ^ 1) * HID + hb), g, v[0], v[1]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < TwShape::MY; j += 2) {
+        const int hid = ((y0 + wy * (TY / TwShape::WY) + 16 * j) >> 5) * 16 + 4 * g;
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(siluf_(acc[i][j][e]) * acc[i][j + 1][e]);
+        *reinterpret_cast<bf16x4*>(h + m * HID + hid) = v;
+      }
     }
   }
 }
