@@ -68,9 +68,7 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>&
       zv[cb][e] = round_to<ZT>(zacc[cb][e]);  // the value as stored
       s += zv[cb][e];
     }
-  s += __shfl_xor(s, 16, 64);
-  s += __shfl_xor(s, 32, 64);
-  const float mean = s * (1.0f / C);
+  const float mean = group_sum_fast(s) * (1.0f / C);
   float q = 0.f;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb)
@@ -79,9 +77,7 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionArgs<ZT, CT>&
       const float d = zv[cb][e] - mean;
       q += d * d;
     }
-  q += __shfl_xor(q, 16, 64);
-  q += __shfl_xor(q, 32, 64);
-  const float rstd = rsqrtf(q * (1.0f / C) + a.pb_eps);
+  const float rstd = rsqrtf(group_sum_fast(q) * (1.0f / C) + a.pb_eps);
   f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < kC; ++t) {
@@ -229,10 +225,10 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 // walked in chunks of 32 whose W_a / W_b rows and W_o columns (24 KiB) stream
 // into three LDS stages by direct global -> LDS loads, two chunks ahead,
 // continuing across row tiles (every tile walks the same chunks).  At a tile
-// boundary the residual rows are loaded one row block at a time and the
-// outputs stored, then the pair bias (if asked) is formed from the stored
-// values, then the next tile's rows are loaded; so the loads of one
-// workgroup overlap the other workgroup's MFMA work.
+// boundary each row block in turn adds its residual rows and stores, loads
+// the next block's residual rows, forms the pair bias (if asked) from the
+// stored values and loads its rows of the next tile; so the loads of one
+// workgroup overlap its own epilogue and the other workgroup's MFMA work.
 // LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
 // bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
 // (4 slots; slot t of row r holds chunk t ^ ((r >> 2) & 3): the 16 rows of a
@@ -243,6 +239,56 @@ constexpr int kTpRows = 64 * kRB;
 constexpr int kTpStages = 3;
 constexpr int kTpChunkElems = 3 * 4096;  // W_a, W_b: 32 x 128; W_o: 128 x 32
 constexpr int kTpOps = 6;                // 1 KiB direct loads per wave per chunk
+
+// The pair bias of one 16-row block of the pipelined C = 128 form, from the
+// rows as stored: LN(z) @ W^T for 16 heads with the LayerNorm weight folded
+// into W' = W diag(ln_w) (bf16, in LDS in fragment order: 16 bytes per lane
+// and step) and its bias into b = W ln_b, so pb = rstd (W' (z - mean)) + b.
+// The MFMA's K slots follow the accumulator layout of z: slot e of step t is
+// channel 32t + 16 (e >> 2) + 4g + (e & 3).
+template <typename ZT>
+__device__ __forceinline__ void pair_bias_folded(const TransitionArgs<ZT, bf16>& a,
+                                                 const f32x4 (&zacc)[8], int64_t row, bool valid,
+                                                 const bf16* pbwf, const float* pbb) {
+  constexpr int C = 128, NCB = 8;
+  int l = lane_id();
+  asm volatile("" : "+v"(l));  // lane addresses recomputed per call, not kept live by callers
+  const int g = l >> 4;
+  float d[NCB][4];
+  float s = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d[cb][e] = round_to<ZT>(zacc[cb][e]);  // the value as stored
+      s += d[cb][e];
+    }
+  const float mean = group_sum_fast(s) * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d[cb][e] -= mean;
+      q += d[cb][e] * d[cb][e];
+    }
+  const float rstd = rsqrtf(group_sum_fast(q) * (1.0f / C) + a.pb_eps);
+  f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    Frag<bf16> wf, yf;
+    wf.load(pbwf + (t * 64 + l) * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yf.set(e, d[2 * t + (e >> 2)][e & 3]);
+    mma(pacc, wf, yf);
+  }
+  float bb[4];
+  load4(pbb + 4 * g, bb);
+  if (valid) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a.pb_out[(size_t)(4 * g + e) * a.rows + row] = pacc[e] * rstd + bb[e];
+  }
+}
 
 // A lane's K32 fragment slots of one C = 128 row (channels 32t + 8g .. +7 for
 // t = 0..3) held as raw 16-byte chunks until they are normalised.
@@ -295,19 +341,39 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   constexpr int C = 128, kC = 4, HID = 512, NCB = C / 16, NCHUNK = HID / kTrHid;
   __shared__ __attribute__((aligned(16))) bf16 ws[kTpStages][kTpChunkElems];
   // parameters read every tile, kept in LDS: LN weight, bias; and for the
-  // pair-bias epilogue its LN weight, bias and the 16 x C projection
-  __shared__ __attribute__((aligned(16))) float lnp[4 * C];
-  __shared__ __attribute__((aligned(16))) bf16 pbw[16 * C];
+  // pair-bias epilogue the folded 16 x C projection (fragment order) and
+  // its 16 biases
+  __shared__ __attribute__((aligned(16))) float lnp[2 * C];
+  __shared__ __attribute__((aligned(16))) bf16 pbwf[16 * C];
+  __shared__ __attribute__((aligned(16))) float pbb[16 + 64];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   for (int t = threadIdx.x; t < C; t += 256) {
     lnp[t] = a.ln_w[t];
     lnp[C + t] = a.ln_b[t];
-    lnp[2 * C + t] = a.pb_out ? a.pb_ln_w[t] : 0.f;
-    lnp[3 * C + t] = (a.pb_out && a.pb_ln_b) ? a.pb_ln_b[t] : 0.f;
   }
-  if (a.pb_out)
-    for (int t = threadIdx.x; t < 16 * C; t += 256) pbw[t] = a.pb_w[t];
-  __syncthreads();  // lnp / pbw are read before the first chunk barrier
+  if (a.pb_out) {
+    // thread (w, g, r16) forms fragment slot set (t = w, g) of head r16:
+    // W'[r16][c] = W[r16][c] ln_w[c] for c = 32w + 16 (e >> 2) + 4g + (e & 3),
+    // and its part of b[r16] = sum_c W[r16][c] ln_b[c]; the parts are summed
+    // over g by lane swaps and over w in a fixed order
+    Frag<bf16> wf;
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = 32 * w + 16 * (e >> 2) + 4 * g + (e & 3);
+      const float wv = (float)a.pb_w[r16 * C + c];
+      wf.set(e, wv * a.pb_ln_w[c]);
+      if (a.pb_ln_b) part += wv * a.pb_ln_b[c];
+    }
+    *reinterpret_cast<bf16x8*>(pbwf + threadIdx.x * 8) = wf.v;
+    part = group_sum_fast(part);
+    if (g == 0) pbb[16 + 16 * w + r16] = part;
+    __syncthreads();
+    if (threadIdx.x < 16)
+      pbb[threadIdx.x] = ((pbb[16 + threadIdx.x] + pbb[32 + threadIdx.x]) + pbb[48 + threadIdx.x]) +
+                         pbb[64 + threadIdx.x];
+  }
+  __syncthreads();  // lnp / pbwf / pbb are read before the first chunk barrier
 
   // this workgroup's tiles and chunk loads (only loads that will be consumed
   // are issued, so none is in flight when the workgroup ends)
@@ -393,9 +459,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += x[t][e];
       }
-      s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      const float mean = s * (1.0f / C);
+      const float mean = group_sum_fast(s) * (1.0f / C);
       float v = 0.f;
 #pragma unroll
       for (int t = 0; t < kC; ++t)
@@ -404,9 +468,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
           const float d = x[t][e] - mean;
           v += d * d;
         }
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      const float rstd = rsqrtf(v * (1.0f / C) + a.eps);
+      const float rstd = rsqrtf(group_sum_fast(v) * (1.0f / C) + a.eps);
 #pragma unroll
       for (int t = 0; t < kC; ++t) {
         float lw[8], lb[8];
@@ -489,26 +551,29 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
         for (int rb = 0; rb < kRB; ++rb) mma(acc[rb][cb], fo, hf[rb]);
       }
     }
-    // tile boundary: the next tile's rows and this tile's residual rows are
-    // loaded together (this wave's pending chunk loads are older, so they
-    // complete first), then the outputs are stored.  With float32 rows the
-    // registers do not hold both sets at once: the next rows are loaded after
-    // the stores.
+    // tile boundary.  The loads of the next tile's first two chunks (issued
+    // during this tile's last two chunks) are the only vector memory
+    // operations in flight: complete them here, before any row load, since
+    // the next tile's first chunks only wait on lgkmcnt and the barrier.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // Then one row block at a time: add the residual rows, store, load the
+    // next block's residual rows (their latency covered by the pair bias),
+    // form the pair bias from the stored values, and load the block's rows of
+    // the next tile into the slots its LayerNorm freed (their latency covered
+    // by the remaining blocks' epilogues).
     const int64_t next = tile + gridDim.x;
-    // residual rows one row block at a time; the first block's loads and the
-    // wait below also cover this wave's chunk loads for the next tile
     const int gb = lane_g();
+    Quad<ZT> res[NCB];
+    auto load_res = [&](int rb) {
+      const int64_t rr = min(row_of(tile, rb), a.rows - 1);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
+    };
+    if (a.add) load_res(0);
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
       const bool valid = row < a.rows;
-      Quad<ZT> res[NCB];
-      if (a.add) {
-        const int64_t rr = min(row, a.rows - 1);
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
-      }
-      if (rb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       if (a.add)
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
@@ -516,15 +581,15 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
           for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[cb].get(e);
       store_row_blocks<ZT>(a.out + row * C, a.out + (row ^ 1) * C, 0, acc[rb], valid,
                            (row ^ 1) < a.rows);
-    }
-    if (a.pb_out)
-#pragma unroll
-      for (int rb = 0; rb < kRB; ++rb) {
-        const int64_t row = row_of(tile, rb);
-        pair_bias_epilogue<ZT, bf16, kC>(a, acc[rb], row, row < a.rows, lnp + 2 * C, lnp + 3 * C,
-                                         pbw);
+      if (a.add && rb + 1 < kRB) load_res(rb + 1);
+      if (a.pb_out)
+        pair_bias_folded<ZT>(a, acc[rb], row, valid, pbwf, pbb);
+      {
+        // after the last tile this reads row rows - 1 again, unused
+        const int64_t nrow = min(row_of(next, rb), a.rows - 1);  // pad rows read a real row
+        xr[rb].load(a.x + nrow * C, lane_g());
       }
-    if (next < ntiles) load_rows(next);
+    }
   }
 }
 
