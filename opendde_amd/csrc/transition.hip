@@ -234,6 +234,13 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 // (4 slots; slot t of row r holds chunk t ^ ((r >> 2) & 3): the 16 rows of a
 // fragment read then cover 16 distinct (row position, slot) pairs of a
 // 256-byte bank period, free of bank conflicts).
+// The gate's exponent scale rides on the data: the LayerNorm output is
+// multiplied by -log2(e) (folded into its weight and bias), so GEMM1 yields
+// a'' = -log2(e) a and b'' = -log2(e) b; then
+// silu(a) b = (ln 2)^2 a'' b'' / (1 + 2^a''), and GEMM2's output is scaled
+// back by (ln 2)^2 in the epilogue's residual FMA.  This removes one multiply
+// per hidden unit from the gate.
+constexpr float kLn2Sq = 0.480453013918201424667f;  // (ln 2)^2 = 1 / log2(e)^2
 constexpr int kRB = 3;                   // 16-row blocks per wave
 constexpr int kTpRows = 64 * kRB;
 constexpr int kTpStages = 3;
@@ -348,8 +355,9 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   __shared__ __attribute__((aligned(16))) float pbb[16 + 64];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   for (int t = threadIdx.x; t < C; t += 256) {
-    lnp[t] = a.ln_w[t];
-    lnp[C + t] = a.ln_b[t];
+    // the LayerNorm output carries the factor -log2(e) (see the gate below)
+    lnp[t] = a.ln_w[t] * kNegLog2e;
+    lnp[C + t] = a.ln_b[t] * kNegLog2e;
   }
   if (a.pb_out) {
     // thread (w, g, r16) forms fragment slot set (t = w, g) of head r16:
@@ -539,7 +547,8 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) hf[rb].set(4 * hb + e, siluf_(sa[rb][e]) * sb[rb][e]);
+          for (int e = 0; e < 4; ++e)
+            hf[rb].set(4 * hb + e, (sa[rb][e] * sb[rb][e]) * sigmoid_nl2e(sa[rb][e]));
       }
       // GEMM2: W_o[c][h0 + 8g .. + 7] fragments (staged chunk g, swizzled by
       // (c >> 2) & 3), one 16-channel block at a time, all row blocks
@@ -574,11 +583,12 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
       const bool valid = row < a.rows;
-      if (a.add)
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
+      for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][cb][e] += res[cb].get(e);
+        for (int e = 0; e < 4; ++e)
+          acc[rb][cb][e] = a.add ? fmaf(kLn2Sq, acc[rb][cb][e], res[cb].get(e))
+                                 : kLn2Sq * acc[rb][cb][e];
       store_row_blocks<ZT>(a.out + row * C, a.out + (row ^ 1) * C, 0, acc[rb], valid,
                            (row ^ 1) < a.rows);
       if (a.add && rb + 1 < kRB) load_res(rb + 1);
