@@ -5,7 +5,8 @@
 * N=384 triangle attention (starting node, last 38 tokens padded), bf16 vs
   the fp32 CPU oracle on the same bf16-rounded input.
 * N=768 triangle multiplication, outgoing and incoming, bf16 vs the fp32 CPU
-  oracle.
+  oracle; N=1024 and 1200 (the large contraction tiles) vs the fp32 oracle
+  run on the GPU.
 * One block of the N=1024 trunk workload (51 random pads) in the bench's
   mode (fp32 residual, bf16 arithmetic) vs the oracle run in fp32 on the GPU
   (at this size the CPU oracle takes minutes); plus size-independent
@@ -19,7 +20,7 @@
 import pytest
 import torch
 
-from helpers import assert_bf16, assert_fp32, params_of, say
+from helpers import assert_bf16, assert_fp32, params_of, say, token_pair_mask
 from oracle import reference as ref
 from opendde_amd import _lib
 from opendde_amd import workload as wl
@@ -98,6 +99,27 @@ def test_triangle_multiplication_n768_bf16(outgoing):
 
 def _gpu_params(mod):
     return {k: v.detach().float() for k, v in mod.named_parameters()}
+
+
+@pytest.mark.parametrize("n", [1024, 1200])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_large_contraction_bf16(n, outgoing):
+    """Np = 1024 and 1280 (4 x 4 and 5 x 5 tiles of 256 x 256) take the large
+    contraction kernel; bf16 z against the fp32 oracle run on the GPU."""
+    gen = wl.generator(900 + n)
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = cls(128, 128)
+    wl.init_module_(mod, gen)
+    mod = mod.to(DEV)
+    zb = torch.randn(n, n, 128, generator=gen).to(torch.bfloat16).to(DEV)
+    mask = token_pair_mask(n, n // 20, seed=n, random=True).to(DEV)
+    say(f"    trimul n={n} bf16 outgoing={outgoing} (large contraction tiles)")
+    with torch.no_grad():
+        exp = ref.triangle_multiplication(zb.float(), mask, _gpu_params(mod), outgoing)
+        before = _lib.launch_count(_lib.K_TRIMUL_CONTRACT)
+        got = mod(zb, mask, triangle_multiplicative="hip")
+    assert _lib.launch_count(_lib.K_TRIMUL_CONTRACT) == before + 1
+    assert_bf16(got, exp, f"trimul n={n} bf16 outgoing={outgoing}")
 
 
 def test_trunk_block_n1024_bench_mode():
