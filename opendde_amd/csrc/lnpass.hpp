@@ -85,8 +85,11 @@ __global__ __launch_bounds__(256) void ln_view_bf16_kernel(const ZT* __restrict_
 
 // out[x * np + y][:] = LN(P[:][x][y]) for the channel-major P[CH][np][np]
 // (bf16): a workgroup transposes the 64-column block P[:, x, y0..y0+63]
-// through LDS, then 4 threads per column normalise its CH channels.  Grid
-// (np / 64, np).  Columns with x >= n or y >= n are written as zeros.
+// through LDS, then normalises its 64 rows in two passes of 32, 8 threads
+// per row: thread part p owns the 16-byte chunks p, p + 8, ... of the row, so
+// one store instruction writes 8 whole 128-byte lines.  Grid (np / 64, np).
+// Columns with x >= n or y >= n are written as zeros.  P is read once and the
+// rows are written once: both with the streaming policy.
 // In the transposed tile, row y keeps channel c at column
 // c ^ (8 * ((y >> 3) & 7)) (8-channel groups permuted by y / 8): the lanes of
 // one transposing store cover 8 channels at 8 rows y0 + 8k + e, which then
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
                                                                 const float* __restrict__ ln_b,
                                                                 float eps, bf16* __restrict__ out) {
   constexpr int LD = CH + 8;     // LDS row stride (elements) of the transposed tile
-  constexpr int Q = CH / 4;      // channels per thread in the LayerNorm pass
+  constexpr int CPT = CH / 64;   // 16-byte chunks per thread in the LayerNorm pass
   static_assert(CH % 64 == 0, "the column permutation stays within 64-channel groups");
   __shared__ __attribute__((aligned(16))) bf16 t[64 * LD];
   const int x = blockIdx.y, y0 = blockIdx.x * 64;
@@ -117,8 +120,10 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
     if (NU % 256 == 0 || u < NU) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint4 v = *reinterpret_cast<const uint4*>(src + (size_t)(c4 + i) * np * np + yy);
-        ld[k][i][0] = v.x; ld[k][i][1] = v.y; ld[k][i][2] = v.z; ld[k][i][3] = v.w;
+        const f32x4 v =
+            load_stream(reinterpret_cast<const f32x4*>(src + (size_t)(c4 + i) * np * np + yy));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ld[k][i][e] = __float_as_uint(v[e]);
       }
     }
   }
@@ -140,47 +145,56 @@ __global__ __launch_bounds__(256) void ln_transpose_bf16_kernel(const bf16* __re
     }
   }
   __syncthreads();
-  const int yl = threadIdx.x >> 2, part = threadIdx.x & 3;
-  const int y = y0 + yl;
-  const bool valid = x < n && y < n;
-  const bf16* row = t + yl * LD;
-  const int sw = 8 * ((yl >> 3) & 7);
-  float v[Q];
+  const int part = threadIdx.x & 7;
 #pragma unroll
-  for (int k = 0; k < Q / 8; ++k) {
-    const bf16x8 h = *reinterpret_cast<const bf16x8*>(row + ((part * Q + 8 * k) ^ sw));
+  for (int pass = 0; pass < 2; ++pass) {
+    const int yl = 32 * pass + (threadIdx.x >> 3);
+    const int y = y0 + yl;
+    const bool valid = x < n && y < n;
+    const bf16* row = t + yl * LD;
+    const int sw = 8 * ((yl >> 3) & 7);
+    float v[CPT][8];
+    float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[8 * k + e] = (float)h[e];
-  }
-  float s = 0.f;
+    for (int k = 0; k < CPT; ++k) {
+      const bf16x8 h = *reinterpret_cast<const bf16x8*>(row + ((8 * (8 * k + part)) ^ sw));
 #pragma unroll
-  for (int e = 0; e < Q; ++e) s += v[e];
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
-  const float mean = s * (1.0f / CH);
-  float q = 0.f;
+      for (int e = 0; e < 8; ++e) {
+        v[k][e] = (float)h[e];
+        s += v[k][e];
+      }
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    const float mean = s * (1.0f / CH);
+    float q = 0.f;
 #pragma unroll
-  for (int e = 0; e < Q; ++e) {
-    const float d = v[e] - mean;
-    q += d * d;
-  }
-  q += __shfl_xor(q, 1, 64);
-  q += __shfl_xor(q, 2, 64);
-  const float rstd = rsqrtf(q * (1.0f / CH) + eps);
-  bf16* dst = out + ((size_t)x * np + y) * CH + part * Q;
+    for (int k = 0; k < CPT; ++k)
 #pragma unroll
-  for (int k = 0; k < Q / 8; ++k) {
-    const int c0 = part * Q + 8 * k;  // LayerNorm parameters as 16-byte vectors
-    float lw[8], lb[8];
-    load4(ln_w + c0, lw);
-    load4(ln_w + c0 + 4, lw + 4);
-    load4(ln_b + c0, lb);
-    load4(ln_b + c0 + 4, lb + 4);
-    bf16x8 h;
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[k][e] - mean;
+        q += d * d;
+      }
+    q += __shfl_xor(q, 1, 64);
+    q += __shfl_xor(q, 2, 64);
+    q += __shfl_xor(q, 4, 64);
+    const float rstd = rsqrtf(q * (1.0f / CH) + eps);
+    bf16* dst = out + ((size_t)x * np + y) * CH;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      h[e] = (bf16)(valid ? (v[8 * k + e] - mean) * rstd * lw[e] + lb[e] : 0.f);
-    reinterpret_cast<bf16x8*>(dst)[k] = h;
+    for (int k = 0; k < CPT; ++k) {
+      const int c0 = 8 * (8 * k + part);  // LayerNorm parameters as 16-byte vectors
+      float lw[8], lb[8];
+      load4(ln_w + c0, lw);
+      load4(ln_w + c0 + 4, lw + 4);
+      load4(ln_b + c0, lb);
+      load4(ln_b + c0 + 4, lb + 4);
+      bf16x8 h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        h[e] = (bf16)(valid ? (v[k][e] - mean) * rstd * lw[e] + lb[e] : 0.f);
+      store_stream(reinterpret_cast<bf16x8*>(dst + c0), h);
+    }
   }
 }
 
