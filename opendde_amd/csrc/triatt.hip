@@ -1050,22 +1050,28 @@ __global__ __launch_bounds__(256) void triatt_core_exact_kernel(TriattCoreArgs<C
     for (int r = 0; r < R; ++r) {
       const CT* Vr = a.v + ((size_t)rr[r] * a.heads + h) * jp * 32;
       float sum[2] = {0.f, 0.f};
-      for (int k0 = 0; k0 < jp; k0 += 32) {
+      // eight key blocks' loads in flight at a time (walking the blocks one
+      // by one costs one load latency each); keys >= n are selected out
+      for (int k0 = 0; k0 < jp; k0 += 8 * 32) {
+        Frag<CT> vf[8][2];  // lane: channel half db, row r16; keys k0 + 32u + slot_key(g, e)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          Frag<CT> vf;  // lane: channel half db, row r16; keys k0 + slot_key(g, e)
-          vf.load(Vr + (size_t)(k0 >> 5) * 1024 + (db * 64 + l) * 8);
+        for (int u = 0; u < 8; ++u)
+          if (k0 + 32 * u < jp)
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (k0 + slot_key(g, e) < n) sum[db] += vf.get(e);
-        }
+            for (int db = 0; db < 2; ++db)
+              vf[u][db].load(Vr + (size_t)((k0 >> 5) + u) * 1024 + (db * 64 + l) * 8);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (k0 + 32 * u < jp)
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                sum[db] += k0 + 32 * u + slot_key(g, e) < n ? vf[u][db].get(e) : 0.f;
       }
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
-        float t = sum[db];
-        t += __shfl_xor(t, 16, 64);
-        t += __shfl_xor(t, 32, 64);
-        sum[db] = t;  // every lane with this r16 holds channel 16*db + r16
+        sum[db] = group_sum_fast(sum[db]);  // every lane with this r16: channel 16*db + r16
       }
       // accumulator layout: lane (g, r16) holds channels 16*db + 4g + e of query r16
 #pragma unroll
