@@ -601,6 +601,8 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       }
     }
   }
+  // the last tile's unused row loads complete before the wave ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // fp32 arithmetic (true fp32 products on v_mfma_f32_16x16x4_f32), any C in
