@@ -9,10 +9,11 @@
   run on the GPU.
 * One block of the N=1024 trunk workload (51 random pads) in the bench's
   mode (fp32 residual, bf16 arithmetic) vs the oracle run in fp32 on the GPU
-  (at this size the CPU oracle takes minutes); plus size-independent
-  properties: the ending node through swapped strides equals the starting
-  node on the transposed copy bit for bit, and repeated runs are bitwise
-  deterministic.
+  (at this size the CPU oracle takes minutes), and one block at the shipped
+  model's pair width (c_z 384, 12 heads, hidden 384) the same way; plus
+  size-independent properties: the ending node through swapped strides
+  equals the starting node on the transposed copy bit for bit, and repeated
+  runs are bitwise deterministic.
 * N=2048, 4 blocks, bf16: runs without running out of memory and stays
   finite (every block's parity is in test_gpu_trunk.py).
 """
@@ -140,6 +141,32 @@ def test_trunk_block_n1024_bench_mode():
     assert torch.equal(zg, zg2) and torch.equal(sg, sg2), "block is not deterministic"
     assert_bf16(zg - z, ze - z, "trunk block z update")
     assert_bf16(sg - s, se - s, "trunk block s update")
+
+
+def test_opendde_v1_width_block_n1024_bench_mode():
+    """One block at the shipped model's pair width (c_z 384, hidden_scale_up:
+    12 triangle heads, multiplication hidden 384) at N = 1024 with 51 random
+    pads, in the bench's mode: the wide kernels at their full size (256 x 256
+    gate tiles, the transposing LayerNorm at Np = 1024, the large contraction
+    tiles) against the oracle run in fp32 on the GPU."""
+    cfg = wl.PairConfig("opendde_v1_block_n1024", 1024, c_z=384, heads=12,
+                        c_hidden_mul=384, n_pad=51, random_pad=True, seed=3)
+    z, s, mask, gen = wl.make_inputs(cfg)
+    blk = PairformerBlock(n_heads=cfg.n_heads_single, c_z=cfg.c_z, c_s=cfg.c_s,
+                          hidden_scale_up=True)
+    wl.init_module_(blk, gen)
+    blk = blk.eval().to(DEV)
+    assert blk.tri_att_start.mha.no_heads == 12 and blk.tri_mul_out.c_hidden == 384
+    z, s, mask = z.to(DEV), s.to(DEV), mask.to(DEV)
+    say(f"    v1-width block n={cfg.n} c_z={cfg.c_z} pads={cfg.n_pad}")
+    with torch.no_grad():
+        se, ze = ref.pairformer_block(s, z, mask, _gpu_params(blk), no_heads_pair=12,
+                                      n_heads=cfg.n_heads_single, chunk_size=32)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            sg, zg = blk(s, z.clone(), mask, triangle_multiplicative="hip",
+                         triangle_attention="hip", inplace_safe=True)
+    assert_bf16(zg - z, ze - z, "v1-width block z update")
+    assert_bf16(sg - s, se - s, "v1-width block s update")
 
 
 def test_ending_node_strides_equal_transposed_starting_node_n1024():
