@@ -342,7 +342,9 @@ template <> struct Quad<bf16> {
   __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
 };
 
-template <typename ZT>
+// kAdd / kPb: the residual add and the pair-bias epilogue, fixed per
+// instantiation so that each form's epilogue is straight-line code
+template <typename ZT, bool kAdd, bool kPb>
 __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<ZT, bf16> a,
                                                                  int64_t ntiles) {
   constexpr int C = 128, kC = 4, HID = 512, NCB = C / 16, NCHUNK = HID / kTrHid;
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     lnp[t] = a.ln_w[t] * kNegLog2e;
     lnp[C + t] = a.ln_b[t] * kNegLog2e;
   }
-  if (a.pb_out) {
+  if (kPb) {
     // thread (w, g, r16) forms fragment slot set (t = w, g) of head r16:
     // W'[r16][c] = W[r16][c] ln_w[c] for c = 32w + 16 (e >> 2) + 4g + (e & 3),
     // and its part of b[r16] = sum_c W[r16][c] ln_b[c]; the parts are summed
@@ -578,7 +580,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
     };
-    if (a.add) load_res(0);
+    if (kAdd) load_res(0);
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
@@ -587,12 +589,12 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          acc[rb][cb][e] = a.add ? fmaf(kLn2Sq, acc[rb][cb][e], res[cb].get(e))
+          acc[rb][cb][e] = kAdd ? fmaf(kLn2Sq, acc[rb][cb][e], res[cb].get(e))
                                  : kLn2Sq * acc[rb][cb][e];
       store_row_blocks<ZT>(a.out + row * C, a.out + (row ^ 1) * C, 0, acc[rb], valid,
                            (row ^ 1) < a.rows);
-      if (a.add && rb + 1 < kRB) load_res(rb + 1);
-      if (a.pb_out)
+      if (kAdd && rb + 1 < kRB) load_res(rb + 1);
+      if (kPb)
         pair_bias_folded<ZT>(a, acc[rb], row, valid, pbwf, pbb);
       {
         // after the last tile this reads row rows - 1 again, unused
@@ -1020,7 +1022,19 @@ int run_transition(const odde_transition_args* a, hipStream_t st) {
   if (a->c == 128 && a->n_factor == 4) {
     const int64_t ntiles = (p.rows + kTpRows - 1) / kTpRows;
     const int grid = (int)std::min<int64_t>(ntiles, 2 * 256);
-    hipLaunchKernelGGL((transition_pipe_kernel<ZT>), dim3(grid), dim3(256), 0, st, p, ntiles);
+    const bool pb = p.pb_out != nullptr;
+    if (p.add && pb)
+      hipLaunchKernelGGL((transition_pipe_kernel<ZT, true, true>), dim3(grid), dim3(256), 0, st, p,
+                         ntiles);
+    else if (p.add)
+      hipLaunchKernelGGL((transition_pipe_kernel<ZT, true, false>), dim3(grid), dim3(256), 0, st,
+                         p, ntiles);
+    else if (pb)
+      hipLaunchKernelGGL((transition_pipe_kernel<ZT, false, true>), dim3(grid), dim3(256), 0, st,
+                         p, ntiles);
+    else
+      hipLaunchKernelGGL((transition_pipe_kernel<ZT, false, false>), dim3(grid), dim3(256), 0, st,
+                         p, ntiles);
   }
   else if (a->c == 64 && a->n_factor == 4) launch_tr<ZT, CT, 2, 4>(p, st);
   else if (a->c == 256 && a->n_factor == 4) launch_tr<ZT, CT, 8, 4>(p, st);
