@@ -152,8 +152,7 @@ __global__ __launch_bounds__(256 * BaSplit<D>::KS) void bias_attn_kernel(BiasAtt
         sv[r] = key < a.nk ? fmaf(bc[r], kLog2e, sacc[r]) : -INFINITY;
         bm = fmaxf(bm, sv[r]);
       }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      bm = group_max_fast(bm);
       const float mn = fmaxf(m, bm);  // finite: every 16-key step has a key
       const float scale = __builtin_amdgcn_exp2f(m - mn);  // 0 at the first step
       lsum *= scale;
@@ -176,8 +175,7 @@ __global__ __launch_bounds__(256 * BaSplit<D>::KS) void bias_attn_kernel(BiasAtt
         }
     }
   }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  lsum = group_sum_fast(lsum);
   if constexpr (KS > 1) {
     // merge the groups' partial softmaxes: groups 1.. leave (m, lsum, o) per
     // lane in LDS (the staging area, free once every group left its loop) and

@@ -312,7 +312,7 @@ __device__ __forceinline__ void ln_rows_to_frags(const ZT* row_ptr, bool valid,
     }
     for (int e = 0; e < 8; ++e) s += x[t][e];
   }
-  const float mean = group_sum(s) * (1.0f / C);
+  const float mean = group_sum_fast(s) * (1.0f / C);
   float q = 0.f;
 #pragma unroll
   for (int t = 0; t < kC; ++t)
@@ -320,7 +320,7 @@ __device__ __forceinline__ void ln_rows_to_frags(const ZT* row_ptr, bool valid,
       const float d = x[t][e] - mean;
       q += d * d;
     }
-  const float rstd = rsqrtf(group_sum(q) * (1.0f / C) + eps);
+  const float rstd = rsqrtf(group_sum_fast(q) * (1.0f / C) + eps);
 #pragma unroll
   for (int t = 0; t < kC; ++t) {
     float w[8], b[8];
