@@ -531,6 +531,10 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
       load_ab(0, 0);
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
+        // raised issue priority while this wave feeds the matrix pipe, so
+        // that with two waves per SIMD the MFMAs of one overlap the other's
+        // gate arithmetic instead of queueing behind it
+        __builtin_amdgcn_s_setprio(1);
         f32x4 sa[kRB], sb[kRB];
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb) sa[rb] = sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -546,6 +550,7 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
           }
           __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
