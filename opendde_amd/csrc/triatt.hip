@@ -956,6 +956,9 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
         }
         kpf.load(KPs + lr * 32 + 8 * g);
         f32x4 s[2][QB];
+        // raised issue priority while this wave issues QK^T: with two waves
+        // per SIMD, its MFMAs go ahead of the other wave's exponentials
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -963,6 +966,7 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
             s[kb][qb] = bfr[kb][qb];
             mma(s[kb][qb], kf[kb], qf[r][qb]);
           }
+        __builtin_amdgcn_s_setprio(0);
         Frag<CT> pf[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
