@@ -21,8 +21,9 @@ workload on this host (median of 5).  ``configs`` holds the other workloads
 the path is specified on, each timed on the GPU (median of per-iteration HIP
 events) and, for the first three and one block of the trunk, on the CPU
 oracle (median of 5 runs after 1 warm-up): the N=128 block in fp32, N=384
-triangle attention, N=768 triangle multiplication (both directions), the
-N=2048 x 4-block stress stack.  ``machine`` holds the MFMA rates and HBM copy
+triangle attention, N=768 triangle multiplication (both directions), one
+N=1024 block of the trunk workload in fp32 arithmetic, the N=2048 x 4-block
+stress stack with the single track.  ``machine`` holds the MFMA rates and HBM copy
 bandwidth measured on this GPU next to the data sheet's.  ``layer_norm``
 times the standalone fast LayerNorm (forward and backward) on the workload's
 pair tensor shape, N*N x 128 bf16, outside the trunk step.
@@ -185,21 +186,23 @@ def probe_machine(dev):
     """Sustained MFMA rates (bf16 16x16x32, f32 16x16x4; 2 workgroups of 4
     waves per CU, 8 independent chains per wave), the attention core's
     instruction mix as a ceiling (odde_probe_mix) and HBM bandwidth on this
-    GPU: the library's streaming probe over 2 GiB (read; copy and in-place
-    rewrite, bytes read + written) and torch's device copy beside it."""
-    lib = _lib.load()
+    GPU: the streaming probe over 2 GiB (read; copy and in-place rewrite,
+    bytes read + written) and torch's device copy beside it.  The probes live
+    in the measurement library (opendde_amd.probe), not the product library;
+    each is timed with events on the stream it launches on."""
+    from opendde_amd import probe as pr
+    lib = pr.load()
     sink = torch.zeros(256, device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     out = {"cus": cus}
-    for name, code, iters in (("bf16", _lib.BF16, 4000), ("f32", _lib.F32, 1000)):
+    for name, code, iters in (("bf16", pr.BF16, 4000), ("f32", pr.F32, 1000)):
         fl = ctypes.c_double(0.0)
-        call = lambda it: _lib.check(lib.odde_probe_mfma(code, it, 2 * cus,  # noqa: E731
-                                                         ctypes.c_void_p(sink.data_ptr()),
-                                                         ctypes.byref(fl), stream),
-                                     "odde_probe_mfma")
-        call(100)
-        ms = kernel_avg_ms(lambda: call(iters), _lib.K_PROBE, reps=3)
+        call = lambda it: pr.check(lib.odde_probe_mfma(code, it, 2 * cus,  # noqa: E731
+                                                       ctypes.c_void_p(sink.data_ptr()),
+                                                       ctypes.byref(fl), stream),
+                                   "odde_probe_mfma")
+        ms = gpu_median_ms(lambda: call(iters), warm=1, iters=3)
         out[f"mfma_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
     out["mfma_bf16_tflops_spec"] = PEAK_BF16_TFLOPS
     out["mfma_f32_tflops_spec"] = PEAK_F32_TFLOPS
@@ -208,31 +211,79 @@ def probe_machine(dev):
     # the MFMA and exponential parts alone
     for name, parts in (("mfma_only", 1), ("exp_only", 2), ("mix", 3)):
         fl = ctypes.c_double(0.0)
-        call = lambda it: _lib.check(lib.odde_probe_mix(parts, it, 2 * cus,  # noqa: E731
-                                                        ctypes.c_void_p(sink.data_ptr()),
-                                                        ctypes.byref(fl), stream),
-                                     "odde_probe_mix")
-        call(50)
-        ms = kernel_avg_ms(lambda: call(2000), _lib.K_PROBE, reps=3)
+        call = lambda it: pr.check(lib.odde_probe_mix(parts, it, 2 * cus,  # noqa: E731
+                                                      ctypes.c_void_p(sink.data_ptr()),
+                                                      ctypes.byref(fl), stream),
+                                   "odde_probe_mix")
+        ms = gpu_median_ms(lambda: call(2000), warm=1, iters=3)
         out[f"core_mix_{name}_tflops"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
     src = torch.zeros(1 << 29, device=dev)
     dst = torch.zeros_like(src)
     nbytes = src.numel() * 4
-    # the library's streaming probe (non-temporal loads and stores, as the
-    # row-tile kernels stream pair data): read, copy, in-place rewrite
+    # the streaming probe (non-temporal loads and stores, as the row-tile
+    # kernels stream pair data): read, copy, in-place rewrite
     for name, mode, traffic in (("read", 0, nbytes), ("copy", 1, 2 * nbytes),
                                 ("inplace", 2, 2 * nbytes)):
-        call = lambda m=mode: _lib.check(lib.odde_probe_stream(  # noqa: E731
+        call = lambda m=mode: pr.check(lib.odde_probe_stream(  # noqa: E731
             m, ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes, stream),
             "odde_probe_stream")
-        call()
-        ms = kernel_avg_ms(call, _lib.K_PROBE, reps=5)
+        ms = gpu_median_ms(call, warm=1, iters=5)
         out[f"hbm_{name}_gbs"] = round(traffic / (ms * 1e-3) / 1e9, 1)
     # torch's device copy of the same 2 GiB, for comparison
     ms = gpu_median_ms(lambda: dst.copy_(src), warm=2, iters=5)
     out["hbm_torch_copy_gbs"] = round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
     out["hbm_gbs_spec"] = PEAK_HBM_GBS
     del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
+def fp32_block_leg(dev):
+    """fp32 arithmetic at the trunk's size: one block of the N=1024 workload
+    (51 random pads, c_s 384) with fp32 z and no autocast, in place -- the
+    reference's default inference precision.  GPU time (median of per-step
+    events) and the per-kernel launch times of one further step."""
+    cfg = wl.TRUNK_N1024
+    z, s, mask, gen = wl.make_inputs(cfg)
+    blk = PairformerBlock(n_heads=16, c_z=128, c_s=384)
+    wl.init_module_(blk, gen)
+    blk = blk.eval().to(dev)
+    z0, sg, mg = z.to(dev), s.to(dev), mask.to(dev)
+    zw = torch.empty_like(z0)
+
+    def fp32_block():
+        zw.copy_(z0)
+        with torch.no_grad():
+            blk(sg, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
+                inplace_safe=True)
+
+    ms = gpu_median_ms(fp32_block, warm=2, iters=5)
+    f = flops(cfg.n)["block"]
+    t = f / (ms * 1e-3) / 1e12
+    per_kernel = {}
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    fp32_block()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    fk = flops(cfg.n)
+    for kid, name in _lib.KERNEL_NAMES.items():
+        tot, cnt = _lib.timing_query(kid)
+        if cnt:
+            ent = {"launches": cnt, "avg_ms": round(tot / cnt, 4)}
+            fl = {"triatt_core": fk["core"], "trimul_contract": fk["contract"]}.get(name)
+            if fl:
+                kt = fl / (tot / cnt * 1e-3) / 1e12
+                ent.update(tflops=round(kt, 2), pct_f32_peak=round(100 * kt / PEAK_F32_TFLOPS, 2))
+            per_kernel[name] = ent
+    _lib.timing_reset()
+    out = dict(
+        gpu_ms=round(ms, 3), gflop=round(f / 1e9, 1), tflops=round(t, 2),
+        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2), dtype="fp32", residual_dtype="fp32",
+        pad_tokens=cfg.n_pad, kernels=per_kernel)
+    log(f"bench: fp32 block n=1024 {ms:.2f} ms")
+    del blk, z0, zw, sg, mg
     torch.cuda.empty_cache()
     return out
 
@@ -344,19 +395,22 @@ def config_legs(dev, with_cpu: bool):
     del mo, mi, zg, mg
     torch.cuda.empty_cache()
 
-    # cfg5: N=2048, 4 blocks (no single track), bench mode, peak memory
+    res["fp32_block_n1024"] = fp32_block_leg(dev)
+
+    # cfg5: N=2048, 4 blocks with the single track (c_s 384), bench mode,
+    # peak memory
     cfg = wl.STRESS_N2048
-    z, _, mask, gen = wl.make_inputs(cfg)
-    stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=16, c_z=cfg.c_z, c_s=0)
+    z, s, mask, gen = wl.make_inputs(cfg)
+    stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=16, c_z=cfg.c_z, c_s=cfg.c_s)
     wl.init_module_(stack, gen)
     stack = stack.eval().to(dev)
-    z0, mg = z.to(dev), mask.to(dev)
+    z0, s0, mg = z.to(dev), s.to(dev), mask.to(dev)
     zw = torch.empty_like(z0)
 
     def stress():
         zw.copy_(z0)
         with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
-            stack(None, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
+            stack(s0, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
                   inplace_safe=True)
 
     torch.cuda.synchronize()
@@ -364,7 +418,7 @@ def config_legs(dev, with_cpu: bool):
     base = torch.cuda.memory_allocated(dev)
     ms = gpu_median_ms(stress, warm=1, iters=3)
     peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
-    fb = flops(cfg.n, c_s=0)
+    fb = flops(cfg.n, c_s=cfg.c_s)
     f = cfg.n_blocks * fb["block"]
     t = f / (ms * 1e-3) / 1e12
     res["cfg5_stress_4x_n2048_bf16"] = dict(
@@ -372,9 +426,9 @@ def config_legs(dev, with_cpu: bool):
         tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
         peak_gib_above_inputs=round(peak, 2), total_gib_in_use=round(
             torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2), dtype="bf16",
-        residual_dtype="fp32")
+        residual_dtype="fp32", c_s=cfg.c_s)
     log(f"bench: cfg5 stress n=2048 x4 {ms:.1f} ms, peak {peak:.1f} GiB")
-    del stack, z0, zw, mg
+    del stack, z0, s0, zw, mg
     torch.cuda.empty_cache()
     return res
 
@@ -525,6 +579,9 @@ def main():
                     help="trunk: c_z 128, 4 triangle heads, hidden 128 (the benchmark "
                          "configuration); opendde_v1: the shipped model's pair width, c_z 384 "
                          "with hidden_scale_up (12 heads, hidden 384)")
+    ap.add_argument("--fp32-block", action="store_true",
+                    help="run only the fp32-arithmetic N=1024 block leg and print its JSON "
+                         "(for kernel traces of that leg)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "
                          "size, then one trunk step over a single block; prints nothing else")
@@ -536,6 +593,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.fp32_block:
+        print(json.dumps({"fp32_block_n1024": fp32_block_leg(dev)}), flush=True)
+        return
     v1 = args.preset == "opendde_v1"
     c_z, heads, ch = (384, 12, 384) if v1 else (128, 4, 128)
     cfg = wl.PairConfig("trunk", args.n, c_z=c_z, n_blocks=args.blocks,

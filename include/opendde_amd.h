@@ -51,8 +51,7 @@ extern "C" {
 #define ODDE_K_LAYER_NORM_BWD 9
 #define ODDE_K_OPM 10
 #define ODDE_K_BIAS_ATTN 11
-#define ODDE_K_PROBE 12
-#define ODDE_K_COUNT 13
+#define ODDE_K_COUNT 12
 
 int odde_abi_version(void);
 const char* odde_last_error(void);
@@ -406,37 +405,6 @@ int64_t odde_launch_count(int kernel_id);
 int odde_timing_enable(int on);
 int odde_timing_reset(void);
 int odde_timing_query(int kernel_id, double* total_ms, int64_t* launches);
-
-/* Machine-rate probe (no counterpart in the reference): launches `grid`
- * workgroups of 4 waves that each run 8 independent MFMA accumulator chains
- * of `iters` instructions (dtype ODDE_BF16: v_mfma_f32_16x16x32_bf16;
- * ODDE_F32: v_mfma_f32_16x16x4_f32) and returns the flops it performs in
- * *flops; time it with odde_timing_* (kernel id ODDE_K_PROBE) to get the
- * sustained MFMA rate.  `sink`: 256 floats of device memory (practically
- * never written). */
-int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flops,
-                    void* hip_stream);
-
-/* Co-issue probe (no counterpart in the reference): the triangle-attention
- * core's per-key-block instruction mix at its tile -- 40 MFMA 16x16x32 bf16,
- * 64 v_exp_f32, 32 v_cvt_pk_bf16_f32 per iteration, no memory traffic -- on
- * `grid` workgroups of 4 waves.  parts: 1 = the MFMAs alone, 2 = the
- * exponentials alone, 3 = the whole mix.  *flops: the attention flops the
- * iterations stand for (QK^T and PV of 2 rows x 64 queries x 32 keys x head
- * dim 32 per wave and iteration), so flops / time is the core's ceiling on
- * this GPU.  Timed like odde_probe_mfma (kernel id ODDE_K_PROBE). */
-int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
-                   void* hip_stream);
-
-/* Streaming-bandwidth probe (no counterpart in the reference): the HBM rate a
- * kernel that touches its data once can reach with the non-temporal cache
- * policy the row-tile kernels use.  mode 0 reads `bytes` of src (dst: at
- * least 256 floats, practically never written); mode 1 copies src to dst;
- * mode 2 rewrites dst in place with its own contents (src unused).  bytes: a
- * positive multiple of 16; 16-byte aligned buffers.  Time it with
- * odde_timing_* (kernel id ODDE_K_PROBE); the traffic is `bytes` for mode 0
- * and 2 * bytes otherwise. */
-int odde_probe_stream(int mode, const void* src, void* dst, uint64_t bytes, void* hip_stream);
 
 #ifdef __cplusplus
 }

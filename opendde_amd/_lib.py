@@ -28,13 +28,12 @@ K_TRANSITION = 7
 K_LAYER_NORM, K_LAYER_NORM_BWD = 8, 9
 K_OPM = 10
 K_BIAS_ATTN = 11
-K_PROBE = 12
 KERNEL_NAMES = {
     K_TRIATT_PROJ: "triatt_proj", K_TRIATT_CORE: "triatt_core", K_TRIATT_OUT: "triatt_out",
     K_TRIMUL_PROJ: "trimul_proj", K_TRIMUL_CONTRACT: "trimul_contract",
     K_TRIMUL_OUT: "trimul_out", K_TRIATT_RELAYOUT: "triatt_relayout",
     K_TRANSITION: "transition", K_LAYER_NORM: "layer_norm", K_LAYER_NORM_BWD: "layer_norm_bwd",
-    K_OPM: "outer_product_mean", K_BIAS_ATTN: "bias_attn", K_PROBE: "probe",
+    K_OPM: "outer_product_mean", K_BIAS_ATTN: "bias_attn",
 }
 
 _i32, _i64, _u32, _u64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
@@ -162,9 +161,6 @@ SYMBOLS = {
     "odde_timing_enable": (_i32, [_i32]),
     "odde_timing_reset": (_i32, []),
     "odde_timing_query": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
-    "odde_probe_mfma": (_i32, [_i32, _i64, _i32, _vp, ctypes.POINTER(ctypes.c_double), _vp]),
-    "odde_probe_mix": (_i32, [_i32, _i64, _i32, _vp, ctypes.POINTER(ctypes.c_double), _vp]),
-    "odde_probe_stream": (_i32, [_i32, _vp, _vp, _u64, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -2,7 +2,9 @@
 
 Compiles every ``csrc/*.hip`` with ``hipcc --offload-arch=gfx950`` (in
 parallel, one process per source), then links one shared library with a pure
-C ABI (``include/opendde_amd.h``).  Packed-FP32 instruction selection is
+C ABI (``include/opendde_amd.h``).  The machine-rate probes the benchmark
+reports (``csrc/probe/*.hip``) link into a library of their own,
+``lib/libopendde_amd_probe.so`` (``include/opendde_amd_probe.h``).  Packed-FP32 instruction selection is
 disabled for device code.  Run ``python -m opendde_amd.build``.
 """
 
@@ -18,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 LIBNAME = "libopendde_amd.so"
+PROBE_LIBNAME = "libopendde_amd_probe.so"
 ARCH = "gfx950"
 
 DEVICE_FLAGS = [
@@ -65,15 +68,13 @@ def _compile(src: str, objdir: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile and link; returns the library path.  Always rebuilds."""
-    objdir = os.path.join(HERE, "_build")
-    os.makedirs(objdir, exist_ok=True)
-    os.makedirs(LIBDIR, exist_ok=True)
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, objdir, verbose), srcs))
-    out = os.path.join(LIBDIR, LIBNAME)
+def probe_sources():
+    d = os.path.join(CSRC, "probe")
+    return sorted(os.path.join(d, f) for f in os.listdir(d) if f.endswith(".hip"))
+
+
+def _link(objs, name: str, verbose: bool) -> str:
+    out = os.path.join(LIBDIR, name)
     tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
@@ -83,6 +84,21 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, out)
     return out
+
+
+def build(verbose: bool = False) -> str:
+    """Compile and link the product library and, apart from it, the
+    measurement library of machine-rate probes (``PROBE_LIBNAME``, used by
+    the benchmark only); returns the product library's path.  Always
+    rebuilds."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    os.makedirs(LIBDIR, exist_ok=True)
+    srcs, psrcs = sources(), probe_sources()
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(psrcs))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, objdir, verbose), srcs + psrcs))
+    _link(objs[len(srcs):], PROBE_LIBNAME, verbose)
+    return _link(objs[:len(srcs)], LIBNAME, verbose)
 
 
 if __name__ == "__main__":

@@ -1,12 +1,36 @@
-// Machine-rate probe: the MFMA throughput this GPU actually sustains, so that
-// kernel figures can be quoted against a measured peak as well as the data
-// sheet's.  Every wave runs 8 independent accumulator chains of one MFMA
-// shape for `iters` rounds; nothing is loaded, one conditional store per lane
-// keeps the results live.
-#include "common.hpp"
-#include "runtime.hpp"
+// Machine-rate probes, built into their own measurement library
+// (libopendde_amd_probe.so, declared in include/opendde_amd_probe.h), apart
+// from the product library: the MFMA throughput this GPU actually sustains,
+// the triangle-attention core's instruction mix with no memory traffic, and
+// the streaming HBM rate, so that kernel figures can be quoted against
+// measured peaks as well as the data sheet's.  The caller times a probe with
+// events on the stream it passes.
+#include <string>
+
+#include "../../../include/opendde_amd_probe.h"
+#include "../common.hpp"
 
 namespace odde {
+
+namespace {
+thread_local std::string g_probe_error;
+
+int probe_error(const char* msg) {
+  g_probe_error = msg;
+  return -1;
+}
+
+int probe_launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return 0;
+  g_probe_error = std::string(what) + ": " + hipGetErrorString(e);
+  return -2;
+}
+}  // namespace
+
+// MFMA rate: every wave runs 8 independent accumulator chains of one MFMA
+// shape for `iters` rounds; nothing is loaded, one conditional store per lane
+// keeps the results live.
 
 template <bool kBf16>
 __global__ __launch_bounds__(256) void mfma_probe_kernel(float* __restrict__ sink, int64_t iters) {
@@ -125,32 +149,32 @@ using namespace odde;
 
 extern "C" {
 
+const char* odde_probe_last_error(void) { return g_probe_error.c_str(); }
+
 int odde_probe_mfma(int dtype, int64_t iters, int grid, float* sink, double* flops,
                     void* stream) {
   if (!sink || !flops || iters <= 0 || grid <= 0)
-    return set_error(ODDE_EINVAL, "probe_mfma: bad argument");
-  if (dtype != ODDE_BF16 && dtype != ODDE_F32)
-    return set_error(ODDE_EINVAL, "probe_mfma: dtype must be ODDE_BF16 or ODDE_F32");
+    return probe_error("probe_mfma: bad argument");
+  if (dtype != ODDE_PROBE_BF16 && dtype != ODDE_PROBE_F32)
+    return probe_error("probe_mfma: dtype must be ODDE_PROBE_BF16 or ODDE_PROBE_F32");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LaunchScope ls(ODDE_K_PROBE, st);
   // flops per instruction: 2 * 16 * 16 * K (K = 32 bf16, 4 f32)
-  const double per = 2.0 * 16 * 16 * (dtype == ODDE_BF16 ? 32 : 4);
+  const double per = 2.0 * 16 * 16 * (dtype == ODDE_PROBE_BF16 ? 32 : 4);
   *flops = per * 8.0 * (double)iters * 4.0 * (double)grid;  // 8 chains, 4 waves per workgroup
-  if (dtype == ODDE_BF16)
+  if (dtype == ODDE_PROBE_BF16)
     hipLaunchKernelGGL(mfma_probe_kernel<true>, dim3(grid), dim3(256), 0, st, sink, iters);
   else
     hipLaunchKernelGGL(mfma_probe_kernel<false>, dim3(grid), dim3(256), 0, st, sink, iters);
-  return check_launch("probe_mfma");
+  return probe_launched("probe_mfma");
 }
 
 int odde_probe_stream(int mode, const void* src, void* dst, uint64_t bytes, void* stream) {
-  if (mode < 0 || mode > 2) return set_error(ODDE_EINVAL, "probe_stream: mode must be 0, 1 or 2");
+  if (mode < 0 || mode > 2) return probe_error("probe_stream: mode must be 0, 1 or 2");
   if (!dst || (mode != 2 && !src) || bytes == 0 || bytes % 16 != 0)
-    return set_error(ODDE_EINVAL, "probe_stream: bad argument (bytes: a positive multiple of 16)");
+    return probe_error("probe_stream: bad argument (bytes: a positive multiple of 16)");
   if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0)
-    return set_error(ODDE_EINVAL, "probe_stream: buffers must be 16-byte aligned");
+    return probe_error("probe_stream: buffers must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LaunchScope ls(ODDE_K_PROBE, st);
   const uint64_t n16 = bytes / 16;
   const uint64_t want = (n16 + 1023) / 1024;  // 4 chunks per thread per trip
   const int grid = (int)(want < 8192 ? want : 8192);
@@ -161,16 +185,15 @@ int odde_probe_stream(int mode, const void* src, void* dst, uint64_t bytes, void
     case 1: hipLaunchKernelGGL(stream_probe_kernel<1>, dim3(grid), dim3(256), 0, st, s4, d4, n16); break;
     default: hipLaunchKernelGGL(stream_probe_kernel<2>, dim3(grid), dim3(256), 0, st, s4, d4, n16);
   }
-  return check_launch("probe_stream");
+  return probe_launched("probe_stream");
 }
 
 int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flops,
                    void* stream) {
   if (!sink || !flops || iters <= 0 || grid <= 0)
-    return set_error(ODDE_EINVAL, "probe_mix: bad argument");
-  if (parts < 1 || parts > 3) return set_error(ODDE_EINVAL, "probe_mix: parts must be 1, 2 or 3");
+    return probe_error("probe_mix: bad argument");
+  if (parts < 1 || parts > 3) return probe_error("probe_mix: parts must be 1, 2 or 3");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LaunchScope ls(ODDE_K_PROBE, st);
   // the attention flops one iteration stands for: QK^T and PV of 2 rows x 64
   // queries x 32 keys x head dim 32 (2 * 2 * 2 * 64 * 32 * 32), per wave
   *flops = 524288.0 * (double)iters * 4.0 * (double)grid;
@@ -179,7 +202,7 @@ int odde_probe_mix(int parts, int64_t iters, int grid, float* sink, double* flop
     case 2: hipLaunchKernelGGL(mix_probe_kernel<2>, dim3(grid), dim3(256), 0, st, sink, iters); break;
     default: hipLaunchKernelGGL(mix_probe_kernel<3>, dim3(grid), dim3(256), 0, st, sink, iters);
   }
-  return check_launch("probe_mix");
+  return probe_launched("probe_mix");
 }
 
 }  // extern "C"

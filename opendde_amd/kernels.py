@@ -66,6 +66,24 @@ def _pair_view_ok(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be square in its pair dims")
 
 
+def pair_layout_ok(t: torch.Tensor) -> bool:
+    """The kernels can read (and write) ``t`` [*, N, N, C] in place through
+    its strides: unit channel stride, leading dims that collapse to one batch
+    stride by a view, and 16-byte aligned rows (base address and the row,
+    column and batch strides)."""
+    if t.dim() < 3 or t.stride(-1) != 1:
+        return False
+    if t.numel() == 0:
+        return True
+    try:
+        v = t.view((-1,) + tuple(t.shape[-3:]))
+    except RuntimeError:
+        return False
+    es = t.element_size()
+    strides = (v.stride(0) if v.shape[0] > 1 else 0, v.stride(1), v.stride(2))
+    return t.data_ptr() % 16 == 0 and all((st * es) % 16 == 0 for st in strides)
+
+
 def _batch_view(t: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
     """``t`` [*, N, N, C] as a [B, N, N, C] view (never a copy: ``out`` is
     written through it) with B and the batch stride in elements."""
@@ -83,8 +101,16 @@ def _batch_view(t: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
 
 # Converted weights are cached per source tensor *object* (held by weak
 # reference, so a freed parameter whose device address is reused by a new one
-# can never hit) and its version counter (in-place updates invalidate).
+# can never hit) and its version counter (in-place updates invalidate).  An
+# entry is dropped as soon as one of its source tensors is freed, so the
+# converted copies of a discarded model release their device memory with it.
 _wcache: Dict[Tuple, Tuple] = {}
+
+
+def _evict(key, ref) -> None:
+    ent = _wcache.get(key)
+    if ent is not None and any(r is ref for r in ent[0]):
+        del _wcache[key]
 
 
 def _cached(key, srcs, make):
@@ -93,11 +119,15 @@ def _cached(key, srcs, make):
         refs, versions, val = ent
         if all(r() is s for r, s in zip(refs, srcs)) and versions == tuple(s._version for s in srcs):
             return val
-    if len(_wcache) > 4096:
-        _wcache.clear()
     val = make()
-    _wcache[key] = (tuple(weakref.ref(s) for s in srcs), tuple(s._version for s in srcs), val)
+    refs = tuple(weakref.ref(s, lambda r, k=key: _evict(k, r)) for s in srcs)
+    _wcache[key] = (refs, tuple(s._version for s in srcs), val)
     return val
+
+
+def cache_size() -> int:
+    """Number of converted-weight entries held (for tests)."""
+    return len(_wcache)
 
 
 def prepared(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:

@@ -154,15 +154,22 @@ class Linear(nn.Linear):
             with torch.amp.autocast("cuda", enabled=False):
                 b = self.bias.to(self.precision) if self.bias is not None else None
                 return F.linear(x.to(self.precision), self.weight.to(self.precision), b).to(d)
-        if x.is_cuda and _bf16_autocast(x):
+        if x.is_cuda and _bf16_autocast(x) and not self._needs_grad():
             # what bf16 autocast does for F.linear (input, weight and bias in
             # bf16, bf16 result), with the weight and bias cast once per
-            # version instead of on every call
+            # version instead of on every call; the cached copies are
+            # detached, so a call that trains the parameters takes F.linear
+            # under autocast below
             bf = torch.bfloat16
             with torch.amp.autocast("cuda", enabled=False):
                 b = prepared(self.bias, bf) if self.bias is not None else None
                 return F.linear(x.to(bf), prepared(self.weight, bf), b)
         return F.linear(x, self.weight, self.bias)
+
+    def _needs_grad(self) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return self.weight.requires_grad or (self.bias is not None and self.bias.requires_grad)
 
 
 LinearNoBias = partial(Linear, bias=False)

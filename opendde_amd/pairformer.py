@@ -270,6 +270,10 @@ class PairformerBlock(nn.Module):
         # shapes or dtypes the kernels do not cover run the torch path
         hip_mul = hip_mul and _hip_covers(self.tri_mul_out, z, "TriangleMultiplicativeUpdate")
         hip_att = hip_att and _hip_covers(self.tri_att_start, z, "TriangleAttention")
+        if (hip_mul or hip_att) and not K.pair_layout_ok(z):
+            # the kernels read z through its strides; a layout they cannot
+            # (uncollapsible leading dims, unaligned rows) runs on a copy
+            z = z.contiguous()
 
         # triangle multiplications: z + update, in place when allowed
         for mod in (self.tri_mul_out, self.tri_mul_in):

@@ -51,19 +51,21 @@ def kernel_triangular_mult(x, direction, mask, norm_in_weight, norm_in_bias, p_i
     [..., N, N, C], mask [..., N, N]; returns the update (no residual)."""
     if direction not in ("outgoing", "incoming"):
         raise ValueError(f"direction must be 'outgoing' or 'incoming', got {direction}")
-    lead = x.shape[:-3]
-    xs = x.reshape((-1,) + tuple(x.shape[-3:]))
-    ms = None if mask is None else mask.expand(lead + tuple(x.shape[-3:-1])).reshape(
-        (-1,) + tuple(x.shape[-3:-1]))
-    out = torch.empty_like(xs, memory_format=torch.contiguous_format)
-    for b in range(xs.shape[0]):
-        K.triangle_multiplication(
-            xs[b], None if ms is None else ms[b], outgoing=direction == "outgoing",
-            norm_in_weight=norm_in_weight, norm_in_bias=norm_in_bias,
-            p_in_weight=p_in_weight, g_in_weight=g_in_weight,
-            norm_out_weight=norm_out_weight, norm_out_bias=norm_out_bias,
-            p_out_weight=p_out_weight, g_out_weight=g_out_weight, out=out[b], eps=eps)
-    return out.reshape(x.shape)
+    # all leading views in one library call (batch strides), as the module
+    # path runs them
+    return K.triangle_multiplication(
+        hip_layout(x), mask, outgoing=direction == "outgoing",
+        norm_in_weight=norm_in_weight, norm_in_bias=norm_in_bias,
+        p_in_weight=p_in_weight, g_in_weight=g_in_weight,
+        norm_out_weight=norm_out_weight, norm_out_bias=norm_out_bias,
+        p_out_weight=p_out_weight, g_out_weight=g_out_weight, eps=eps)
+
+
+def hip_layout(z: torch.Tensor) -> torch.Tensor:
+    """``z`` itself when the kernels read it through its strides, else a
+    contiguous copy (leading dims that no view collapses, a non-unit channel
+    stride or unaligned rows)."""
+    return z if K.pair_layout_ok(z) else z.contiguous()
 
 
 # ---------------------------------------------------------------------------
@@ -218,7 +220,7 @@ class TriangleAttention(nn.Module):
             if why is None:
                 # chunk_size only bounds memory in the torch path; the fused
                 # HIP path never materialises the logits.
-                return self.hip_apply(x, mask)
+                return self.hip_apply(hip_layout(x), mask)
             hook.note_fallback("TriangleAttention", why)
         if mask is None:
             mask = x.new_ones(x.shape[:-1])
@@ -301,10 +303,14 @@ class TriangleMultiplicativeUpdate(nn.Module):
         if _use_hip(triangle_multiplicative, z):
             why = self.hip_unsupported(z)
             if why is None:
+                zl = hip_layout(z)
                 if add:
                     # in-place inference form: z <- z + update, one fused pass
-                    return self.hip_apply(z, mask, out=z, add_residual=True)
-                return self.hip_apply(z, mask)
+                    if zl is z:
+                        return self.hip_apply(z, mask, out=z, add_residual=True)
+                    z.copy_(self.hip_apply(zl, mask, out=zl, add_residual=True))
+                    return z
+                return self.hip_apply(zl, mask)
             hook.note_fallback("TriangleMultiplicativeUpdate", why)
         if mask is None:
             mask = z.new_ones(z.shape[:-1])

@@ -176,7 +176,7 @@ TRIATT_N384 = PairConfig("triangle_attention_start_n384_bf16", 384, c_s=0,
 TRIMUL_N768 = PairConfig("triangle_multiplication_n768_bf16", 768, c_s=0, seed=2)
 TRUNK_N1024 = PairConfig("pairformer_trunk_48x_n1024_bf16", 1024, n_blocks=48,
                          n_pad=51, random_pad=True, seed=3)
-STRESS_N2048 = PairConfig("pairformer_4x_n2048_bf16", 2048, c_s=0, n_blocks=4, seed=4)
+STRESS_N2048 = PairConfig("pairformer_4x_n2048_bf16", 2048, n_blocks=4, seed=4)
 
 
 def make_inputs(cfg: PairConfig, with_s: Optional[bool] = None):

@@ -197,3 +197,18 @@ def test_noalloc_layer_norm_bwd_rejects_what_its_scratch_cannot_hold():
     a.struct_size = 8
     rc, msg = _status("odde_layer_norm_bwd_noalloc", a)
     assert rc == -1 and "struct_size" in msg
+
+
+def test_probe_library_is_separate_and_exports_its_header():
+    """The machine-rate probes live in the measurement library only: the
+    product library exports none of them."""
+    from opendde_amd import probe as pr
+    text = open(os.path.join(ROOT, "include", "opendde_amd_probe.h")).read()
+    declared = sorted(set(re.findall(r"\b(odde_probe_[a-z_0-9]+)\s*\(", text)))
+    assert set(declared) == set(pr.SYMBOLS)
+    plib = pr.load()
+    for name in declared:
+        assert hasattr(plib, name), f"missing export {name}"
+    lib = _lib.load()
+    for name in declared:
+        assert not hasattr(lib, name), f"{name} exported by the product library"

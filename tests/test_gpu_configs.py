@@ -14,8 +14,12 @@
   size-independent properties: the ending node through swapped strides
   equals the starting node on the transposed copy bit for bit, and repeated
   runs are bitwise deterministic.
-* N=2048, 4 blocks, bf16: runs without running out of memory and stays
-  finite (every block's parity is in test_gpu_trunk.py).
+* One block of the N=1024 trunk workload with fp32 arithmetic throughout
+  (the reference's default inference precision) vs the oracle run in fp32 on
+  the GPU: max-abs <= 1e-4 on the updates.
+* N=2048, 4 blocks with the single track (c_s 384), bf16: runs without
+  running out of memory and stays finite (every block's parity is in
+  test_gpu_trunk.py).
 """
 
 import pytest
@@ -143,6 +147,37 @@ def test_trunk_block_n1024_bench_mode():
     assert_bf16(sg - s, se - s, "trunk block s update")
 
 
+def test_trunk_block_n1024_fp32():
+    """One block of the benchmark workload (N=1024, 51 random pads, c_s 384)
+    with fp32 arithmetic throughout -- the reference's default inference
+    precision (opendde/config/model_base.py:36-37) -- in place, against the
+    oracle run in fp32 on the GPU (TF32 off): max-abs <= 1e-4 on the updates."""
+    old = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        cfg = wl.TRUNK_N1024
+        z, s, mask, gen = wl.make_inputs(cfg)
+        blk = _block(cfg, gen).to(DEV)
+        z, s, mask = z.to(DEV), s.to(DEV), mask.to(DEV)
+        say(f"    fp32 trunk block n={cfg.n} pads={cfg.n_pad}")
+        with torch.no_grad():
+            se, ze = ref.pairformer_block(s, z, mask, _gpu_params(blk), no_heads_pair=cfg.heads,
+                                          n_heads=cfg.n_heads_single, chunk_size=64)
+            counts = [_lib.launch_count(k) for k in (_lib.K_TRIATT_CORE, _lib.K_TRIMUL_CONTRACT,
+                                                     _lib.K_TRANSITION, _lib.K_BIAS_ATTN)]
+            sg, zg = blk(s, z.clone(), mask, triangle_multiplicative="hip",
+                         triangle_attention="hip", inplace_safe=True)
+            torch.cuda.synchronize()
+        after = [_lib.launch_count(k) for k in (_lib.K_TRIATT_CORE, _lib.K_TRIMUL_CONTRACT,
+                                                _lib.K_TRANSITION, _lib.K_BIAS_ATTN)]
+        assert [a - b for a, b in zip(after, counts)] == [2, 2, 2, 1]
+        assert zg.dtype == torch.float32
+        assert_fp32(zg - z, ze - z, "fp32 trunk block z update")
+        assert_fp32(sg - s, se - s, "fp32 trunk block s update")
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = old
+
+
 def test_opendde_v1_width_block_n1024_bench_mode():
     """One block at the shipped model's pair width (c_z 384, hidden_scale_up:
     12 triangle heads, multiplication hidden 384) at N = 1024 with 51 random
@@ -183,23 +218,28 @@ def test_ending_node_strides_equal_transposed_starting_node_n1024():
 
 
 def test_stress_n2048_four_blocks():
+    """N=2048 x 4 blocks with the single track (c_s 384): the pair-bias
+    epilogue and the single-track attention core at the bias's largest size
+    ([16, 2048, 2048] fp32)."""
     cfg = wl.STRESS_N2048
-    z, _, mask, gen = wl.make_inputs(cfg)
+    z, s, mask, gen = wl.make_inputs(cfg)
     stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=cfg.n_heads_single, c_z=cfg.c_z,
-                            c_s=0)
+                            c_s=cfg.c_s)
     wl.init_module_(stack, gen)
     stack = stack.eval().to(DEV)
-    z, mask = z.to(DEV), mask.to(DEV)
-    say(f"    stress n={cfg.n} blocks={cfg.n_blocks}")
+    z, s, mask = z.to(DEV), s.to(DEV), mask.to(DEV)
+    say(f"    stress n={cfg.n} blocks={cfg.n_blocks} c_s={cfg.c_s}")
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
+    before = _lib.launch_count(_lib.K_BIAS_ATTN)
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
-        _, zs = stack(None, z.clone(), mask, triangle_multiplicative="hip",
-                      triangle_attention="hip", inplace_safe=True)
+        ss, zs = stack(s, z.clone(), mask, triangle_multiplicative="hip",
+                       triangle_attention="hip", inplace_safe=True)
     torch.cuda.synchronize()
     peak = (torch.cuda.max_memory_allocated() - base) / 2 ** 30
     say(f"    n=2048 4 blocks: peak {peak:.1f} GiB above the inputs")
-    assert torch.isfinite(zs).all()
+    assert _lib.launch_count(_lib.K_BIAS_ATTN) == before + cfg.n_blocks
+    assert torch.isfinite(zs).all() and torch.isfinite(ss).all()
     assert peak < 32, f"peak memory {peak:.1f} GiB"
     # parity of all four blocks against the fp32 oracle: test_gpu_trunk.py

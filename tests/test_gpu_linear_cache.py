@@ -32,6 +32,32 @@ def test_linear_under_autocast_equals_autocast_linear(bias):
             lin.weight.mul_(1.5)  # a new version: the cached copy must not be reused
 
 
+@pytest.mark.parametrize("bias", [True, False])
+def test_linear_under_autocast_trains_its_parameters(bias):
+    """With gradients on, the cached (detached) casts must not be used: the
+    backward reaches weight and bias exactly as autocast's F.linear does."""
+    say(f"[gpu] linear backward under autocast bias={bias}")
+    lin = seeded((Linear if bias else LinearNoBias)(384, 256), 5).to(DEV)
+    x = torch.randn(512, 384, device=DEV, requires_grad=True)
+    gy = torch.randn(512, 256, device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = lin(x)
+    y.backward(gy.to(y.dtype))
+    assert lin.weight.grad is not None and x.grad is not None
+    if bias:
+        assert lin.bias.grad is not None
+    got = [lin.weight.grad.clone(), x.grad.clone()] + ([lin.bias.grad.clone()] if bias else [])
+    lin.zero_grad()
+    x.grad = None
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y2 = F.linear(x, lin.weight, lin.bias)
+    y2.backward(gy.to(y2.dtype))
+    exp = [lin.weight.grad, x.grad] + ([lin.bias.grad] if bias else [])
+    assert torch.equal(y, y2)
+    for g, e in zip(got, exp):
+        assert torch.equal(g, e)
+
+
 def test_single_attention_shared_cast_is_bit_identical():
     say("[gpu] single attention with one shared bf16 input cast")
     att = seeded(SingleAttention(384, 384, 384, 24, 16), 4).to(DEV)

@@ -1,6 +1,7 @@
-"""The machine-rate probes the bench reports (no counterpart in the
-reference): they launch, time through the library's events, and return the
-flop counts their documentation states."""
+"""The machine-rate probes the bench reports (measurement library
+libopendde_amd_probe.so, apart from the product library; no counterpart in
+the reference): they launch on the given stream, return the flop counts their
+documentation states, and reject bad arguments with a status and a message."""
 
 import ctypes
 
@@ -9,60 +10,75 @@ import torch
 
 from helpers import say
 from opendde_amd import _lib
+from opendde_amd import probe as pr
 
 pytestmark = pytest.mark.gpu
 
 
-def _timed(fn):
-    torch.cuda.synchronize()
-    _lib.timing_reset()
-    _lib.timing_enable(True)
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _timed_ms(fn):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
     fn()
+    e1.record()
     torch.cuda.synchronize()
-    _lib.timing_enable(False)
-    tot, cnt = _lib.timing_query(_lib.K_PROBE)
-    _lib.timing_reset()
-    return tot, cnt
+    return e0.elapsed_time(e1)
 
 
 @pytest.mark.parametrize("parts", [1, 2, 3])
 def test_mix_probe_runs_and_counts_attention_flops(parts):
     say(f"[gpu] mix probe parts={parts}")
-    lib = _lib.load()
+    lib = pr.load()
     sink = torch.zeros(256, device="cuda")
     fl = ctypes.c_double(0.0)
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    tot, cnt = _timed(lambda: _lib.check(lib.odde_probe_mix(parts, 20, 8, ctypes.c_void_p(
-        sink.data_ptr()), ctypes.byref(fl), stream), "odde_probe_mix"))
-    assert cnt == 1 and tot > 0
+    before = [_lib.launch_count(k) for k in _lib.KERNEL_NAMES]
+    ms = _timed_ms(lambda: pr.check(lib.odde_probe_mix(parts, 20, 8, ctypes.c_void_p(
+        sink.data_ptr()), ctypes.byref(fl), _stream()), "odde_probe_mix"))
+    assert ms > 0
     assert fl.value == 524288.0 * 20 * 4 * 8
-    assert float(sink.abs().sum()) == 0.0  # the sink is never written
+    # the product library is not involved
+    assert [_lib.launch_count(k) for k in _lib.KERNEL_NAMES] == before
+
+
+@pytest.mark.parametrize("code", [pr.BF16, pr.F32])
+def test_mfma_probe_counts_flops(code):
+    say(f"[gpu] mfma probe dtype={code}")
+    lib = pr.load()
+    sink = torch.zeros(256, device="cuda")
+    fl = ctypes.c_double(0.0)
+    ms = _timed_ms(lambda: pr.check(lib.odde_probe_mfma(code, 50, 4, ctypes.c_void_p(
+        sink.data_ptr()), ctypes.byref(fl), _stream()), "odde_probe_mfma"))
+    assert ms > 0
+    assert fl.value == 2.0 * 16 * 16 * (32 if code == pr.BF16 else 4) * 8 * 50 * 4 * 4
 
 
 def test_probes_reject_bad_arguments():
-    lib = _lib.load()
+    lib = pr.load()
     fl = ctypes.c_double(0.0)
     assert lib.odde_probe_mix(4, 10, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
+    assert b"parts" in lib.odde_probe_last_error()
     assert lib.odde_probe_mix(1, 0, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
     assert lib.odde_probe_mfma(7, 10, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
 
 
 def test_stream_probe_modes():
     """Mode 1 copies exactly, mode 2 leaves its buffer's bits unchanged, mode
-    0 reads without writing; each is one timed launch (ragged sizes cover the
-    bounds of the grid-stride loop)."""
-    lib = _lib.load()
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    0 reads without writing (ragged sizes cover the bounds of the grid-stride
+    loop; dst holds at least the 256 floats mode 0 may write)."""
+    lib = pr.load()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     for n in (4, 1000, (1 << 20) + 12):
         say(f"[gpu] stream probe n={n}")
         src = torch.randn(n, device="cuda")
         dst = torch.zeros(max(n, 256), device="cuda")
-        ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
         for mode in (0, 1, 2):
             before = dst.clone()
-            tot, cnt = _timed(lambda: _lib.check(lib.odde_probe_stream(
-                mode, ptr(src), ptr(dst), n * 4, stream), "odde_probe_stream"))
-            assert cnt == 1 and tot > 0
+            ms = _timed_ms(lambda: pr.check(lib.odde_probe_stream(
+                mode, ptr(src), ptr(dst), n * 4, _stream()), "odde_probe_stream"))
+            assert ms > 0
             if mode == 0:
                 assert torch.equal(dst, before)
             elif mode == 1:
@@ -72,11 +88,10 @@ def test_stream_probe_modes():
 
 
 def test_stream_probe_rejects_bad_arguments():
-    lib = _lib.load()
+    lib = pr.load()
     p = ctypes.c_void_p(0x1000)
     assert lib.odde_probe_stream(3, p, p, 64, None) == -1
     assert lib.odde_probe_stream(1, p, p, 63, None) == -1
     assert lib.odde_probe_stream(1, None, p, 64, None) == -1
     assert lib.odde_probe_stream(0, p, p, 0, None) == -1
     assert lib.odde_probe_stream(1, ctypes.c_void_p(0x1004), p, 64, None) == -1
-

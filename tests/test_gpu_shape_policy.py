@@ -20,14 +20,14 @@ from opendde_amd import workload as wl
 from opendde_amd.pairformer import PairformerBlock
 from opendde_amd.triangular import (Attention, TriangleAttention,
                                     TriangleMultiplicationIncoming,
-                                    TriangleMultiplicationOutgoing)
+                                    TriangleMultiplicationOutgoing, kernel_triangular_mult)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
 def _launches():
-    return [_lib.launch_count(k) for k in range(_lib.K_PROBE)]
+    return [_lib.launch_count(k) for k in _lib.KERNEL_NAMES]
 
 
 def _pair(n, c, dtype=torch.float32, seed=0, lead=()):
@@ -154,3 +154,50 @@ def test_batched_triangle_multiplication_is_one_call(monkeypatch, outgoing, dtyp
         assert len(calls) == 1
         assert torch.equal(got, per)
         assert math.isfinite(float(got.float().abs().max()))
+
+
+def test_permuted_batch_runs_on_a_copy(monkeypatch):
+    """Leading dims that no view collapses (a permuted 2-D batch): the modules
+    run the kernels on a contiguous copy (one library call) instead of
+    raising, and the in-place form writes the result back into z."""
+    n, c = 40, 128
+    att = seeded(TriangleAttention(c_in=c, c_hidden=32, no_heads=4), 14).to(DEV)
+    mul = seeded(TriangleMultiplicationOutgoing(c_z=c, c_hidden=128), 15).to(DEV)
+    base = _pair(n, c, seed=16, lead=(3, 2))
+    z = base.transpose(0, 1)  # [2, 3, N, N, C], not collapsible by a view
+    mask = token_pair_mask(n, 4).to(DEV)
+    say("[gpu] permuted 2-D batch")
+    with torch.no_grad():
+        exp_att = att.hip_apply(z.contiguous(), mask)
+        calls = _count_calls(monkeypatch, "odde_triatt_fwd")
+        got_att = att(z, mask=mask, triangle_attention="hip")
+        assert len(calls) == 1 and torch.equal(got_att, exp_att)
+        exp_mul = z.contiguous()
+        mul.hip_apply(exp_mul, mask, out=exp_mul, add_residual=True)
+        zi = z.clone().transpose(0, 1).contiguous().transpose(0, 1)  # same permuted layout
+        calls = _count_calls(monkeypatch, "odde_trimul_fwd")
+        got = mul(zi, mask=mask, inplace_safe=True, _add_with_inplace=True,
+                  triangle_multiplicative="hip")
+        assert len(calls) == 1 and got is zi and torch.equal(zi, exp_mul)
+
+
+def test_kernel_triangular_mult_slot_is_one_call(monkeypatch):
+    """The reference's function slot with leading dims: one library call with
+    batch strides, equal to the per-view calls bit for bit."""
+    n, c = 48, 128
+    mod = seeded(TriangleMultiplicationIncoming(c_z=c, c_hidden=128), 17).to(DEV)
+    x = _pair(n, c, torch.bfloat16, seed=18, lead=(2, 2))
+    mask = token_pair_mask(n, 6, seed=2, random=True).to(DEV, torch.bfloat16)
+    p_in = torch.cat([mod.linear_a_p.weight, mod.linear_b_p.weight]).bfloat16()
+    g_in = torch.cat([mod.linear_a_g.weight, mod.linear_b_g.weight]).bfloat16()
+    args = (mod.layer_norm_in.weight, mod.layer_norm_in.bias, p_in, g_in,
+            mod.layer_norm_out.weight, mod.layer_norm_out.bias, mod.linear_z.weight.bfloat16(),
+            mod.linear_g.weight.bfloat16(), 1e-5)
+    say("[gpu] kernel_triangular_mult slot, leading dims (2, 2)")
+    with torch.no_grad():
+        per = torch.stack([torch.stack([kernel_triangular_mult(x[a, b], "incoming", mask, *args)
+                                        for b in range(2)]) for a in range(2)])
+        calls = _count_calls(monkeypatch, "odde_trimul_fwd")
+        got = kernel_triangular_mult(x, "incoming", mask, *args)
+        assert len(calls) == 1
+        assert got.shape == x.shape and torch.equal(got, per)

@@ -8,8 +8,12 @@
   tolerance is the bf16 tier's, applied to the accumulated updates z - z0 and
   s - s0 after the last block: relative-L2 <= 1e-2 and max-abs <= 5e-2.
   The error of every block is logged, so growth over depth is visible.
-* The stress trunk: all 4 blocks at N=2048 (c_s 0, seed 4), same bar, plus
-  its peak memory.
+* The stress trunk: all 4 blocks at N=2048 (c_s 384, seed 4: the single
+  track's pair bias is [16, 2048, 2048] fp32, 256 MiB), same bar, plus its
+  peak memory.
+* The shipped model's pair width over depth: c_z 384 with hidden_scale_up
+  (12 triangle heads, multiplication hidden 384, c_s 384), 8 blocks at
+  N=1024 and 48 blocks at N=160, same bar, every block's error logged.
 
 Each trajectory runs block by block (the stack is exactly that loop, and
 ``test_stack_equals_block_loop`` checks it bit for bit); the oracle
@@ -50,8 +54,9 @@ def _err(got, exp):
 
 
 def _stack(cfg, gen):
+    v1 = cfg.c_z == 384
     stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=cfg.n_heads_single, c_z=cfg.c_z,
-                            c_s=cfg.c_s)
+                            c_s=cfg.c_s, hidden_scale_up=v1)
     wl.init_module_(stack, gen)
     return stack.eval().to(DEV)
 
@@ -100,11 +105,34 @@ def test_trunk_48_blocks_n1024_bench_mode_matches_fp32_oracle():
 @pytest.mark.timeout(600)
 def test_stress_4_blocks_n2048_matches_fp32_oracle():
     cfg = wl.STRESS_N2048
-    say(f"[gpu] stress {cfg.n_blocks} blocks n={cfg.n} vs fp32 GPU oracle")
-    (zh, _), (zr, _), z0, _ = _compare_trunks(cfg, chunk=32)
+    assert cfg.c_s == 384
+    say(f"[gpu] stress {cfg.n_blocks} blocks n={cfg.n} c_s={cfg.c_s} vs fp32 GPU oracle")
+    (zh, sh), (zr, sr), z0, s0 = _compare_trunks(cfg, chunk=32)
     rz, mz = _err(zh - z0, zr - z0)
-    say(f"    final z-z0 rel_l2={rz:.3e} max_abs={mz:.3e}")
+    rs, ms = _err(sh - s0, sr - s0)
+    say(f"    final z-z0 rel_l2={rz:.3e} max_abs={mz:.3e}; s-s0 rel_l2={rs:.3e} max_abs={ms:.3e}")
     assert rz <= BF16_REL_L2 and mz <= BF16_MAX_ABS, f"z: rel-L2 {rz:.3e}, max-abs {mz:.3e}"
+    assert rs <= BF16_REL_L2 and ms <= BF16_MAX_ABS, f"s: rel-L2 {rs:.3e}, max-abs {ms:.3e}"
+
+
+V1_STACK_N1024 = wl.PairConfig("opendde_v1_stack_8x_n1024", 1024, c_z=384, heads=12,
+                               c_hidden_mul=384, n_blocks=8, n_pad=51, random_pad=True, seed=3)
+V1_STACK_N160 = wl.PairConfig("opendde_v1_stack_48x_n160", 160, c_z=384, heads=12,
+                              c_hidden_mul=384, n_blocks=48, n_pad=8, random_pad=True, seed=5)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("cfg", [V1_STACK_N1024, V1_STACK_N160], ids=lambda c: c.name)
+def test_opendde_v1_width_stack_matches_fp32_oracle(cfg):
+    """The shipped model's pair width (opendde/config/model_base.py:19-30,
+    modules/pairformer.py:91-93) over depth, in the bench's mode."""
+    say(f"[gpu] v1-width stack {cfg.n_blocks} blocks n={cfg.n} c_z={cfg.c_z} vs fp32 GPU oracle")
+    (zh, sh), (zr, sr), z0, s0 = _compare_trunks(cfg, chunk=32)
+    rz, mz = _err(zh - z0, zr - z0)
+    rs, ms = _err(sh - s0, sr - s0)
+    say(f"    final z-z0 rel_l2={rz:.3e} max_abs={mz:.3e}; s-s0 rel_l2={rs:.3e} max_abs={ms:.3e}")
+    assert rz <= BF16_REL_L2 and mz <= BF16_MAX_ABS, f"z: rel-L2 {rz:.3e}, max-abs {mz:.3e}"
+    assert rs <= BF16_REL_L2 and ms <= BF16_MAX_ABS, f"s: rel-L2 {rs:.3e}, max-abs {ms:.3e}"
 
 
 def test_stack_equals_block_loop():

@@ -91,3 +91,41 @@ def test_mask_view_broadcasts_over_the_batch():
         K._mask_view(torch.ones(4, n, n), (3,), n, CPU)
     with pytest.raises(ValueError, match="leading dims"):
         K._mask_view(torch.ones(2, 2, n, n), (2,), n, CPU)
+
+
+def test_pair_layout_predicate():
+    z = _z(lead=(2, 3))
+    assert K.pair_layout_ok(z)
+    assert K.pair_layout_ok(z[1])  # one view of a batch
+    assert K.pair_layout_ok(z.transpose(-2, -3))  # the ending-node strides
+    assert not K.pair_layout_ok(z.transpose(0, 1))  # leading dims that no view collapses
+    assert not K.pair_layout_ok(torch.zeros(8, 8, 256)[..., ::2])  # channel stride 2
+    assert not K.pair_layout_ok(torch.zeros(8, 8, 130)[..., 1:129])  # rows not 16-byte aligned
+    assert K.pair_layout_ok(_z(n=0))
+
+
+def test_weight_cache_entry_dies_with_its_parameter():
+    import gc
+    w = torch.nn.Parameter(torch.randn(64, 64))
+    w2 = torch.nn.Parameter(torch.randn(8, 64))
+    n0 = K.cache_size()
+    a = K.prepared(w, torch.bfloat16)
+    b = K.prepared_cat((w, w2), torch.bfloat16)
+    assert K.cache_size() == n0 + 2 and a.dtype == torch.bfloat16 and b.shape == (72, 64)
+    assert K.prepared(w, torch.bfloat16) is a  # a hit while the version holds
+    K.prepared_cat((w2, torch.nn.Parameter(torch.randn(4, 64))), torch.bfloat16)
+    gc.collect()
+    assert K.cache_size() == n0 + 2  # its temporary source died: entry gone
+    del w
+    gc.collect()
+    assert K.cache_size() == n0  # both remaining entries named the freed parameter
+
+
+def test_linear_takes_the_cached_cast_only_without_gradients():
+    from opendde_amd.layers import Linear
+    lin = Linear(16, 8)
+    assert lin._needs_grad()
+    with torch.no_grad():
+        assert not lin._needs_grad()
+    lin.requires_grad_(False)
+    assert not lin._needs_grad()
