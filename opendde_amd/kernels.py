@@ -107,10 +107,15 @@ def _batch_view(t: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
 _wcache: Dict[Tuple, Tuple] = {}
 
 
-def _evict(key, ref) -> None:
-    ent = _wcache.get(key)
-    if ent is not None and any(r is ref for r in ent[0]):
-        del _wcache[key]
+def _evictor(cache: Dict, key):
+    """Weakref callback dropping ``cache[key]`` when one of the entry's own
+    source references dies (closure state only: it may run at interpreter
+    shutdown, after module globals are cleared)."""
+    def cb(ref) -> None:
+        ent = cache.get(key)
+        if ent is not None and any(r is ref for r in ent[0]):
+            del cache[key]
+    return cb
 
 
 def _cached(key, srcs, make):
@@ -120,7 +125,8 @@ def _cached(key, srcs, make):
         if all(r() is s for r, s in zip(refs, srcs)) and versions == tuple(s._version for s in srcs):
             return val
     val = make()
-    refs = tuple(weakref.ref(s, lambda r, k=key: _evict(k, r)) for s in srcs)
+    cb = _evictor(_wcache, key)
+    refs = tuple(weakref.ref(s, cb) for s in srcs)
     _wcache[key] = (refs, tuple(s._version for s in srcs), val)
     return val
 

@@ -29,3 +29,16 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """The measured errors of the tolerance checks that ran (see
+    helpers.margin), so the margins show in a plain ``-q`` run."""
+    try:
+        from helpers import MARGINS
+    except ImportError:
+        return
+    if MARGINS:
+        terminalreporter.section("parity margins (measured error vs bar)")
+        for line in MARGINS:
+            terminalreporter.write_line(line)

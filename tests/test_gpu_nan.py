@@ -40,6 +40,8 @@ def _check(got, exp, tol, what):
     assert int(en.sum()) > 0, f"{what}: the NaN did not reach the reference's output"
     assert torch.equal(gn, en), f"{what}: NaN positions differ"
     fin = ~en
+    if not bool(fin.any()):
+        return  # the NaN reached every element (a whole block spreads it everywhere)
     assert torch.isfinite(got[fin]).all(), f"{what}: an Inf appeared"
     ma = float((got[fin] - exp[fin]).abs().max())
     assert ma <= tol, f"{what}: max-abs {ma:.3e} on the finite elements"
