@@ -288,15 +288,17 @@ def fp32_block_leg(dev):
     return out
 
 
-def config_legs(dev, with_cpu: bool):
+def config_legs(dev, with_cpu: bool, only=None):
     """The path's other specified workloads: GPU time (median of per-iteration
     events), TFLOP/s over the algorithmic flops, % of peak, the compulsory
     HBM bytes per ms of the module legs, and the CPU oracle (fp32, median of
-    5 after 1 warm-up) beside them."""
+    5 after 1 warm-up) beside them.  ``only``: the legs to run (names cfg1,
+    cfg2, cfg3, fp32, cfg5), all by default."""
     if with_cpu:
         from oracle import reference as ref
     cores = cpu_threads() if with_cpu else None
     res = {}
+    want = lambda name: only is None or name in only  # noqa: E731
 
     def cpu_leg(fn, fl):
         if not with_cpu:
@@ -305,131 +307,137 @@ def config_legs(dev, with_cpu: bool):
         return {"cpu_ms": round(med * 1e3, 2), "cpu_gflops": round(fl / med / 1e9, 2),
                 "cpu_cores": cores, "cpu_runs_s": [round(t, 3) for t in ts]}
 
-    # cfg1: one PairformerBlock at N=128, fp32 (c_s 384, 16 single heads)
-    cfg = wl.BLOCK_N128
-    z, s, mask, gen = wl.make_inputs(cfg)
-    blk = PairformerBlock(n_heads=16, c_z=128, c_s=384, c_hidden_mul=128,
-                          c_hidden_pair_att=32, no_heads_pair=4)
-    wl.init_module_(blk, gen)
-    blk = blk.eval()
-    p = _cpu_params(blk)
-    blk = blk.to(dev)
-    zg, sg, mg = z.to(dev), s.to(dev), mask.to(dev)
-    f = flops(cfg.n)["block"]
-    with torch.no_grad():
-        ms = gpu_median_ms(lambda: blk(sg, zg, mg, triangle_multiplicative="hip",
-                                       triangle_attention="hip"))
-    t = f / (ms * 1e-3) / 1e12
-    res["cfg1_block_n128_fp32"] = dict(
-        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
-        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2), dtype="fp32",
-        **cpu_leg(lambda: ref.pairformer_block(s, z, mask, p), f))
-    log(f"bench: cfg1 block n=128 fp32 {ms:.3f} ms")
-    del blk, zg, sg, mg
+    if want("cfg1"):
+        # cfg1: one PairformerBlock at N=128, fp32 (c_s 384, 16 single heads)
+        cfg = wl.BLOCK_N128
+        z, s, mask, gen = wl.make_inputs(cfg)
+        blk = PairformerBlock(n_heads=16, c_z=128, c_s=384, c_hidden_mul=128,
+                              c_hidden_pair_att=32, no_heads_pair=4)
+        wl.init_module_(blk, gen)
+        blk = blk.eval()
+        p = _cpu_params(blk)
+        blk = blk.to(dev)
+        zg, sg, mg = z.to(dev), s.to(dev), mask.to(dev)
+        f = flops(cfg.n)["block"]
+        with torch.no_grad():
+            ms = gpu_median_ms(lambda: blk(sg, zg, mg, triangle_multiplicative="hip",
+                                           triangle_attention="hip"))
+        t = f / (ms * 1e-3) / 1e12
+        res["cfg1_block_n128_fp32"] = dict(
+            gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+            pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2), dtype="fp32",
+            **cpu_leg(lambda: ref.pairformer_block(s, z, mask, p), f))
+        log(f"bench: cfg1 block n=128 fp32 {ms:.3f} ms")
+        del blk, zg, sg, mg
 
-    # cfg2: TriangleAttention starting node at N=384, bf16 z, last 38 tokens padded
-    cfg = wl.TRIATT_N384
-    z, _, mask, gen = wl.make_inputs(cfg)
-    mod = TriangleAttention(cfg.c_z, cfg.head_dim, cfg.heads)
-    wl.init_module_(mod, gen)
-    mod = mod.eval()
-    p = _cpu_params(mod)
-    mod = mod.to(dev)
-    zb = z.to(torch.bfloat16)
-    zg, mg = zb.to(dev), mask.to(dev)
-    fa = flops(cfg.n)
-    f = fa["core"] + fa["att_lin"]
-    fn = lambda: mod(zg, mg, triangle_attention="hip")  # noqa: E731
-    with torch.no_grad():
-        ms = gpu_median_ms(fn)
-        core_ms = kernel_avg_ms(fn, _lib.K_TRIATT_CORE)
-    t, tc = f / (ms * 1e-3) / 1e12, fa["core"] / (core_ms * 1e-3) / 1e12
-    zf = zb.float()
-    res["cfg2_triatt_start_n384_bf16"] = dict(
-        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
-        pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
-        core_ms=round(core_ms, 4), core_tflops=round(tc, 2),
-        core_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
-        hbm_gbs=round((2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
-        dtype="bf16", pad_tokens=cfg.n_pad,
-        **cpu_leg(lambda: ref.triangle_attention(zf, mask, p, cfg.heads), f))
-    log(f"bench: cfg2 tri-attn n=384 {ms:.3f} ms")
-    del mod, zg, mg
+    if want("cfg2"):
+        # cfg2: TriangleAttention starting node at N=384, bf16 z, last 38 tokens padded
+        cfg = wl.TRIATT_N384
+        z, _, mask, gen = wl.make_inputs(cfg)
+        mod = TriangleAttention(cfg.c_z, cfg.head_dim, cfg.heads)
+        wl.init_module_(mod, gen)
+        mod = mod.eval()
+        p = _cpu_params(mod)
+        mod = mod.to(dev)
+        zb = z.to(torch.bfloat16)
+        zg, mg = zb.to(dev), mask.to(dev)
+        fa = flops(cfg.n)
+        f = fa["core"] + fa["att_lin"]
+        fn = lambda: mod(zg, mg, triangle_attention="hip")  # noqa: E731
+        with torch.no_grad():
+            ms = gpu_median_ms(fn)
+            core_ms = kernel_avg_ms(fn, _lib.K_TRIATT_CORE)
+        t, tc = f / (ms * 1e-3) / 1e12, fa["core"] / (core_ms * 1e-3) / 1e12
+        zf = zb.float()
+        res["cfg2_triatt_start_n384_bf16"] = dict(
+            gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+            pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+            core_ms=round(core_ms, 4), core_tflops=round(tc, 2),
+            core_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
+            hbm_gbs=round((2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
+            dtype="bf16", pad_tokens=cfg.n_pad,
+            **cpu_leg(lambda: ref.triangle_attention(zf, mask, p, cfg.heads), f))
+        log(f"bench: cfg2 tri-attn n=384 {ms:.3f} ms")
+        del mod, zg, mg
 
-    # cfg3: TriangleMultiplication outgoing + incoming at N=768, bf16 z
-    cfg = wl.TRIMUL_N768
-    z, _, mask, gen = wl.make_inputs(cfg)
-    mo = TriangleMultiplicationOutgoing(cfg.c_z, cfg.c_hidden_mul)
-    mi = TriangleMultiplicationIncoming(cfg.c_z, cfg.c_hidden_mul)
-    wl.init_module_(mo, gen)
-    wl.init_module_(mi, gen)
-    po, pi = _cpu_params(mo), _cpu_params(mi)
-    mo, mi = mo.eval().to(dev), mi.eval().to(dev)
-    zb = z.to(torch.bfloat16)
-    zg, mg = zb.to(dev), mask.to(dev)
-    fm = flops(cfg.n)
-    f = 2 * (fm["contract"] + fm["mul_lin"])
+    if want("cfg3"):
+        # cfg3: TriangleMultiplication outgoing + incoming at N=768, bf16 z
+        cfg = wl.TRIMUL_N768
+        z, _, mask, gen = wl.make_inputs(cfg)
+        mo = TriangleMultiplicationOutgoing(cfg.c_z, cfg.c_hidden_mul)
+        mi = TriangleMultiplicationIncoming(cfg.c_z, cfg.c_hidden_mul)
+        wl.init_module_(mo, gen)
+        wl.init_module_(mi, gen)
+        po, pi = _cpu_params(mo), _cpu_params(mi)
+        mo, mi = mo.eval().to(dev), mi.eval().to(dev)
+        zb = z.to(torch.bfloat16)
+        zg, mg = zb.to(dev), mask.to(dev)
+        fm = flops(cfg.n)
+        f = 2 * (fm["contract"] + fm["mul_lin"])
 
-    def fn():
-        mo(zg, mg, triangle_multiplicative="hip")
-        mi(zg, mg, triangle_multiplicative="hip")
+        def fn():
+            mo(zg, mg, triangle_multiplicative="hip")
+            mi(zg, mg, triangle_multiplicative="hip")
 
-    with torch.no_grad():
-        ms = gpu_median_ms(fn)
-        ct_ms = kernel_avg_ms(fn, _lib.K_TRIMUL_CONTRACT)
-    t, tc = f / (ms * 1e-3) / 1e12, fm["contract"] / (ct_ms * 1e-3) / 1e12
-    zf = zb.float()
+        with torch.no_grad():
+            ms = gpu_median_ms(fn)
+            ct_ms = kernel_avg_ms(fn, _lib.K_TRIMUL_CONTRACT)
+        t, tc = f / (ms * 1e-3) / 1e12, fm["contract"] / (ct_ms * 1e-3) / 1e12
+        zf = zb.float()
 
-    def cpu3():
-        ref.triangle_multiplication(zf, mask, po, True)
-        ref.triangle_multiplication(zf, mask, pi, False)
+        def cpu3():
+            ref.triangle_multiplication(zf, mask, po, True)
+            ref.triangle_multiplication(zf, mask, pi, False)
 
-    res["cfg3_trimul_out_in_n768_bf16"] = dict(
-        gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
-        pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
-        contract_ms=round(ct_ms, 4), contract_tflops=round(tc, 2),
-        contract_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
-        hbm_gbs=round(2 * (2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
-        dtype="bf16", **cpu_leg(cpu3, f))
-    log(f"bench: cfg3 tri-mul n=768 out+in {ms:.3f} ms")
-    del mo, mi, zg, mg
-    torch.cuda.empty_cache()
+        res["cfg3_trimul_out_in_n768_bf16"] = dict(
+            gpu_ms=round(ms, 4), gflop=round(f / 1e9, 2), tflops=round(t, 2),
+            pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+            contract_ms=round(ct_ms, 4), contract_tflops=round(tc, 2),
+            contract_pct_bf16_peak=round(100 * tc / PEAK_BF16_TFLOPS, 2),
+            hbm_gbs=round(2 * (2 * cfg.n ** 2 * cfg.c_z * 2 + cfg.n ** 2 * 4) / (ms * 1e-3) / 1e9, 1),
+            dtype="bf16", **cpu_leg(cpu3, f))
+        log(f"bench: cfg3 tri-mul n=768 out+in {ms:.3f} ms")
+        del mo, mi, zg, mg
+        torch.cuda.empty_cache()
 
-    res["fp32_block_n1024"] = fp32_block_leg(dev)
+    if want("fp32"):
+        res["fp32_block_n1024"] = fp32_block_leg(dev)
 
-    # cfg5: N=2048, 4 blocks with the single track (c_s 384), bench mode,
-    # peak memory
-    cfg = wl.STRESS_N2048
-    z, s, mask, gen = wl.make_inputs(cfg)
-    stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=16, c_z=cfg.c_z, c_s=cfg.c_s)
-    wl.init_module_(stack, gen)
-    stack = stack.eval().to(dev)
-    z0, s0, mg = z.to(dev), s.to(dev), mask.to(dev)
-    zw = torch.empty_like(z0)
+    if want("cfg5"):
+        # cfg5: N=2048, 4 blocks with the single track (c_s 384), bench mode,
+        # peak memory
+        cfg = wl.STRESS_N2048
+        z, s, mask, gen = wl.make_inputs(cfg)
+        stack = PairformerStack(n_blocks=cfg.n_blocks, n_heads=16, c_z=cfg.c_z, c_s=cfg.c_s)
+        wl.init_module_(stack, gen)
+        stack = stack.eval().to(dev)
+        z0, s0, mg = z.to(dev), s.to(dev), mask.to(dev)
+        zw = torch.empty_like(z0)
 
-    def stress():
-        zw.copy_(z0)
-        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
-            stack(s0, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
-                  inplace_safe=True)
+        def stress():
+            zw.copy_(z0)
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                stack(s0, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
+                      inplace_safe=True)
 
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats(dev)
-    base = torch.cuda.memory_allocated(dev)
-    ms = gpu_median_ms(stress, warm=1, iters=3)
-    peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
-    fb = flops(cfg.n, c_s=cfg.c_s)
-    f = cfg.n_blocks * fb["block"]
-    t = f / (ms * 1e-3) / 1e12
-    res["cfg5_stress_4x_n2048_bf16"] = dict(
-        gpu_ms=round(ms, 2), block_ms=round(ms / cfg.n_blocks, 3), gflop=round(f / 1e9, 1),
-        tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
-        peak_gib_above_inputs=round(peak, 2), total_gib_in_use=round(
-            torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2), dtype="bf16",
-        residual_dtype="fp32", c_s=cfg.c_s)
-    log(f"bench: cfg5 stress n=2048 x4 {ms:.1f} ms, peak {peak:.1f} GiB")
-    del stack, z0, s0, zw, mg
-    torch.cuda.empty_cache()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        ms = gpu_median_ms(stress, warm=1, iters=3)
+        peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+        fb = flops(cfg.n, c_s=cfg.c_s)
+        f = cfg.n_blocks * fb["block"]
+        t = f / (ms * 1e-3) / 1e12
+        res["cfg5_stress_4x_n2048_bf16"] = dict(
+            gpu_ms=round(ms, 2), block_ms=round(ms / cfg.n_blocks, 3), gflop=round(f / 1e9, 1),
+            tflops=round(t, 2), pct_bf16_peak=round(100 * t / PEAK_BF16_TFLOPS, 2),
+            peak_gib_above_inputs=round(peak, 2), total_gib_in_use=round(
+                torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2), dtype="bf16",
+            residual_dtype="fp32", c_s=cfg.c_s)
+        log(f"bench: cfg5 stress n=2048 x4 {ms:.1f} ms, peak {peak:.1f} GiB")
+        del stack, z0, s0, zw, mg
+        torch.cuda.empty_cache()
+
     return res
 
 
@@ -579,9 +587,11 @@ def main():
                     help="trunk: c_z 128, 4 triangle heads, hidden 128 (the benchmark "
                          "configuration); opendde_v1: the shipped model's pair width, c_z 384 "
                          "with hidden_scale_up (12 heads, hidden 384)")
-    ap.add_argument("--fp32-block", action="store_true",
-                    help="run only the fp32-arithmetic N=1024 block leg and print its JSON "
-                         "(for kernel traces of that leg)")
+    ap.add_argument("--leg", choices=["cfg1", "cfg2", "cfg3", "fp32", "cfg5"],
+                    help="run only this workload leg on the GPU (no CPU oracle) and print "
+                         "its JSON: cfg1 N=128 block fp32, cfg2 N=384 attention, cfg3 N=768 "
+                         "multiplication, fp32 the N=1024 block in fp32 arithmetic, cfg5 "
+                         "N=2048 x 4 blocks (for kernel traces of one leg)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "
                          "size, then one trunk step over a single block; prints nothing else")
@@ -593,8 +603,8 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
-    if args.fp32_block:
-        print(json.dumps({"fp32_block_n1024": fp32_block_leg(dev)}), flush=True)
+    if args.leg:
+        print(json.dumps(config_legs(dev, with_cpu=False, only={args.leg})), flush=True)
         return
     v1 = args.preset == "opendde_v1"
     c_z, heads, ch = (384, 12, 384) if v1 else (128, 4, 128)
