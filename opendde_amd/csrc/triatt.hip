@@ -1873,7 +1873,7 @@ void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
 // ODDE_TRIATT_TILE="R,QB,RG,QS" selects another instantiation.
 struct CoreTile { int r, qb, rg, qs; };
 
-CoreTile core_tile(int rows_per_bias, int batches, bool f32) {
+CoreTile core_tile(int rows_per_bias, int batches, bool f32, int jp, int rows, int heads) {
   // f32 fragments are twice as wide: the bf16 tile would spill
   static CoreTile env = [] {
     CoreTile d{0, 0, 0, 0};
@@ -1883,7 +1883,13 @@ CoreTile core_tile(int rows_per_bias, int batches, bool f32) {
     }
     return d;
   }();
-  const CoreTile t = env.r ? env : (f32 ? CoreTile{2, 2, 2, 4} : CoreTile{2, 4, 2, 2});
+  CoreTile t = env.r ? env : (f32 ? CoreTile{2, 2, 2, 4} : CoreTile{2, 4, 2, 2});
+  // bf16 at small sizes: with fewer than 2048 workgroups of 4 rows x 128
+  // queries the last round of workgroups leaves most CUs idle; 4 rows x 64
+  // queries doubles the count (3 workgroups per CU).  N = 384: 0.089 ->
+  // 0.080 ms; from N = 512 up the default is as fast or faster.
+  if (!env.r && !f32 && (int64_t)(jp / 128) * ((rows + 3) / 4) * heads < 2048)
+    t = CoreTile{2, 2, 2, 2};
   // all rows of a workgroup share one bias batch
   if (batches > 1 && rows_per_bias % (t.r * t.rg) != 0) return CoreTile{1, t.qb, 1, t.qs};
   return t;
@@ -1906,7 +1912,7 @@ int launch_core(const TriattCoreArgs<CT>& p0, int batches, hipStream_t st) {
   TriattCoreArgs<CT> p = p0;
   p.out16 = sizeof(CT) == 2 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 &&
             ((p.o_row | p.o_h | p.o_j) & 7) == 0;
-  const CoreTile t = core_tile(p.rows_per_bias, batches, sizeof(CT) == 4);
+  const CoreTile t = core_tile(p.rows_per_bias, batches, sizeof(CT) == 4, p.jp, p.rows, p.heads);
   LaunchScope ls(ODDE_K_TRIATT_CORE, st);
 #define ODDE_TILE(R, QB, RG, QS)                                              \
   else if (t.r == R && t.qb == QB && t.rg == RG && t.qs == QS)                \

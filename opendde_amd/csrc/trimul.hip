@@ -18,6 +18,8 @@
 //
 // Workspace (CT = compute type, Np = N rounded up to 128):
 //   A, B, P : [Ch][Np][Np]
+#include <string.h>
+
 #include "common.hpp"
 #include "gemm.hpp"
 #include "lnpass.hpp"
@@ -247,15 +249,30 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
     }
 }
 
-// Np >= 1024: 256 x 256 tiles staged 64 k at a time (whole 128-byte lines of
+// Np >= 768: 256 x 256 tiles staged 64 k at a time (whole 128-byte lines of
 // each row; 128 KiB of LDS, one workgroup per CU), software-pipelined, each
-// wave a 64 x 128 block; smaller Np: 256 x 128 tiles staged 32 k at a time
+// wave a 64 x 128 block; Np = 512: 256 x 128 tiles staged 32 k at a time
 // (two workgroups per CU), which keeps more workgroups per channel.  Chosen
 // by measurement on MI355X (N = 1024: the pipelined loop 0.311 / 0.281 ms
 // outgoing / incoming against 0.317 / 0.290 ms for the plain one; deeper
-// 32-k staging, with or without a k-blocked operand layout, was slower).
+// 32-k staging, with or without a k-blocked operand layout, was slower;
+// N = 768: 0.138 against 0.152 ms for the 256 x 128 form).
+// ODDE_CONTRACT_TILE=256x256 or 256x128 overrides the choice by Np (tuning).
+inline int contract_tile_override() {
+  static const int v = [] {
+    const char* e = getenv("ODDE_CONTRACT_TILE");
+    if (!e) return 0;
+    if (strcmp(e, "256x256") == 0) return 1;
+    if (strcmp(e, "256x128") == 0) return 2;
+    return 0;
+  }();
+  return v;
+}
+
 inline void launch_contract_big(const ContractArgs<bf16>& k, int np, int ch, hipStream_t st) {
-  if (np >= 1024) {
+  const int ov = contract_tile_override();
+  // 256 x 256 from Np = 768 up (N = 768: 0.152 -> 0.138 ms against 256 x 128)
+  if (ov == 1 || (ov == 0 && np >= 768)) {
     const int tiles = (np / 256) * (np / 256);
     hipLaunchKernelGGL((trimul_contract_big_kernel<256, 256, 4, 2, 64, true>), dim3(tiles * ch),
                        dim3(512), 0, st, k);
