@@ -153,23 +153,30 @@ __device__ __forceinline__ V swap_lane_pairs(const V& v) {
 }
 
 // Streaming stores of whole 128-byte lines.  Each lane of a pair (2k, 2k + 1)
-// holds two 16-byte chunks of its own line: lo for slot s and hi for slot
-// s + 4 (the four lanes l, l + 16, l + 32, l + 48 hold s = 0..3 of the same
-// lines).  Storing lo, then hi, would leave each instruction with half lines,
-// which the streaming policy writes back poorly; here the pair exchanges one
-// chunk, so the first instruction writes the even lane's whole line and the
-// second the odd lane's.  `partner` is the other lane's line; own_ok and
-// partner_ok say whether the two lines are stored at all.  Every lane of the
-// wave must be active.
+// holds two 16-byte chunks of its own line: lo for slot slot_lo and hi for
+// slot slot_hi (the four lanes l, l + 16, l + 32, l + 48 hold four disjoint
+// slot pairs that together cover the line).  Storing lo, then hi, would leave
+// each instruction with half lines, which the streaming policy writes back
+// poorly; here the pair exchanges one chunk, so the first instruction writes
+// the even lane's whole line and the second the odd lane's.  `partner` is the
+// other lane's line; own_ok and partner_ok say whether the two lines are
+// stored at all.  Every lane of the wave must be active.
 template <typename V>
-__device__ __forceinline__ void store_line_pair(V* own, V* partner, int s, const V& lo, const V& hi,
-                                                bool own_ok = true, bool partner_ok = true) {
+__device__ __forceinline__ void store_line_pair_at(V* own, V* partner, int slot_lo, int slot_hi,
+                                                   const V& lo, const V& hi, bool own_ok = true,
+                                                   bool partner_ok = true) {
   const bool odd = threadIdx.x & 1;
   // even lanes receive the odd lane's lo, odd lanes the even lane's hi
   const V got = swap_lane_pairs(odd ? lo : hi);
-  const int slot = s + (odd ? 4 : 0);
+  const int slot = odd ? slot_hi : slot_lo;
   if (odd ? partner_ok : own_ok) store_stream((odd ? partner : own) + slot, odd ? got : lo);
   if (odd ? own_ok : partner_ok) store_stream((odd ? own : partner) + slot, odd ? hi : got);
+}
+// the slot pair (s, s + 4), s = 0..3
+template <typename V>
+__device__ __forceinline__ void store_line_pair(V* own, V* partner, int s, const V& lo, const V& hi,
+                                                bool own_ok = true, bool partner_ok = true) {
+  store_line_pair_at(own, partner, s, s + 4, lo, hi, own_ok, partner_ok);
 }
 
 __device__ __forceinline__ void load4(const float* p, float* o) {

@@ -224,23 +224,33 @@ __global__ __launch_bounds__(256, 2) void transition_kernel(TransitionArgs<ZT, C
 // (the four lanes of a row reduce by shuffles).  The hidden dimension is
 // walked in chunks of 32 whose W_a / W_b rows and W_o columns (24 KiB) stream
 // into three LDS stages by direct global -> LDS loads, two chunks ahead,
-// continuing across row tiles (every tile walks the same chunks).  At a tile
-// boundary each row block in turn adds its residual rows and stores, loads
-// the next block's residual rows, forms the pair bias (if asked) from the
-// stored values and loads its rows of the next tile; so the loads of one
-// workgroup overlap its own epilogue and the other workgroup's MFMA work.
+// continuing across row tiles (every tile walks the same chunks).
+// Residual: GEMM2's output rows are permuted so that a lane's accumulators
+// hold exactly the channels of the K32 fragment slots it loads for the
+// LayerNorm (block cb of row r16 holds channels 32 (cb >> 1) + 8 g + 4 (cb & 1)
+// + 0..3; the W_o fragment row of lane r16 in block cb is channel
+// 32 (cb >> 1) + 8 (r16 >> 2) + 4 (cb & 1) + (r16 & 3)), so the rows loaded
+// for the LayerNorm become the accumulators' initial values: x is read from
+// memory once and the epilogue has no residual to load or add.  At a tile
+// boundary each row block in turn stores (a lane's 8 consecutive channels,
+// whole lines together with the neighbouring row's lanes), forms the pair
+// bias (if asked) from the stored values and loads its rows of the next tile
+// into the registers just stored; so the loads of one workgroup overlap its
+// own epilogue and the other workgroup's MFMA work.
 // LDS layouts (bf16 elements): W_a, W_b chunk rows of 128 (16 slots of 16
 // bytes; slot t of row r holds chunk t ^ (r & 15)); W_o chunk rows of 32
-// (4 slots; slot t of row r holds chunk t ^ ((r >> 2) & 3): the 16 rows of a
-// fragment read then cover 16 distinct (row position, slot) pairs of a
-// 256-byte bank period, free of bank conflicts).
+// (4 slots; slot t of channel row c holds chunk t ^ ((c >> 3) & 3): the 16
+// rows of a fragment read, channels 8j + i + const for i, j = 0..3, then
+// cover 16 distinct (row position, slot) pairs of a 256-byte bank period,
+// free of bank conflicts).
 // The gate's exponent scale rides on the data: the LayerNorm output is
 // multiplied by -log2(e) (folded into its weight and bias), so GEMM1 yields
 // a'' = -log2(e) a and b'' = -log2(e) b; then
-// silu(a) b = (ln 2)^2 a'' b'' / (1 + 2^a''), and GEMM2's output is scaled
-// back by (ln 2)^2 in the epilogue's residual FMA.  This removes one multiply
-// per hidden unit from the gate.
-constexpr float kLn2Sq = 0.480453013918201424667f;  // (ln 2)^2 = 1 / log2(e)^2
+// silu(a) b = (ln 2)^2 a'' b'' / (1 + 2^a'') = a'' b'' / (log2(e)^2 (1 + 2^a'')),
+// the denominator one FMA, as 1 + 2^a'' was one add.  This removes one
+// multiply per hidden unit from the gate and the output scale from the
+// epilogue.
+constexpr float kLog2eSq = 2.08136898100560782f;  // log2(e)^2 = 1 / (ln 2)^2
 constexpr int kRB = 3;                   // 16-row blocks per wave
 constexpr int kTpRows = 64 * kRB;
 constexpr int kTpStages = 3;
@@ -252,7 +262,7 @@ constexpr int kTpOps = 6;                // 1 KiB direct loads per wave per chun
 // into W' = W diag(ln_w) (bf16, in LDS in fragment order: 16 bytes per lane
 // and step) and its bias into b = W ln_b, so pb = rstd (W' (z - mean)) + b.
 // The MFMA's K slots follow the accumulator layout of z: slot e of step t is
-// channel 32t + 16 (e >> 2) + 4g + (e & 3).
+// channel 32t + 8g + e.
 template <typename ZT>
 __device__ __forceinline__ void pair_bias_folded(const TransitionArgs<ZT, bf16>& a,
                                                  const f32x4 (&zacc)[8], int64_t row, bool valid,
@@ -326,21 +336,26 @@ struct RowSlots {
   }
 };
 
-// A lane's four output channels of one row (acc layout) as stored in ZT.
-template <typename ZT> struct Quad;
-template <> struct Quad<float> {
-  f32x4 v;
-  // the residual re-read of a row the kernel read once already: streamed
-  __device__ __forceinline__ void load(const float* p) {
-    v = load_stream(reinterpret_cast<const f32x4*>(p));
+// One output row of the pipelined form from its accumulators: lane (g, r16)
+// holds channels 32t + 8g .. +7 in blocks 2t, 2t + 1.  fp32 rows go out as
+// whole 128-byte lines (line t) together with the row of lane r16 ^ 1.
+template <typename ZT>
+__device__ __forceinline__ void store_rows_pipe(ZT* row, ZT* partner_row, const f32x4 (&r)[8],
+                                                bool ok, bool partner_ok) {
+  const int g = lane_id() >> 4;
+  if constexpr (sizeof(ZT) == 4) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      store_line_pair_at(reinterpret_cast<f32x4*>(row + 32 * t),
+                         reinterpret_cast<f32x4*>(partner_row + 32 * t), 2 * g, 2 * g + 1,
+                         r[2 * t], r[2 * t + 1], ok, partner_ok);
+  } else {
+    if (!ok) return;
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+      store4(row + 32 * (cb >> 1) + 8 * g + 4 * (cb & 1), r[cb][0], r[cb][1], r[cb][2], r[cb][3]);
   }
-  __device__ __forceinline__ float get(int e) const { return v[e]; }
-};
-template <> struct Quad<bf16> {
-  bf16x4 v;
-  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x4*>(p); }
-  __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
-};
+}
 
 // kAdd / kPb: the residual add and the pair-bias epilogue, fixed per
 // instantiation so that each form's epilogue is straight-line code
@@ -363,14 +378,14 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   }
   if (kPb) {
     // thread (w, g, r16) forms fragment slot set (t = w, g) of head r16:
-    // W'[r16][c] = W[r16][c] ln_w[c] for c = 32w + 16 (e >> 2) + 4g + (e & 3),
+    // W'[r16][c] = W[r16][c] ln_w[c] for c = 32w + 8g + e,
     // and its part of b[r16] = sum_c W[r16][c] ln_b[c]; the parts are summed
     // over g by lane swaps and over w in a fixed order
     Frag<bf16> wf;
     float part = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = 32 * w + 16 * (e >> 2) + 4 * g + (e & 3);
+      const int c = 32 * w + 8 * g + e;
       const float wv = (float)a.pb_w[r16 * C + c];
       wf.set(e, wv * a.pb_ln_w[c]);
       if (a.pb_ln_b) part += wv * a.pb_ln_b[c];
@@ -398,13 +413,14 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
   // 16-byte chunks are swizzled by key(row) = (4 (row >> 3) + (row & 3)) & 15
   // = 8 (op & 1) + 4 (w >> 1) + (l >> 4) (the 16 rows one GEMM1 fragment read
   // touches, 8 (m >> 2) + 4 hb + (m & 3), have the distinct keys m); W_o
-  // block bi holds channels 16 bi + (l >> 2).
+  // block bi holds channels c = 16 bi + (l >> 2), swizzled by
+  // (c >> 3) & 3 = (2 w + (l >> 5)) & 3.
   const int wu = __builtin_amdgcn_readfirstlane(w);
   int lane_ab[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p)
     lane_ab[p] = (l >> 4) * C + ((l & 15) ^ (8 * p + 4 * (w >> 1) + (l >> 4))) * 8;
-  const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((l >> 4) & 3)) * 8;
+  const int lane_o = (l >> 2) * HID + ((l & 3) ^ ((2 * w + (l >> 5)) & 3)) * 8;
   auto issue = [&](int q) {
     const int h0 = (q % NCHUNK) * kTrHid;
     bf16* base = ws[q % kTpStages];
@@ -452,15 +468,22 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb) sa_off[hb] = (8 * (r16 >> 2) + 4 * hb + (r16 & 3)) * C;
   const int so_sw = (r16 >> 2) & 3;
+  const int so_ch = 8 * (r16 >> 2) + (r16 & 3);
   const float* ln_w = lnp;
   const float* ln_b = lnp + C;
   int q = 0;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    // LayerNorm of the wave's rows (already in registers) into B fragments
+    // LayerNorm of the wave's rows (already in registers) into B fragments:
+    // the statistics of every row block, then the normalisation one K32 step
+    // at a time over the row blocks, so that a step's parameters (16
+    // registers) are read once and die with it.  The rows themselves then
+    // become the accumulators' initial values (the residual), in the
+    // accumulator layout (block cb = slots 2t + k: channels 32t + 8g + 4k +
+    // 0..3).
     Frag<bf16> xf[kRB][kC];
+    float mean[kRB], rstd[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
-      const bool valid = row_of(tile, rb) < a.rows;
       float x[kC][8];
       float s = 0.f;
 #pragma unroll
@@ -469,33 +492,54 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += x[t][e];
       }
-      const float mean = group_sum_fast(s) * (1.0f / C);
+      mean[rb] = group_sum_fast(s) * (1.0f / C);
       float v = 0.f;
 #pragma unroll
       for (int t = 0; t < kC; ++t)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float d = x[t][e] - mean;
+          const float d = x[t][e] - mean[rb];
           v += d * d;
         }
-      const float rstd = rsqrtf(group_sum_fast(v) * (1.0f / C) + a.eps);
+      rstd[rb] = rsqrtf(group_sum_fast(v) * (1.0f / C) + a.eps);
+    }
 #pragma unroll
-      for (int t = 0; t < kC; ++t) {
-        float lw[8], lb[8];
-        load4(ln_w + 32 * t + 8 * g, lw);
-        load4(ln_w + 32 * t + 8 * g + 4, lw + 4);
-        load4(ln_b + 32 * t + 8 * g, lb);
-        load4(ln_b + 32 * t + 8 * g + 4, lb + 4);
+    for (int t = 0; t < kC; ++t) {
+      float lw[8], lb[8];
+      load4(ln_w + 32 * t + 8 * g, lw);
+      load4(ln_w + 32 * t + 8 * g + 4, lw + 4);
+      load4(ln_b + 32 * t + 8 * g, lb);
+      load4(ln_b + 32 * t + 8 * g + 4, lb + 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          xf[rb][t].set(e, valid ? (x[t][e] - mean) * rstd * lw[e] + lb[e] : 0.f);
+      for (int rb = 0; rb < kRB; ++rb) {
+        // (x - mean) rstd lw + lb as x (rstd lw) + (lb - mean rstd lw), so that
+        // no x - mean is kept from the variance pass (the rows stay live as
+        // the residual; 32 more live values per row block would spill)
+        const bool valid = row_of(tile, rb) < a.rows;
+        float x[8];
+        xr[rb].get(t, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float sc = rstd[rb] * lw[e];
+          xf[rb][t].set(e, valid ? fmaf(x[e], sc, fmaf(-mean[rb], sc, lb[e])) : 0.f);
+        }
       }
     }
     f32x4 acc[kRB][NCB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int cb = 0; cb < NCB; ++cb) {
+        if (!kAdd) {
+          acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (sizeof(ZT) == 4) {
+          acc[rb][cb] = xr[rb].c[cb];
+        } else {
+          const bf16x8 xv = __builtin_bit_cast(bf16x8, xr[rb].c[cb >> 1]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][cb][e] = (float)xv[4 * (cb & 1) + e];
+        }
+      }
 
     for (int hc = 0; hc < NCHUNK; ++hc, ++q) {
       // This wave's loads of chunk q have landed: the loads of a tile's
@@ -555,14 +599,19 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
         for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            hf[rb].set(4 * hb + e, (sa[rb][e] * sb[rb][e]) * sigmoid_nl2e(sa[rb][e]));
+            hf[rb].set(4 * hb + e,
+                       (sa[rb][e] * sb[rb][e]) *
+                           __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(sa[rb][e]),
+                                                      kLog2eSq, kLog2eSq)));
       }
       // GEMM2: W_o[c][h0 + 8g .. + 7] fragments (staged chunk g, swizzled by
-      // (c >> 2) & 3), one 16-channel block at a time, all row blocks
+      // (c >> 3) & 3 = (r16 >> 2) & 3), one 16-channel block at a time, all
+      // row blocks; fragment row r16 of block cb is channel
+      // 32 (cb >> 1) + 8 (r16 >> 2) + 4 (cb & 1) + (r16 & 3)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         Frag<bf16> fo;
-        fo.load(wo + (cb * 16 + r16) * kTrHid + (g ^ so_sw) * 8);
+        fo.load(wo + (32 * (cb >> 1) + 4 * (cb & 1) + so_ch) * kTrHid + (g ^ so_sw) * 8);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb) mma(acc[rb][cb], fo, hf[rb]);
       }
@@ -572,33 +621,16 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
     // operations in flight: complete them here, before any row load, since
     // the next tile's first chunks only wait on lgkmcnt and the barrier.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // Then one row block at a time: add the residual rows, store, load the
-    // next block's residual rows (their latency covered by the pair bias),
-    // form the pair bias from the stored values, and load the block's rows of
-    // the next tile into the slots its LayerNorm freed (their latency covered
-    // by the remaining blocks' epilogues).
+    // Then one row block at a time: store, form the pair bias from the stored
+    // values, and load the block's rows of the next tile into the registers
+    // just stored (their latency covered by the remaining blocks' epilogues).
     const int64_t next = tile + gridDim.x;
-    const int gb = lane_g();
-    Quad<ZT> res[NCB];
-    auto load_res = [&](int rb) {
-      const int64_t rr = min(row_of(tile, rb), a.rows - 1);
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) res[cb].load(a.x + rr * C + cb * 16 + 4 * gb);
-    };
-    if (kAdd) load_res(0);
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int64_t row = row_of(tile, rb);
       const bool valid = row < a.rows;
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc[rb][cb][e] = kAdd ? fmaf(kLn2Sq, acc[rb][cb][e], res[cb].get(e))
-                                 : kLn2Sq * acc[rb][cb][e];
-      store_row_blocks<ZT>(a.out + row * C, a.out + (row ^ 1) * C, 0, acc[rb], valid,
-                           (row ^ 1) < a.rows);
-      if (kAdd && rb + 1 < kRB) load_res(rb + 1);
+      store_rows_pipe<ZT>(a.out + row * C, a.out + (row ^ 1) * C, acc[rb], valid,
+                          (row ^ 1) < a.rows);
       if (kPb)
         pair_bias_folded<ZT>(a, acc[rb], row, valid, pbwf, pbb);
       {
