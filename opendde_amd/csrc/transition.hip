@@ -38,6 +38,9 @@ struct TransitionArgs {
   float* pb_out;         // [16][rows]
   float pb_eps;
   const float* pb_zero;  // C zeros (stand-in for a null pb_ln_b)
+  // fp32 form with the hidden dimension split over gridDim.y workgroups:
+  // partial outputs [splits][rows][C] (null: one split, full epilogue)
+  float* part = nullptr;
 };
 
 constexpr int kTrRows = 128;  // rows per workgroup tile
@@ -655,6 +658,10 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 // floats, <= 7 MB) stays resident in L2 and the rows of a workgroup read it
 // once.  Splitting the hidden dimension over the waves keeps short row counts
 // (the single track's N rows) spread over 4x more waves than a row split.
+// For short row counts the hidden chunks are also split over gridDim.y
+// workgroups (a.part set): each writes its partial 16 x C output to
+// a.part[blockIdx.y], and transition_f32_reduce_kernel adds the partials in
+// split order and the residual.
 template <typename ZT, int kC>
 __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, float> a,
                                                              int64_t nblk) {
@@ -671,7 +678,8 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
     f32x4 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int hc = w; hc < NCHUNK; hc += 4) {
+    const int per = NCHUNK / (int)gridDim.y;  // hidden chunks of this split
+    for (int hc = (int)blockIdx.y * per + w; hc < ((int)blockIdx.y + 1) * per; hc += 4) {
       const int h0 = hc * kTrHid;
       // GEMM1 (W x^T orientation): lane (g, r16) ends with hidden units
       // h0 + 16 hb + 4g + e of row r16 -- slot 4 hb + e of a B fragment
@@ -705,7 +713,17 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
       for (int cb = 0; cb < NCB; ++cb) part[w - 1][cb][l] = acc[cb];
     }
     __syncthreads();
-    if (w == 0) {
+    if (w == 0 && a.part) {
+      // this split's partial: lane holds row r16, channels cb*16 + 4g + e
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc[cb] += part[k][cb][l];
+        if (valid)
+          *reinterpret_cast<f32x4*>(a.part + ((size_t)blockIdx.y * a.rows + row) * C + cb * 16 +
+                                    4 * g) = acc[cb];
+      }
+    } else if (w == 0) {
       // lane holds row r16, channels cb*16 + 4g + e
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
@@ -723,6 +741,151 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
     }
     __syncthreads();  // part is reused by the next row block
   }
+}
+
+// out = (add ? x : 0) + sum over splits of part[split] (split order), f32x4
+// per thread over rows x C.
+template <typename ZT>
+__global__ __launch_bounds__(256) void transition_f32_reduce_kernel(TransitionArgs<ZT, float> a,
+                                                                    int splits, int c) {
+  const int64_t n4 = a.rows * c / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    f32x4 v = a.add ? reinterpret_cast<const f32x4*>(a.x)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int y = 0; y < splits; ++y) v += reinterpret_cast<const f32x4*>(a.part)[y * n4 + i];
+    reinterpret_cast<f32x4*>(a.out)[i] = v;
+  }
+}
+
+// fp32 arithmetic, pipelined form for C in {64, 128}, n = 4 (the pair
+// transition in fp32 arithmetic).  Wave w of a workgroup of kW waves owns 16
+// rows of a 16 kW-row tile (persistent over tiles), LayerNorms them into K32
+// fragments in registers and walks the whole hidden dimension in chunks of
+// 32; the chunk's W_a / W_b rows and W_o columns (fp32, 384 C bytes) stream
+// into two LDS stages by direct global -> LDS loads, one chunk ahead, shared
+// by every wave of the workgroup.  Against the unstaged fp32 form (16 rows
+// per workgroup, weight fragments straight from L2) a weight byte fetched
+// from L2 serves 16 kW rows instead of 16.  GEMM1 runs in W x^T orientation:
+// lane (g, r16) ends with hidden units h0 + 16 hb + 4g + e of its row, slot
+// 4 hb + e of GEMM2's B fragment.  LDS layouts (16-byte chunks): W_a / W_b
+// chunk rows of C / 4 chunks, W_o rows (one per channel) of 8 chunks; chunk
+// position p of row r holds chunk p ^ (r & 7), so the 8 rows that a group of
+// 8 lanes reads at one chunk index land on 8 distinct 16-byte bank groups.
+template <int kC>
+struct TfStage {
+  static constexpr int C = kC * 32;
+  f32x4 wa[kTrHid * C / 4];  // [32 hidden][C / 4 chunks]
+  f32x4 wb[kTrHid * C / 4];
+  f32x4 wo[C * 8];           // [C][8 chunks of 4 hidden]
+};
+
+template <typename ZT, int kC, int kW>
+__global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(TransitionArgs<ZT, float> a,
+                                                                      int64_t ntiles) {
+  constexpr int C = kC * 32, HID = 4 * C, NCB = C / 16, NCHUNK = HID / kTrHid;
+  constexpr int CPR = C / 4;                 // 16-byte chunks per W_a / W_b row
+  constexpr int NAB = kTrHid * CPR / 64;     // direct loads per W_a (W_b) chunk
+  constexpr int NO = C * 8 / 64;             // direct loads per W_o chunk
+  constexpr int NOPS = 2 * NAB + NO;
+  static_assert(NOPS % kW == 0, "every wave issues the same number of direct loads");
+  __shared__ TfStage<kC> st[2];
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+
+  // this workgroup's tiles; only loads that will be consumed are issued
+  const int my_tiles =
+      blockIdx.x < ntiles ? (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0;
+  if (my_tiles == 0) return;
+  const int Q = my_tiles * NCHUNK;
+  // chunk q of the workgroup's sequence into stage q & 1: wave w issues ops
+  // w, w + kW, ...; op < 2 NAB is 1 KiB of W_a (W_b) rows (lane l: row
+  // (64 i + l) / CPR, position (64 i + l) % CPR), the rest 1 KiB of W_o
+  // (lane l: channel 8 i + (l >> 3), position l & 7)
+  auto issue = [&](int q) {
+    const int h0 = (q % NCHUNK) * kTrHid;
+    TfStage<kC>& S = st[q & 1];
+#pragma unroll
+    for (int j = 0; j < NOPS / kW; ++j) {
+      const int op = wu + j * kW;
+      const float* src;
+      f32x4* dst;
+      if (op < 2 * NAB) {
+        const int m = op / NAB, i = op % NAB;
+        const int idx = 64 * i + l, rr = idx / CPR, pos = idx % CPR;
+        src = (m ? a.wb : a.wa) + (size_t)(h0 + rr) * C + (pos ^ (rr & 7)) * 4;
+        dst = (m ? S.wb : S.wa) + 64 * i;
+      } else {
+        const int i = op - 2 * NAB;
+        const int c = 8 * i + (l >> 3), pos = l & 7;
+        src = a.wo + (size_t)c * HID + h0 + (pos ^ (c & 7)) * 4;
+        dst = S.wo + 64 * i;
+      }
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    }
+  };
+  issue(0);
+
+  const int key = r16 & 7;  // the swizzle key of every fragment row this lane reads
+  int q = 0;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t row = tile * (16 * kW) + 16 * w + r16;
+    const bool valid = row < a.rows;
+    Frag<float> xf[kC];
+    ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
+                                   xf);
+    f32x4 acc[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hc = 0; hc < NCHUNK; ++hc, ++q) {
+      // this wave's loads of chunk q (its only vector memory operations in
+      // flight) have landed and its reads of chunk q - 1 are done; the
+      // barrier publishes chunk q and frees stage (q + 1) & 1 for chunk q + 1
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      barrier_nofence();
+      if (q + 1 < Q) issue(q + 1);
+      const TfStage<kC>& S = st[q & 1];
+      Frag<float> hf;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+        const int rr = 16 * hb + r16;
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+          Frag<float> fa, fb;
+          fa.lo = S.wa[rr * CPR + ((8 * t + 2 * g) ^ key)];
+          fa.hi = S.wa[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
+          fb.lo = S.wb[rr * CPR + ((8 * t + 2 * g) ^ key)];
+          fb.hi = S.wb[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
+          mma(sa, fa, xf[t]);
+          mma(sb, fb, xf[t]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
+      }
+      // GEMM2: W_o[c][h0 + 4g .. + 3] and [h0 + 16 + 4g .. + 3] (chunks g, 4 + g)
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const int c = 16 * cb + r16;
+        Frag<float> fo;
+        fo.lo = S.wo[c * 8 + (g ^ key)];
+        fo.hi = S.wo[c * 8 + ((4 + g) ^ key)];
+        mma(acc[cb], fo, hf);
+      }
+    }
+    // epilogue: lane holds row r16 of the wave, channels 16 cb + 4g + e
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int c0 = cb * 16 + 4 * g;
+      float base[4] = {0.f, 0.f, 0.f, 0.f};
+      if (valid && a.add) load4(a.x + row * C + c0, base);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[cb][e] += base[e];
+      if (valid) store4(a.out + row * C + c0, acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
+    }
+    if (a.pb_out)
+      pair_bias_epilogue<ZT, float, kC>(a, acc, row, valid, a.pb_ln_w, a.pb_ln_b, a.pb_w);
+  }
+  // the last chunk's loads were all consumed; nothing is in flight
 }
 
 // Wide form (C = 384): a LayerNorm pass into bf16 rows, then two NT GEMMs on
@@ -941,7 +1104,25 @@ int64_t transition_wide_rows(int64_t rows) {
   const int64_t q = transition_wide_small(rows) ? 8 * 128 : 8 * kTwTX;
   return (rows + q - 1) / q * q;
 }
+// fp32 arithmetic with few rows (fewer than 512 blocks of 16): the hidden
+// chunks split over S workgroups per row block, S the largest divisor of
+// the chunks per wave (4C / 32 / 4) that keeps the grid within 1024
+// workgroups.  1: no split.  Not with the pair-bias epilogue.
+int transition_f32_splits(const odde_transition_args* a) {
+  if (a->compute_dtype != ODDE_F32 || a->n_factor != 4 || a->pb_heads) return 1;
+  if (a->c != 64 && a->c != 128 && a->c != 256 && a->c != 384) return 1;
+  const int64_t nblk = (a->rows + 15) / 16;
+  if (nblk >= 512 || nblk == 0) return 1;
+  const int per_wave = a->c / 32;  // 4C / 32 chunks over 4 waves
+  int best = 1;
+  for (int d = 1; d <= per_wave; ++d)
+    if (per_wave % d == 0 && nblk * d <= 1024) best = d;
+  return best;
+}
+
 uint64_t transition_ws_bytes(const odde_transition_args* a) {
+  const int splits = transition_f32_splits(a);
+  if (splits > 1) return (uint64_t)splits * (uint64_t)a->rows * (uint64_t)a->c * 4 + 256;
   if (!transition_wide(a->c, a->n_factor, a->compute_dtype)) return 0;
   // normalised rows [Mp][C] and hidden activations [Mp][4C], bf16; with the
   // split output GEMM its fp32 partial sums [kTwSplit][Mp][C]
@@ -1030,6 +1211,47 @@ int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
   const int64_t nblk = (p.rows + 15) / 16;
   const int grid = (int)std::min<int64_t>(nblk, 8 * 256);
   LaunchScope ls(ODDE_K_TRANSITION, st);
+  // the staged form when its tiles fill the GPU and the weights can be
+  // staged by 16-byte direct loads
+  const bool aligned16 = ((reinterpret_cast<uintptr_t>(p.wa) | reinterpret_cast<uintptr_t>(p.wb) |
+                           reinterpret_cast<uintptr_t>(p.wo)) & 15) == 0;
+  if (aligned16 && a->n_factor == 4 && (a->c == 64 || a->c == 128) && p.rows >= 256 * 64) {
+    if (p.rows >= 256 * 128) {  // 8 waves (128 rows) per workgroup, 2 per SIMD
+      const int64_t ntiles = (p.rows + 127) / 128;
+      const int g2 = (int)std::min<int64_t>(ntiles, a->c == 64 ? 2 * 256 : 256);
+      if (a->c == 64)
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 8>), dim3(g2), dim3(512), 0, st, p, ntiles);
+      else
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 8>), dim3(g2), dim3(512), 0, st, p, ntiles);
+    } else {  // 4 waves (64 rows) per workgroup: more workgroups for fewer rows
+      const int64_t ntiles = (p.rows + 63) / 64;
+      const int g2 = (int)std::min<int64_t>(ntiles, a->c == 64 ? 3 * 256 : 256);
+      if (a->c == 64)
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 4>), dim3(g2), dim3(256), 0, st, p, ntiles);
+      else
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 4>), dim3(g2), dim3(256), 0, st, p, ntiles);
+    }
+    return check_launch("transition (fp32)");
+  }
+  const int splits = transition_f32_splits(a);
+  if (splits > 1) {
+    const uint64_t need = (uint64_t)splits * (uint64_t)p.rows * (uint64_t)a->c * 4;
+    if (!a->workspace || a->workspace_bytes < need || (reinterpret_cast<uintptr_t>(a->workspace) & 15))
+      return set_error(ODDE_EINVAL, "transition (fp32, split hidden): workspace missing or too small");
+    p.part = static_cast<float*>(a->workspace);
+    const dim3 g3((unsigned)nblk, (unsigned)splits);
+    switch (a->c) {
+      case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2>), g3, dim3(256), 0, st, p, nblk); break;
+      case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4>), g3, dim3(256), 0, st, p, nblk); break;
+      case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8>), g3, dim3(256), 0, st, p, nblk); break;
+      default: hipLaunchKernelGGL((transition_f32_kernel<float, 12>), g3, dim3(256), 0, st, p, nblk); break;
+    }
+    const int64_t n4 = p.rows * a->c / 4;
+    const int rg = (int)std::min<int64_t>((n4 + 255) / 256, 1024);
+    hipLaunchKernelGGL((transition_f32_reduce_kernel<float>), dim3(rg), dim3(256), 0, st, p, splits,
+                       a->c);
+    return check_launch("transition (fp32, split hidden)");
+  }
   switch (a->c) {
     case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2>), dim3(grid), dim3(256), 0, st, p, nblk); break;
     case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4>), dim3(grid), dim3(256), 0, st, p, nblk); break;

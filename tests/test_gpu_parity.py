@@ -324,7 +324,11 @@ def test_transition_bf16(c, rows):
     assert_bf16(got, exp, f"transition c={c} rows={rows}")
 
 
-@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 130), (384, 17)])
+# at c = 64 and 128 from 16384 rows the weights are staged in LDS, shared by
+# 64-row (4-wave) or, from 32768 rows, 128-row (8-wave) workgroup tiles: both
+# forms, exact and ragged last tiles
+@pytest.mark.parametrize("c,rows", [(128, 1000), (64, 257), (256, 130), (384, 130), (384, 17),
+                                    (128, 16384), (128, 40000), (64, 16400), (64, 33000)])
 def test_transition_fp32(c, rows):
     # fp32 arithmetic (no autocast): the fp32 tier's max-abs 1e-4
     from opendde_amd.pairformer import Transition
@@ -345,11 +349,12 @@ def test_transition_fp32(c, rows):
     assert_fp32(got2, x + exp, f"transition fp32 in place c={c} rows={rows}")
 
 
-@pytest.mark.parametrize("c,ln_offset", [(128, True), (64, False), (384, True)])
-def test_transition_fp32_pair_bias_projection(c, ln_offset):
+@pytest.mark.parametrize("c,ln_offset,n", [(128, True, 37), (64, False, 37), (384, True, 37),
+                                            (128, True, 131), (64, False, 182)])
+def test_transition_fp32_pair_bias_projection(c, ln_offset, n):
     # the fp32 tier's pair bias from the fused epilogue, against the oracle
+    # (n = 131 and 182: the LDS-staged forms)
     from opendde_amd.pairformer import AttentionPairBias, Transition
-    n = 37
     tr = seeded(Transition(c, 4), 740, STD * (128 / c) ** 0.5)
     apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=c, create_offset_ln_z=ln_offset), 741,
                  0.1 * (128 / c) ** 0.5)
