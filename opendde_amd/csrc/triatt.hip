@@ -158,109 +158,157 @@ struct TriattProjArgs {
   float eps;
 };
 
-template <typename ZT, typename CT, int kC>
+// Wave w of a workgroup owns pair rows (i, j0 + 16 w .. + 15) for kRB
+// consecutive rows i: every weight fragment it reads from L2 serves kRB row
+// blocks (the fp32 form, whose weights are too large to hold, is bound by
+// those reads).  Rows i at or past n are skipped (workgroup-uniform).
+template <typename ZT, typename CT, int kC, int kRB = 1>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
-  const int i = blockIdx.y;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int j0 = blockIdx.x * 64 + w * 16;
   const int jl = j0 + r16;
-  const bool valid = jl < a.n;
-  const ZT* rowp = a.z + (int64_t)i * a.z_s0 + (int64_t)(valid ? jl : 0) * a.z_s1;
-  Frag<CT> x[kC];
-  ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, x);
-
+  const int i0 = blockIdx.y * kRB;
   const int H = a.heads, HD = H * 32, jp = a.jp;
+  Frag<CT> x[kRB][kC];
 
-  // mask row: additive form for the exact core, keep flags for the fast one
-  __shared__ float keep_s[64];
-  __shared__ int wmasked[4];
-  float mv = -INFINITY, kp = 0.f;
-  if (valid) {
-    const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
-    mv = (m - 1.0f) * a.mask_inf;
-    kp = m == 1.0f ? 1.f : 0.f;
+  // mask rows: additive form for the exact core, keep flags for the fast one
+  __shared__ float keep_s[kRB][64];
+  __shared__ int wmasked[kRB][4];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    const int i = i0 + rb;
+    const bool live = i < a.n;
+    const bool valid = live && jl < a.n;
+    const ZT* rowp = a.z + (int64_t)(live ? i : 0) * a.z_s0 + (int64_t)(valid ? jl : 0) * a.z_s1;
+    ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, x[rb]);
+    float mv = -INFINITY, kp = 0.f;
+    if (valid) {
+      const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
+      mv = (m - 1.0f) * a.mask_inf;
+      kp = m == 1.0f ? 1.f : 0.f;
+    }
+    if (g == 0) {
+      if (live) a.mb[(size_t)i * jp + jl] = mv;
+      keep_s[rb][w * 16 + r16] = kp;
+    }
+    const bool any_masked = __any(mv != 0.f);
+    if (l == 0) wmasked[rb][w] = any_masked ? 1 : 0;
   }
-  if (g == 0) {
-    a.mb[(size_t)i * jp + jl] = mv;
-    keep_s[w * 16 + r16] = kp;
-  }
-  const bool any_masked = __any(mv != 0.f);
-  if (l == 0) wmasked[w] = any_masked ? 1 : 0;
   __syncthreads();
-  if (threadIdx.x < 2) {
-    const int b = threadIdx.x;  // 32-key block b of this 64-key tile = waves 2b, 2b+1
-    a.mflag[(size_t)i * (jp >> 5) + blockIdx.x * 2 + b] = wmasked[2 * b] | wmasked[2 * b + 1];
+  bool zero_v[kRB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    const int i = i0 + rb;
+    zero_v[rb] = false;
+    if (i >= a.n) continue;
+    if (threadIdx.x < 2) {
+      const int b = threadIdx.x;  // 32-key block b of this 64-key tile = waves 2b, 2b+1
+      a.mflag[(size_t)i * (jp >> 5) + blockIdx.x * 2 + b] = wmasked[rb][2 * b] | wmasked[rb][2 * b + 1];
+    }
+    if (threadIdx.x < 64) {
+      const int t = threadIdx.x, kb = t >> 5, s = t & 31;
+      a.keep[((size_t)i * (jp >> 5) + blockIdx.x * 2 + kb) * 32 + s] =
+          from_f32<CT>(keep_s[rb][kb * 32 + slot_key(s >> 3, s & 7)]);
+    }
+    zero_v[rb] = a.anykeep[i] != 0;
   }
-  if (threadIdx.x < 64) {
-    const int t = threadIdx.x, kb = t >> 5, s = t & 31;
-    a.keep[((size_t)i * (jp >> 5) + blockIdx.x * 2 + kb) * 32 + s] =
-        from_f32<CT>(keep_s[kb * 32 + slot_key(s >> 3, s & 7)]);
-  }
-  const bool zero_v = a.anykeep[i] != 0;
 
   // q, k, gate: product W x^T -> lane holds pair row jl, channels o..o+3.
-  float ss = 0.f;
+  float ss[kRB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) ss[rb] = 0.f;
   for (int ob = 0; ob < HD / 16; ++ob) {
-    f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ak = aq, ag = aq;
+    f32x4 aq[kRB], ak[kRB], ag[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) aq[rb] = ak[rb] = ag[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       Frag<CT> f;
       load_w_frag(a.wq, C, ob * 16, HD, t, f);
-      mma(aq, f, x[t]);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(aq[rb], f, x[rb][t]);
       load_w_frag(a.wk, C, ob * 16, HD, t, f);
-      mma(ak, f, x[t]);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ak[rb], f, x[rb][t]);
       load_w_frag(a.wg, C, ob * 16, HD, t, f);
-      mma(ag, f, x[t]);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], f, x[rb][t]);
     }
     const int o = ob * 16 + 4 * g;
     const int h = o >> 5, d = o & 31;
-    const size_t off = (((size_t)i * H + h) * jp + jl) * 32 + d;
-    const float s = a.q_scale;
-    store4(a.q + off, aq[0] * s, aq[1] * s, aq[2] * s, aq[3] * s);
-    store4(a.k + off, ak[0], ak[1], ak[2], ak[3]);
-    store4(a.gate + off, sigmoidf_(ag[0]), sigmoidf_(ag[1]), sigmoidf_(ag[2]), sigmoidf_(ag[3]));
-    ss += ak[0] * ak[0] + ak[1] * ak[1] + ak[2] * ak[2] + ak[3] * ak[3];
-    if (ob & 1) {  // the 32 channels of head ob/2 are complete
-      const float nrm = lanes16_max(sqrtf(group_sum_fast(ss)));
-      if (l == 0) atomicMax(&a.kmax[i * H + (ob >> 1)], __float_as_uint(nrm));
-      ss = 0.f;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int i = i0 + rb;
+      if (i >= a.n) continue;
+      const size_t off = (((size_t)i * H + h) * jp + jl) * 32 + d;
+      const float s = a.q_scale;
+      store4(a.q + off, aq[rb][0] * s, aq[rb][1] * s, aq[rb][2] * s, aq[rb][3] * s);
+      store4(a.k + off, ak[rb][0], ak[rb][1], ak[rb][2], ak[rb][3]);
+      store4(a.gate + off, sigmoidf_(ag[rb][0]), sigmoidf_(ag[rb][1]), sigmoidf_(ag[rb][2]),
+             sigmoidf_(ag[rb][3]));
+      ss[rb] += ak[rb][0] * ak[rb][0] + ak[rb][1] * ak[rb][1] + ak[rb][2] * ak[rb][2] +
+                ak[rb][3] * ak[rb][3];
+      if (ob & 1) {  // the 32 channels of head ob/2 are complete
+        const float nrm = lanes16_max(sqrtf(group_sum_fast(ss[rb])));
+        if (l == 0) atomicMax(&a.kmax[i * H + (ob >> 1)], __float_as_uint(nrm));
+        ss[rb] = 0.f;
+      }
     }
   }
 
   // v: product x W^T -> lane holds channel o, pair rows j0+4g .. +3.
   const int jb = j0 + 4 * g;
-  float vk[4];
+  float vk[kRB][4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) vk[e] = zero_v ? keep_s[w * 16 + 4 * g + e] : 1.f;
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vk[rb][e] = zero_v[rb] ? keep_s[rb][w * 16 + 4 * g + e] : 1.f;
   for (int ob = 0; ob < HD / 16; ++ob) {
-    f32x4 av = {0.f, 0.f, 0.f, 0.f};
+    f32x4 av[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) av[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       Frag<CT> f;
       load_w_frag(a.wv, C, ob * 16, HD, t, f);
-      mma(av, x[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(av[rb], x[rb][t], f);
     }
     const int o = ob * 16 + r16;
-    store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), av[0] * vk[0], av[1] * vk[1],
-           av[2] * vk[2], av[3] * vk[3]);
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int i = i0 + rb;
+      if (i >= a.n) continue;
+      store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), av[rb][0] * vk[rb][0],
+             av[rb][1] * vk[rb][1], av[rb][2] * vk[rb][2], av[rb][3] * vk[rb][3]);
+    }
   }
 
   // triangle bias: channel h = r16 (< H), rows jb..jb+3 -> bias[h][i][jb..]
   {
-    f32x4 ab = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ab[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) ab[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       Frag<CT> f;
       load_w_frag(a.wb, C, 0, H, t, f);
-      mma(ab, x[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ab[rb], x[rb][t], f);
     }
     const float s = kLog2e;
-    const float bm = group_max_fast(fmaxf(fmaxf(ab[0], ab[1]), fmaxf(ab[2], ab[3])) * s);
-    if (r16 < H) {
-      store4(a.bias + ((size_t)r16 * jp + i) * jp + jb, ab[0] * s, ab[1] * s, ab[2] * s,
-             ab[3] * s);
-      if (g == 0) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int i = i0 + rb;
+      if (i >= a.n) continue;
+      const float bm =
+          group_max_fast(fmaxf(fmaxf(ab[rb][0], ab[rb][1]), fmaxf(ab[rb][2], ab[rb][3])) * s);
+      if (r16 < H) {
+        store4(a.bias + ((size_t)r16 * jp + i) * jp + jb, ab[rb][0] * s, ab[rb][1] * s,
+               ab[rb][2] * s, ab[rb][3] * s);
+        if (g == 0) atomicMax(&a.bmax[r16 * jp + i], fkey(bm));
+      }
     }
   }
 }
@@ -1802,6 +1850,15 @@ int check_triatt(const odde_triatt_args* a) {
 
 template <typename ZT, typename CT, int kC>
 void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
+  // fp32 weights are read from L2 per fragment: more rows i per wave as
+  // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
+  // large enough (n >= 256)
+  constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 8 ? 2 : 1;
+  if (kRB > 1 && n >= 256) {
+    dim3 grid(jp / 64, (n + kRB - 1) / kRB);
+    hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, kRB>), grid, dim3(256), 0, st, p);
+    return;
+  }
   dim3 grid(jp / 64, n);
   hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
 }

@@ -47,53 +47,70 @@ struct TrimulProjArgs {
   float eps;
 };
 
-template <typename ZT, typename CT, int kC>
+// Wave w of a workgroup owns pair rows (x, y0 + 16 w .. + 15) for kRB
+// consecutive first indices x: every weight fragment it reads from L2 serves
+// kRB row blocks (the fp32 form, whose weights are too large to hold, is
+// bound by those reads).
+template <typename ZT, typename CT, int kC, int kRB = 1>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
-  const int x_ = blockIdx.y;  // first index of the (strided) view
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int y0 = blockIdx.x * 64 + w * 16;
   const int yl = y0 + r16;
-  const bool valid = x_ < a.n && yl < a.n;
-  const ZT* rowp = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
-  Frag<CT> xf[kC];
-  ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xf);
-
   // mask for the four rows y0+4g .. +3 this lane writes
   const int yb = y0 + 4 * g;
-  float mk[4];
+  Frag<CT> xf[kRB][kC];
+  float mk[kRB][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int y = yb + r;
-    mk[r] = (x_ < a.n && y < a.n)
-                ? (a.mask ? a.mask[(int64_t)x_ * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
-                : 0.f;
+  for (int rb = 0; rb < kRB; ++rb) {
+    const int x_ = blockIdx.y * kRB + rb;  // first index of the (strided) view
+    const bool valid = x_ < a.n && yl < a.n;
+    const ZT* rowp =
+        a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
+    ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xf[rb]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int y = yb + r;
+      mk[rb][r] = (x_ < a.n && y < a.n)
+                      ? (a.mask ? a.mask[(int64_t)x_ * a.m_s0 + (int64_t)y * a.m_s1] : 1.0f)
+                      : 0.f;
+    }
   }
   const int ch = a.ch, np = a.np;
   for (int cb = 0; cb < ch / 16; ++cb) {
-    f32x4 ap = {0.f, 0.f, 0.f, 0.f}, ag = ap, bp = ap, bg = ap;
+    f32x4 ap[kRB], ag[kRB], bp[kRB], bg[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) ap[rb] = ag[rb] = bp[rb] = bg[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       Frag<CT> f;
       load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
-      mma(ap, xf[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ap[rb], xf[rb][t], f);
       load_w_frag(a.wg, C, cb * 16, 2 * ch, t, f);
-      mma(ag, xf[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], xf[rb][t], f);
       load_w_frag(a.wp, C, ch + cb * 16, 2 * ch, t, f);
-      mma(bp, xf[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(bp[rb], xf[rb][t], f);
       load_w_frag(a.wg, C, ch + cb * 16, 2 * ch, t, f);
-      mma(bg, xf[t], f);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(bg[rb], xf[rb][t], f);
     }
     const int c = cb * 16 + r16;
-    const size_t off = ((size_t)c * np + x_) * np + yb;
-    float va[4], vb[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      va[r] = mk[r] * sigmoidf_(ag[r]) * ap[r];
-      vb[r] = mk[r] * sigmoidf_(bg[r]) * bp[r];
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int x_ = blockIdx.y * kRB + rb;
+      const size_t off = ((size_t)c * np + x_) * np + yb;
+      float va[4], vb[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        va[r] = mk[rb][r] * sigmoidf_(ag[rb][r]) * ap[rb][r];
+        vb[r] = mk[rb][r] * sigmoidf_(bg[rb][r]) * bp[rb][r];
+      }
+      store4(a.A + off, va[0], va[1], va[2], va[3]);
+      store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
     }
-    store4(a.A + off, va[0], va[1], va[2], va[3]);
-    store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
   }
 }
 
@@ -1003,6 +1020,15 @@ int check_trimul(const odde_trimul_args* a) {
 
 template <typename ZT, typename CT, int kC>
 void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
+  // fp32 weights are read from L2 per fragment: more row blocks per wave as
+  // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
+  // large enough (np >= 256: np^2 / 256 workgroups and more)
+  constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
+  if (kRB > 1 && p.np >= 256) {
+    dim3 grid(p.np / 64, p.np / kRB);
+    hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kRB>), grid, dim3(256), 0, st, p);
+    return;
+  }
   dim3 grid(p.np / 64, p.np);
   hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
 }
