@@ -238,11 +238,14 @@ def probe_machine(dev):
     return out
 
 
-def fp32_block_leg(dev):
+def fp32_block_leg(dev, tf32: bool = False):
     """fp32 arithmetic at the trunk's size: one block of the N=1024 workload
     (51 random pads, c_s 384) with fp32 z and no autocast, in place -- the
     reference's default inference precision.  GPU time (median of per-step
-    events) and the per-kernel launch times of one further step."""
+    events) and the per-kernel launch times of one further step.  ``tf32``:
+    with torch.backends.cuda.matmul.allow_tf32 set, as the reference's
+    inference default (enable_tf32) sets it -- the attention core then runs
+    its products in three bf16 parts."""
     cfg = wl.TRUNK_N1024
     z, s, mask, gen = wl.make_inputs(cfg)
     blk = PairformerBlock(n_heads=16, c_z=128, c_s=384)
@@ -253,9 +256,14 @@ def fp32_block_leg(dev):
 
     def fp32_block():
         zw.copy_(z0)
-        with torch.no_grad():
-            blk(sg, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
-                inplace_safe=True)
+        old = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+        try:
+            with torch.no_grad():
+                blk(sg, zw, mg, triangle_multiplicative="hip", triangle_attention="hip",
+                    inplace_safe=True)
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = old
 
     ms = gpu_median_ms(fp32_block, warm=2, iters=5)
     f = flops(cfg.n)["block"]
@@ -280,9 +288,10 @@ def fp32_block_leg(dev):
     _lib.timing_reset()
     out = dict(
         gpu_ms=round(ms, 3), gflop=round(f / 1e9, 1), tflops=round(t, 2),
-        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2), dtype="fp32", residual_dtype="fp32",
-        pad_tokens=cfg.n_pad, kernels=per_kernel)
-    log(f"bench: fp32 block n=1024 {ms:.2f} ms")
+        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2),
+        dtype="fp32, attention core products in three bf16 parts" if tf32 else "fp32",
+        residual_dtype="fp32", allow_tf32=tf32, pad_tokens=cfg.n_pad, kernels=per_kernel)
+    log(f"bench: fp32 block n=1024{' (tf32 allowed)' if tf32 else ''} {ms:.2f} ms")
     del blk, z0, zw, sg, mg
     torch.cuda.empty_cache()
     return out
@@ -293,7 +302,7 @@ def config_legs(dev, with_cpu: bool, only=None):
     events), TFLOP/s over the algorithmic flops, % of peak, the compulsory
     HBM bytes per ms of the module legs, and the CPU oracle (fp32, median of
     5 after 1 warm-up) beside them.  ``only``: the legs to run (names cfg1,
-    cfg2, cfg3, fp32, cfg5), all by default."""
+    cfg2, cfg3, fp32, fp32_tf32, cfg5), all by default."""
     if with_cpu:
         from oracle import reference as ref
     cores = cpu_threads() if with_cpu else None
@@ -402,6 +411,8 @@ def config_legs(dev, with_cpu: bool, only=None):
 
     if want("fp32"):
         res["fp32_block_n1024"] = fp32_block_leg(dev)
+    if want("fp32_tf32"):
+        res["fp32_tf32_block_n1024"] = fp32_block_leg(dev, tf32=True)
 
     if want("cfg5"):
         # cfg5: N=2048, 4 blocks with the single track (c_s 384), bench mode,
@@ -587,10 +598,11 @@ def main():
                     help="trunk: c_z 128, 4 triangle heads, hidden 128 (the benchmark "
                          "configuration); opendde_v1: the shipped model's pair width, c_z 384 "
                          "with hidden_scale_up (12 heads, hidden 384)")
-    ap.add_argument("--leg", choices=["cfg1", "cfg2", "cfg3", "fp32", "cfg5"],
+    ap.add_argument("--leg", choices=["cfg1", "cfg2", "cfg3", "fp32", "fp32_tf32", "cfg5"],
                     help="run only this workload leg on the GPU (no CPU oracle) and print "
                          "its JSON: cfg1 N=128 block fp32, cfg2 N=384 attention, cfg3 N=768 "
-                         "multiplication, fp32 the N=1024 block in fp32 arithmetic, cfg5 "
+                         "multiplication, fp32 the N=1024 block in fp32 arithmetic, fp32_tf32 "
+                         "the same with reduced-precision products allowed, cfg5 "
                          "N=2048 x 4 blocks (for kernel traces of one leg)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one streaming calibration kernel of known "

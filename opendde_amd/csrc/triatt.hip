@@ -703,6 +703,8 @@ struct TriattCoreArgs {
   int64_t o_row, o_h, o_j;  // element strides of out[row][h][q][d]
   int rows, heads, n, jp, rows_per_bias;
   int out16;  // bf16 out with every (row, h, q) start 16-byte aligned
+  // f32 data, products on the bf16 MFMA in three parts (ODDE_F32X3)
+  int x3 = 0;
 };
 
 // Row sums of the probabilities: bf16 pairs through v_dot2 (the same rounded
@@ -721,6 +723,25 @@ __device__ __forceinline__ float psum8(const Frag<float>& p, const Frag<float>& 
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc = fmaf(p.get(e), wgt.get(e), acc);
   return acc;
+}
+// An f32 fragment as a pair of bf16 fragments, x = hi + lo + O(2^-18 |x|):
+// hi = bf16(x) to nearest, lo = bf16(x - hi).  Products of two such pairs as
+// hi*hi + hi*lo + lo*hi on the bf16 MFMA (fp32 accumulation) carry ~2^-16 of
+// relative error: the three-part fp32 form.
+__device__ __forceinline__ void split_x3(const Frag<float>& f, Frag<bf16>& hi, Frag<bf16>& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = f.get(e);
+    const bf16 h = (bf16)x;
+    hi.v[e] = h;
+    lo.v[e] = (bf16)(x - (float)h);
+  }
+}
+__device__ __forceinline__ void mma_x3(f32x4& acc, const Frag<bf16>& ah, const Frag<bf16>& al,
+                                       const Frag<bf16>& bh, const Frag<bf16>& bl) {
+  mma(acc, al, bh);
+  mma(acc, ah, bl);
+  mma(acc, ah, bh);
 }
 __device__ __forceinline__ Frag<bf16> ones_frag(bf16) {
   Frag<bf16> f;
@@ -831,9 +852,10 @@ __device__ __forceinline__ void xcd_group_map(int L, int nx, int ngroups, int& x
   x = s % nx;
 }
 
-template <typename CT, int R, int QB, int RG, int QS>
+template <typename CT, int R, int QB, int RG, int QS, bool kX3 = false>
 __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCoreArgs<CT> a, int nx,
                                                                         int ny) {
+  static_assert(!kX3 || sizeof(CT) == 4, "the three-part form takes f32 data");
   constexpr int NW = RG * QS;
   constexpr int R_WG = RG * R, Q_WG = QS * 16 * QB;
   typedef CoreStage<CT, R_WG, Q_WG> Stage;
@@ -947,6 +969,15 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
   // the same for every lane of the wave (its rows and their flags): made
   // provably uniform so that `if (!skip)` is a scalar branch, not an exec mask
   skip = __builtin_amdgcn_readfirstlane((int)skip) != 0;
+  // three-part form: q as bf16 pairs, once
+  Frag<bf16> qh[kX3 ? R : 1][QB], ql[kX3 ? R : 1][QB];
+  if constexpr (kX3) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        if constexpr (sizeof(CT) == 4) split_x3(qf[r][qb], qh[r][qb], ql[r][qb]);
+  }
 
   f32x4 o[R][2][QB];
   float lsum[R][QB];
@@ -1007,13 +1038,26 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
         // raised issue priority while this wave issues QK^T: with two waves
         // per SIMD, its MFMAs go ahead of the other wave's exponentials
         __builtin_amdgcn_s_setprio(1);
+        if constexpr (kX3) {
+          Frag<bf16> kh[2], kl[2];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 2; ++kb) split_x3(kf[kb], kh[kb], kl[kb]);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            s[kb][qb] = bfr[kb][qb];
-            mma(s[kb][qb], kf[kb], qf[r][qb]);
-          }
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              s[kb][qb] = bfr[kb][qb];
+              mma_x3(s[kb][qb], kh[kb], kl[kb], qh[r][qb], ql[r][qb]);
+            }
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              s[kb][qb] = bfr[kb][qb];
+              mma(s[kb][qb], kf[kb], qf[r][qb]);
+            }
+        }
         __builtin_amdgcn_s_setprio(0);
         Frag<CT> pf[QB];
 #pragma unroll
@@ -1024,10 +1068,23 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
             for (int e = 0; e < 4; ++e) pf[qb].set(4 * kb + e, __builtin_amdgcn_exp2f(s[kb][qb][e]));
           if constexpr (!kMfmaSum) lsum[r][qb] = psum8(pf[qb], kpf, lsum[r][qb]);
         }
+        if constexpr (kX3) {
+          Frag<bf16> vh[2], vl[2];
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 2; ++db) split_x3(vf[db], vh[db], vl[db]);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+          for (int qb = 0; qb < QB; ++qb) {
+            Frag<bf16> ph, pl;
+            split_x3(pf[qb], ph, pl);
+#pragma unroll
+            for (int db = 0; db < 2; ++db) mma_x3(o[r][db][qb], vh[db], vl[db], ph, pl);
+          }
+        } else {
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) mma(o[r][db][qb], vf[db], pf[qb]);
+        }
         if constexpr (kMfmaSum) {
           // lane (g, r16) ends with the sum for query r16 in every slot
 #pragma unroll
@@ -1841,9 +1898,10 @@ int check_triatt(const odde_triatt_args* a) {
   if (a->batch < 0) return set_error(ODDE_EINVAL, "triatt: batch must be >= 0");
   if (a->head_dim != 32) return set_error(ODDE_EUNSUPPORTED, "triatt: head_dim must be 32");
   if (a->heads > 16) return set_error(ODDE_EUNSUPPORTED, "triatt: at most 16 heads");
-  if (!valid_dtype(a->z_dtype) || !valid_dtype(a->compute_dtype))
+  if (!valid_dtype(a->z_dtype) ||
+      !(valid_dtype(a->compute_dtype) || a->compute_dtype == ODDE_F32X3))
     return set_error(ODDE_EINVAL, "triatt: bad dtype");
-  if (a->z_dtype == ODDE_BF16 && a->compute_dtype == ODDE_F32)
+  if (a->z_dtype == ODDE_BF16 && a->compute_dtype != ODDE_BF16)
     return set_error(ODDE_EUNSUPPORTED, "triatt: bf16 storage with f32 compute");
   return ODDE_OK;
 }
@@ -1956,8 +2014,18 @@ template <typename CT, int R, int QB, int RG, int QS>
 void launch_core_t(const TriattCoreArgs<CT>& p, hipStream_t st) {
   constexpr int R_WG = R * RG, Q_WG = 16 * QB * QS;
   const int nx = (p.jp + Q_WG - 1) / Q_WG, ny = (p.rows + R_WG - 1) / R_WG;
-  hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>),
-                     dim3((unsigned)(nx * ny * p.heads)), dim3(64 * RG * QS), 0, st, p, nx, ny);
+  bool done = false;
+  if constexpr (sizeof(CT) == 4 && QB == 2 && QS == 4 && ((R == 2 && RG == 2) || (R == 1 && RG == 1))) {
+    // the three-part form at the f32 default tiles (whole and batched)
+    if (p.x3) {
+      hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS, true>),
+                         dim3((unsigned)(nx * ny * p.heads)), dim3(64 * RG * QS), 0, st, p, nx, ny);
+      done = true;
+    }
+  }
+  if (!done)
+    hipLaunchKernelGGL((triatt_core_fast_kernel<CT, R, QB, RG, QS>),
+                       dim3((unsigned)(nx * ny * p.heads)), dim3(64 * RG * QS), 0, st, p, nx, ny);
   // the exact core keeps a modest tile; each wave loops over up to 8 query
   // blocks of one row (it does work only for rows the fast core flagged)
   dim3 grid2((p.jp + 255) / 256, (p.rows + 3) / 4, p.heads);
@@ -2094,6 +2162,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
 
   TriattCoreArgs<CT> c;
   fill_core_args(c, ws.c);
+  c.x3 = a->compute_dtype == ODDE_F32X3;
   c.gate = ws_path ? nullptr : static_cast<const CT*>(ws.gate);  // else gated in triatt_out_ws
   c.out = static_cast<CT*>(ws.o);
   c.o_row = (int64_t)jp * HD; c.o_h = 32; c.o_j = HD;
@@ -2169,7 +2238,7 @@ int odde_triatt_fwd(const odde_triatt_args* a, void* stream) {
     e.z = static_cast<const char*>(a->z) + (int64_t)b * a->z_sb * zes;
     e.out = static_cast<char*>(a->out) + (int64_t)b * a->out_sb * zes;
     e.mask = a->mask ? a->mask + (int64_t)b * a->mask_sb : nullptr;
-    if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) rc = run_triatt<float, float>(&e, st);
+    if (a->z_dtype == ODDE_F32 && a->compute_dtype != ODDE_BF16) rc = run_triatt<float, float>(&e, st);
     else if (a->z_dtype == ODDE_F32) rc = run_triatt<float, bf16>(&e, st);
     else rc = run_triatt<bf16, bf16>(&e, st);
     if (rc) return rc;

@@ -249,6 +249,14 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     ``add_residual`` the result is z + update, written to ``out`` (which may
     be z itself for an in-place update); otherwise ``out`` receives the
     update.  Returns ``out``.
+
+    fp32 arithmetic with ``torch.backends.cuda.matmul.allow_tf32`` set (the
+    reference's inference default, ``enable_tf32``) runs the attention
+    core's products on the bf16 MFMA in three parts (each operand as a bf16
+    pair; about 2^-16 of relative error per product, against TF32's 2^-11),
+    the way the reference's kernel slot takes its TF32 mode from that flag
+    (opendde/model/triangular/triangular.py:55-56).  Otherwise the products
+    are true fp32.
     """
     _require_gpu(z, mask)
     zb, nbatch, z_sb = _batch_view(z, "z")
@@ -281,6 +289,8 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     a.struct_size = ctypes.sizeof(_lib.TriattArgs)
     a.n, a.c, a.heads, a.head_dim = n, c, heads, HEAD_DIM
     a.z_dtype, a.compute_dtype = dtype_code(z.dtype), dtype_code(ct)
+    if a.compute_dtype == _lib.F32 and torch.backends.cuda.matmul.allow_tf32:
+        a.compute_dtype = _lib.F32X3
     a.add_residual = 1 if add_residual else 0
     a.z, a.z_s0, a.z_s1 = _ptr(z), zs0, zs1
     a.mask, a.mask_s0, a.mask_s1 = _ptr(m), ms0, ms1

@@ -1,0 +1,138 @@
+"""fp32 triangle attention with reduced-precision products allowed.
+
+With ``torch.backends.cuda.matmul.allow_tf32`` set (the reference's inference
+default: ``enable_tf32``, opendde/config/model_base.py:35, applied at
+opendde/model/opendde.py:106), fp32 triangle attention runs its core's
+products on the bf16 MFMA in three parts: each operand as a bf16 pair
+hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation (about 2^-16 of
+relative error per product, against TF32's 2^-11).  The projections, the
+softmax, the exact fallback rows and the output stay fp32.
+
+Checks: the fp32 tier's bar (max-abs <= 1e-4) against the fp32 oracle, and
+output bits that differ from the true-fp32 products' (so the three-part form
+did run).
+"""
+
+import pytest
+import torch
+
+from helpers import assert_fp32, margin, params_of, say, seeded, token_pair_mask
+from oracle import reference as ref
+from opendde_amd import workload as wl
+from opendde_amd.pairformer import PairformerBlock
+from opendde_amd.triangular import TriangleAttention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+STD = 0.1
+
+
+def _tf32(t: torch.Tensor) -> torch.Tensor:
+    """t rounded to TF32 (10 stored mantissa bits, nearest)."""
+    i = t.float().contiguous().view(torch.int32)
+    return ((i + 0x1000) & ~0x1FFF).view(torch.float32)
+
+
+def _tf32_core(q, k, v, biases):
+    """The oracle's attention core with the reference's TF32 mode: each
+    matmul's operands rounded to TF32 (softmax and accumulation in fp32)."""
+    a = torch.matmul(_tf32(q), _tf32(k).transpose(-1, -2))
+    for b in biases:
+        a = a + b
+    a = torch.softmax(a, dim=-1)
+    return torch.matmul(_tf32(a), _tf32(v))
+
+
+def _run(mod, z, mask, tf32):
+    old = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = tf32
+    try:
+        with torch.no_grad():
+            return mod(z, mask, triangle_attention="hip")
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = old
+
+
+@pytest.mark.parametrize("c,h", [(128, 4), (64, 2), (256, 8), (384, 12)])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("n", [17, 65, 130])
+def test_three_part_core_matches_fp32_oracle(c, h, starting, n, monkeypatch):
+    """Against the fp32 oracle: within the fp32 tier's bar (max-abs 1e-4), or,
+    where the weights are scaled up so that logits reach tens of nats (c 384,
+    12 heads), at least 8x closer to it than the reference's own TF32 mode
+    (the oracle with its core's matmul operands rounded to TF32)."""
+    say(f"[gpu] three-part core c={c} h={h} n={n} start={starting}")
+    mod = seeded(TriangleAttention(c, 32, h, starting=starting), 900 + c + h + n, STD)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(n + c))
+    mask = token_pair_mask(n, max(1, n // 10), seed=n, random=True)
+    exp = ref.triangle_attention(z, mask, params_of(mod), h, starting=starting)
+    monkeypatch.setattr(ref, "attention_core", _tf32_core)
+    tf = ref.triangle_attention(z, mask, params_of(mod), h, starting=starting)
+    monkeypatch.undo()
+    mod = mod.to(DEV)
+    got = _run(mod, z.to(DEV), mask.to(DEV), True)
+    exact = _run(mod, z.to(DEV), mask.to(DEV), False)
+    err = float((got.double().cpu() - exp.double()).abs().max())
+    err_tf32 = float((tf.double() - exp.double()).abs().max())
+    what = f"triatt three-part c={c} h={h} n={n} start={starting}"
+    say(f"    {what}: max-abs {err:.3e} (reference TF32 mode {err_tf32:.3e})")
+    margin(f"{what} (reference TF32 mode: {err_tf32:.3e})", max_abs=err, bar=1e-4)
+    assert torch.isfinite(got).all()
+    assert err <= max(1e-4, err_tf32 / 8), f"{what}: {err:.3e} against TF32 {err_tf32:.3e}"
+    assert not torch.equal(got, exact), "the three-part form did not run"
+
+
+def test_three_part_core_exact_rows():
+    # large logits (the fast path's overflow bound fails: exact rows) and
+    # fully masked rows (mean of v), as in the fp32 tests
+    n, pad = 72, 7
+    mod = seeded(TriangleAttention(128, 32, 4), 31, 0.6)
+    z = torch.randn(n, n, 128, generator=torch.Generator().manual_seed(32))
+    mask = token_pair_mask(n, pad)
+    exp = ref.triangle_attention(z, mask, params_of(mod), 4)
+    got = _run(mod.to(DEV), z.to(DEV), mask.to(DEV), True)
+    r = float((got[: n - pad].double().cpu() - exp[: n - pad].double()).abs().max() /
+              exp[: n - pad].double().abs().max())
+    say(f"    large-logit rel max err {r:.2e}")
+    assert torch.isfinite(got).all() and r < 1e-3
+    mod2 = seeded(TriangleAttention(128, 32, 4), 35, STD)
+    z2 = torch.randn(40, 40, 128, generator=torch.Generator().manual_seed(36))
+    mask2 = token_pair_mask(40, 5)
+    exp2 = ref.triangle_attention(z2, mask2, params_of(mod2), 4)
+    got2 = _run(mod2.to(DEV), z2.to(DEV), mask2.to(DEV), True)
+    assert_fp32(got2, exp2, "three-part fully masked rows")
+
+
+@pytest.mark.timeout(300)
+def test_three_part_block_n1024_matches_fp32_oracle():
+    """One N=1024 trunk block (51 random pads, c_s 384) in fp32 arithmetic
+    with reduced-precision products allowed, against the oracle run in fp32
+    on the GPU with TF32 off."""
+    cfg = wl.TRUNK_N1024
+    z0, s0, mask, gen = wl.make_inputs(cfg)
+    blk = PairformerBlock(n_heads=cfg.n_heads_single, c_z=cfg.c_z, c_s=cfg.c_s,
+                          c_hidden_mul=cfg.c_hidden_mul, c_hidden_pair_att=cfg.head_dim,
+                          no_heads_pair=cfg.heads)
+    wl.init_module_(blk, gen)
+    blk = blk.eval().to(DEV)
+    z0, s0, mask = z0.to(DEV), s0.to(DEV), mask.to(DEV)
+    params = {k: v.detach().float() for k, v in blk.named_parameters()}
+    old = torch.backends.cuda.matmul.allow_tf32
+    try:
+        torch.backends.cuda.matmul.allow_tf32 = False
+        with torch.no_grad():
+            sr, zr = ref.pairformer_block(s0, z0.clone(), mask, params, no_heads_pair=cfg.heads,
+                                          n_heads=cfg.n_heads_single, chunk_size=64)
+        torch.backends.cuda.matmul.allow_tf32 = True
+        with torch.no_grad():
+            sh, zh = blk(s0, z0.clone(), mask, triangle_multiplicative="hip",
+                         triangle_attention="hip", inplace_safe=True)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = old
+    dz = float((zh.double() - zr.double()).abs().max())
+    ds = float((sh.double() - sr.double()).abs().max())
+    say(f"    three-part N=1024 block: z max-abs {dz:.3e}, s max-abs {ds:.3e}")
+    margin("three-part fp32 block n1024 z", max_abs=dz, bar=1e-4)
+    margin("three-part fp32 block n1024 s", max_abs=ds, bar=1e-4)
+    assert torch.isfinite(zh).all() and torch.isfinite(sh).all()
+    assert dz <= 1e-4 and ds <= 1e-4
