@@ -30,10 +30,11 @@ extern "C" {
 #define ODDE_F32 0
 #define ODDE_BF16 1
 #define ODDE_F16 2 /* LayerNorm entry points only */
-/* compute_dtype of odde_triatt_fwd: f32 data and weights, the attention
- * core's products on the bf16 MFMA in three parts (each operand as a bf16
- * pair hi + lo; hi*hi + hi*lo + lo*hi, f32 accumulation; about 2^-16 of
- * relative error per product).  The f32 mode for callers that allow reduced-
+/* compute_dtype of odde_triatt_fwd and odde_trimul_fwd: f32 data and
+ * weights, the attention core's and the triangle contraction's products on
+ * the bf16 MFMA in three parts (each operand as a bf16 pair hi + lo;
+ * hi*hi + hi*lo + lo*hi, f32 accumulation; about 2^-16 of relative error
+ * per product; the contraction where Np is a multiple of 256).  The f32 mode for callers that allow reduced-
  * precision products: the reference's kernel slot takes TF32 (2^-11) from
  * torch.backends.cuda.matmul.allow_tf32 (opendde/model/triangular/
  * triangular.py:55-56), which its inference default enables

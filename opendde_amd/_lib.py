@@ -21,7 +21,8 @@ LIB_PATH = os.environ.get("OPENDDE_AMD_LIB", os.path.join(HERE, "lib", "libopend
 ABI_VERSION = 1
 
 F32, BF16, F16 = 0, 1, 2
-# triangle attention: f32 data, the core's products as three bf16 parts
+# triangle modules: f32 data, the attention core's and the contraction's
+# products as three bf16 parts
 F32X3 = 3
 K_TRIATT_PROJ, K_TRIATT_CORE, K_TRIATT_OUT = 0, 1, 2
 K_TRIMUL_PROJ, K_TRIMUL_CONTRACT, K_TRIMUL_OUT = 3, 4, 5

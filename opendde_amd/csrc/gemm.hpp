@@ -166,9 +166,13 @@ __device__ __forceinline__ void gemm_nt_mainloop(
 // stage s+1's half 0 under half 1's.  The one barrier per stage sits between
 // the halves, when every wave holds all of stage s in registers: it frees
 // buffer s % 2 for stage s+2 and publishes stage s+1.
-template <int TX, int TY, int WX, bool kPairCols, typename ARow, typename BRow>
-__device__ __forceinline__ void gemm_nt_mainloop_pipe64(
-    ARow arow, BRow brow, int K, bf16* sm,
+// General form: `nst` stages of 64 k, and koff(is_b, st) the element offset
+// of stage st within a row of A (is_b false) or B (a uniform value), so the k
+// walk may revisit or skip parts of a row (the three-part fp32 contraction
+// walks [hi | hi | lo] of A against [hi | lo | hi] of B).
+template <int TX, int TY, int WX, bool kPairCols, typename ARow, typename BRow, typename KOff>
+__device__ __forceinline__ void gemm_nt_mainloop_pipe64_k(
+    ARow arow, BRow brow, int nst, KOff koff, bf16* sm,
     f32x4 (&acc)[GemmShape<TX, TY, WX, 64>::MX][GemmShape<TX, TY, WX, 64>::MY]) {
   constexpr int KC = 64, NS = 2;
   using S = GemmShape<TX, TY, WX, KC>;
@@ -192,7 +196,7 @@ __device__ __forceinline__ void gemm_nt_mainloop_pipe64(
       const bool isb = op >= OPS_A;
       const int blk = isb ? w * S::OPS_B + (op - OPS_A) : w * OPS_A + op;
       __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(src0[op] + st * KC),
+          (const __attribute__((address_space(1))) void*)(src0[op] + koff(isb, st)),
           (__attribute__((address_space(3))) void*)(base + (isb ? TX * KC : 0) + blk * 512),
           16, 0, 0);
     }
@@ -238,7 +242,6 @@ __device__ __forceinline__ void gemm_nt_mainloop_pipe64(
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
-  const int nst = K / KC;
   issue(0);
   if (nst > 1) {
     issue(1);
@@ -264,6 +267,15 @@ __device__ __forceinline__ void gemm_nt_mainloop_pipe64(
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   barrier_nofence();
+}
+
+// K contiguous per row: stage st at k = 64 st.
+template <int TX, int TY, int WX, bool kPairCols, typename ARow, typename BRow>
+__device__ __forceinline__ void gemm_nt_mainloop_pipe64(
+    ARow arow, BRow brow, int K, bf16* sm,
+    f32x4 (&acc)[GemmShape<TX, TY, WX, 64>::MX][GemmShape<TX, TY, WX, 64>::MY]) {
+  gemm_nt_mainloop_pipe64_k<TX, TY, WX, kPairCols>(
+      arow, brow, K / 64, [](bool, int st) { return st * 64; }, sm, acc);
 }
 
 }  // namespace odde

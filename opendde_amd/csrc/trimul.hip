@@ -50,8 +50,10 @@ struct TrimulProjArgs {
 // Wave w of a workgroup owns pair rows (x, y0 + 16 w .. + 15) for kRB
 // consecutive first indices x: every weight fragment it reads from L2 serves
 // kRB row blocks (the fp32 form, whose weights are too large to hold, is
-// bound by those reads).
-template <typename ZT, typename CT, int kC, int kRB = 1>
+// bound by those reads).  kX3 (f32 compute, ODDE_F32X3): A and B are written
+// as bf16 rows of 2 Np, [hi | lo] with hi = bf16(a) and lo = bf16(a - hi),
+// for the three-part contraction.
+template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
@@ -101,15 +103,33 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       const int x_ = blockIdx.y * kRB + rb;
-      const size_t off = ((size_t)c * np + x_) * np + yb;
       float va[4], vb[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         va[r] = mk[rb][r] * sigmoidf_(ag[rb][r]) * ap[rb][r];
         vb[r] = mk[rb][r] * sigmoidf_(bg[rb][r]) * bp[rb][r];
       }
-      store4(a.A + off, va[0], va[1], va[2], va[3]);
-      store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
+      if constexpr (kX3) {
+        const size_t off = ((size_t)c * np + x_) * 2 * np + yb;
+        bf16x4 ha, la, hb, lb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ha[r] = (bf16)va[r];
+          la[r] = (bf16)(va[r] - (float)ha[r]);
+          hb[r] = (bf16)vb[r];
+          lb[r] = (bf16)(vb[r] - (float)hb[r]);
+        }
+        bf16* A16 = reinterpret_cast<bf16*>(a.A) + off;
+        bf16* B16 = reinterpret_cast<bf16*>(a.B) + off;
+        *reinterpret_cast<bf16x4*>(A16) = ha;
+        *reinterpret_cast<bf16x4*>(A16 + np) = la;
+        *reinterpret_cast<bf16x4*>(B16) = hb;
+        *reinterpret_cast<bf16x4*>(B16 + np) = lb;
+      } else {
+        const size_t off = ((size_t)c * np + x_) * np + yb;
+        store4(a.A + off, va[0], va[1], va[2], va[3]);
+        store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
+      }
     }
   }
 }
@@ -298,6 +318,64 @@ inline void launch_contract_big(const ContractArgs<bf16>& k, int np, int ch, hip
     hipLaunchKernelGGL((trimul_contract_big_kernel<256, 128, 4, 3, 32>), dim3(tiles * ch), dim3(512),
                        0, st, k);
   }
+}
+
+// Three-part fp32 contraction (ODDE_F32X3): A and B rows of 2 Np bf16,
+// [hi | lo]; P = A_hi B_hi^T + A_hi B_lo^T + A_lo B_hi^T as one NT GEMM over
+// k = 3 Np, whose walk visits hi, hi, lo of each A row against hi, lo, hi of
+// each B row (256 x 256 tiles, the pipelined 64-k mainloop); P in fp32.
+__global__ __launch_bounds__(512) void trimul_contract_x3_kernel(ContractArgs<bf16> a, float* P) {
+  constexpr int TX = 256, TY = 256, WX = 4;
+  using S = GemmShape<TX, TY, WX, 64>;
+  __shared__ __attribute__((aligned(16))) bf16 sm[2 * S::STAGE_ELEMS];
+  const int TXn = a.np / TX, TYn = a.np / TY;
+  const int tiles = TXn * TYn;
+  int bid = blockIdx.x, c, tile;
+  if ((a.ch & 7) == 0) {  // all tiles of a channel on one XCD
+    const int xcd = bid & 7, local = bid >> 3;
+    c = (local / tiles) * 8 + xcd;
+    tile = local % tiles;
+  } else {
+    c = bid / tiles;
+    tile = bid % tiles;
+  }
+  const int x0 = (tile / TYn) * TX, y0 = (tile % TYn) * TY;
+  const int ld = 2 * a.np;
+  const size_t plane = (size_t)a.np * ld;
+  f32x4 acc[S::MX][S::MY];
+  const bf16* Ab = a.A + c * plane + (size_t)x0 * ld;
+  const bf16* Bb = a.B + c * plane + (size_t)y0 * ld;
+  // B rows staged in the paired-row order of trimul_contract_big_kernel
+  auto arow = [&](int r) { return Ab + (size_t)r * ld; };
+  auto brow = [&](int r) {
+    const int m = r & 15;
+    return Bb + (size_t)((r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * ld;
+  };
+  const int nst0 = a.np / 64;
+  auto koff = [nst0](bool isb, int st) {
+    const int seg = st / nst0, k = st - seg * nst0;
+    return (k + ((isb ? seg == 1 : seg == 2) ? nst0 : 0)) * 64;
+  };
+  gemm_nt_mainloop_pipe64_k<TX, TY, WX, true>(arow, brow, 3 * nst0, koff, sm, acc);
+  // lane: row xx, columns y + 8g .. + 7 (row blocks j, j + 1) and
+  // y + 32 + 8g .. + 7 (row blocks j + 2, j + 3)
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int wx = w % WX, wy = w / WX;
+  float* Pb = P + (size_t)c * a.np * a.np;
+#pragma unroll
+  for (int i = 0; i < S::MX; ++i)
+#pragma unroll
+    for (int j = 0; j < S::MY; j += 4) {
+      const int xx = x0 + wx * (TX / WX) + i * 16 + r16;
+      float* row = Pb + (size_t)xx * a.np + y0 + wy * (TY / S::WY) + j * 16;
+      store4(row + 8 * g, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      store4(row + 8 * g + 4, acc[i][j + 1][0], acc[i][j + 1][1], acc[i][j + 1][2],
+             acc[i][j + 1][3]);
+      store4(row + 32 + 8 * g, acc[i][j + 2][0], acc[i][j + 2][1], acc[i][j + 2][2],
+             acc[i][j + 2][3]);
+      store4(row + 32 + 8 * g + 4, acc[i][j + 3][0], acc[i][j + 3][1], acc[i][j + 3][2],
+             acc[i][j + 3][3]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1011,11 +1089,20 @@ int check_trimul(const odde_trimul_args* a) {
   if (a->batch < 0) return set_error(ODDE_EINVAL, "trimul: batch must be >= 0");
   if (!kdim(a->c) || !kdim(a->c_hidden))
     return set_error(ODDE_EUNSUPPORTED, "trimul: c and c_hidden must be 64, 128, 256 or 384");
-  if (!valid_dtype(a->z_dtype) || !valid_dtype(a->compute_dtype))
+  if (!valid_dtype(a->z_dtype) ||
+      !(valid_dtype(a->compute_dtype) || a->compute_dtype == ODDE_F32X3))
     return set_error(ODDE_EINVAL, "trimul: bad dtype");
-  if (a->z_dtype == ODDE_BF16 && a->compute_dtype == ODDE_F32)
+  if (a->z_dtype == ODDE_BF16 && a->compute_dtype != ODDE_BF16)
     return set_error(ODDE_EUNSUPPORTED, "trimul: bf16 storage with f32 compute");
   return ODDE_OK;
+}
+
+// the three-part form's projection (f32 compute, A and B as [hi | lo] rows)
+template <typename ZT, int kC>
+void launch_tp_x3(const TrimulProjArgs<ZT, float>& p, hipStream_t st) {
+  constexpr int kRB = kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
+  dim3 grid(p.np / 64, p.np / kRB);
+  hipLaunchKernelGGL((trimul_proj_kernel<ZT, float, kC, kRB, true>), grid, dim3(256), 0, st, p);
 }
 
 template <typename ZT, typename CT, int kC>
@@ -1114,9 +1201,23 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   p.wg = static_cast<const CT*>(a->g_in_weight);
   p.A = static_cast<CT*>(ws.A); p.B = static_cast<CT*>(ws.B);
   p.n = n; p.np = np; p.ch = ch; p.eps = a->eps;
+  // the three-part fp32 form where its contraction tiles fit (Np a multiple
+  // of 256); otherwise true fp32 products
+  const bool x3 = sizeof(CT) == 4 && a->compute_dtype == ODDE_F32X3 && np % 256 == 0;
   {
     LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
-    if (!launch_tp_ws<ZT, CT>(p, C, ch, st)) {
+    if constexpr (sizeof(CT) == 4) {
+      if (x3) {
+        switch (C) {
+          case 64: launch_tp_x3<ZT, 2>(p, st); break;
+          case 128: launch_tp_x3<ZT, 4>(p, st); break;
+          case 256: launch_tp_x3<ZT, 8>(p, st); break;
+          case 384: launch_tp_x3<ZT, 12>(p, st); break;
+        }
+      }
+    }
+    if (x3) {
+    } else if (!launch_tp_ws<ZT, CT>(p, C, ch, st)) {
       switch (C) {
         case 64: launch_tp<ZT, CT, 2>(p, st); break;
         case 128: launch_tp<ZT, CT, 4>(p, st); break;
@@ -1132,7 +1233,14 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   k.A = p.A; k.B = p.B; k.P = static_cast<CT*>(ws.P); k.np = np; k.ch = ch;
   {
     LaunchScope ls(ODDE_K_TRIMUL_CONTRACT, st);
-    if constexpr (sizeof(CT) == 2) {
+    if (x3) {
+      ContractArgs<bf16> kb;
+      kb.A = static_cast<const bf16*>(ws.A); kb.B = static_cast<const bf16*>(ws.B);
+      kb.P = nullptr; kb.np = np; kb.ch = ch;
+      const int tiles = (np / 256) * (np / 256);
+      hipLaunchKernelGGL(trimul_contract_x3_kernel, dim3(tiles * ch), dim3(512), 0, st, kb,
+                         static_cast<float*>(ws.P));
+    } else if constexpr (sizeof(CT) == 2) {
       if (np % 256 == 0) {
         launch_contract_big(k, np, ch, st);
       } else {
@@ -1218,7 +1326,7 @@ int odde_trimul_fwd(const odde_trimul_args* a, void* stream) {
     e.z = static_cast<const char*>(a->z) + (int64_t)b * a->z_sb * zes;
     e.out = static_cast<char*>(a->out) + (int64_t)b * a->out_sb * zes;
     e.mask = a->mask ? a->mask + (int64_t)b * a->mask_sb : nullptr;
-    if (a->z_dtype == ODDE_F32 && a->compute_dtype == ODDE_F32) rc = run_trimul<float, float>(&e, st);
+    if (a->z_dtype == ODDE_F32 && a->compute_dtype != ODDE_BF16) rc = run_trimul<float, float>(&e, st);
     else if (a->z_dtype == ODDE_F32) rc = run_trimul<float, bf16>(&e, st);
     else rc = run_trimul<bf16, bf16>(&e, st);
     if (rc) return rc;

@@ -319,7 +319,11 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
     same ``out`` / ``add_residual`` contract as :func:`triangle_attention`.
     ``p_in_weight``/``g_in_weight`` are [2*Ch, C] (a rows then b rows).
     ``f32_out_weight``: with bf16 compute, also hand the library linear_z in
-    f32 (it folds LN_out into that weight with a single bf16 rounding)."""
+    f32 (it folds LN_out into that weight with a single bf16 rounding).
+    fp32 arithmetic with ``torch.backends.cuda.matmul.allow_tf32`` set runs
+    the contraction's products in three bf16 parts, as
+    :func:`triangle_attention` does its core's (where Np is a multiple of
+    256; true fp32 products otherwise)."""
     _require_gpu(z, mask)
     zb, nbatch, z_sb = _batch_view(z, "z")
     n, c = z.shape[-3], z.shape[-1]
@@ -344,6 +348,8 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
     a.struct_size = ctypes.sizeof(_lib.TrimulArgs)
     a.n, a.c, a.c_hidden = n, c, ch
     a.z_dtype, a.compute_dtype = dtype_code(z.dtype), dtype_code(ct)
+    if a.compute_dtype == _lib.F32 and torch.backends.cuda.matmul.allow_tf32:
+        a.compute_dtype = _lib.F32X3
     a.outgoing = 1 if outgoing else 0
     a.add_residual = 1 if add_residual else 0
     a.z, a.z_s0, a.z_s1 = _ptr(z), zb.stride(1), zb.stride(2)

@@ -136,3 +136,55 @@ def test_three_part_block_n1024_matches_fp32_oracle():
     margin("three-part fp32 block n1024 s", max_abs=ds, bar=1e-4)
     assert torch.isfinite(zh).all() and torch.isfinite(sh).all()
     assert dz <= 1e-4 and ds <= 1e-4
+
+
+def _tf32_combine(a, b, outgoing):
+    """The oracle's contraction with the reference's TF32 mode: a and b
+    rounded to TF32 before the sum over k (accumulated in fp32)."""
+    return _orig_combine(_tf32(a), _tf32(b), outgoing)
+
+
+_orig_combine = ref.combine_projections
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("n,c,ch", [(256, 128, 128), (250, 64, 128), (512, 128, 128),
+                                    (300, 128, 128)])
+def test_three_part_contraction_matches_fp32_oracle(outgoing, n, c, ch, monkeypatch):
+    """fp32 triangle multiplication with TF32 allowed: the contraction's
+    products in three bf16 parts where Np (n rounded up to 128) is a multiple
+    of 256 (n 250, 256, 512), true fp32 products otherwise (n 300: Np 384,
+    bit-identical to TF32 off).  Within the fp32 tier's bar of the fp32
+    oracle, or at least 8x closer to it than the reference's TF32 mode."""
+    from opendde_amd.triangular import (TriangleMultiplicationIncoming,
+                                        TriangleMultiplicationOutgoing)
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(c, ch), 950 + n + c + ch, STD)
+    z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(n + 7))
+    mask = token_pair_mask(n, max(1, n // 10), seed=n + 1, random=True)
+    exp = ref.triangle_multiplication(z, mask, params_of(mod), outgoing=outgoing)
+    monkeypatch.setattr(ref, "combine_projections", _tf32_combine)
+    tf = ref.triangle_multiplication(z, mask, params_of(mod), outgoing=outgoing)
+    monkeypatch.undo()
+    mod = mod.to(DEV)
+    res = []
+    for tf32 in (True, False):
+        old = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+        try:
+            with torch.no_grad():
+                res.append(mod(z.to(DEV), mask.to(DEV), triangle_multiplicative="hip"))
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = old
+    got, exact = res
+    err = float((got.double().cpu() - exp.double()).abs().max())
+    err_tf32 = float((tf.double() - exp.double()).abs().max())
+    what = f"trimul three-part n={n} c={c} ch={ch} out={outgoing}"
+    say(f"    {what}: max-abs {err:.3e} (reference TF32 mode {err_tf32:.3e})")
+    margin(f"{what} (reference TF32 mode: {err_tf32:.3e})", max_abs=err, bar=1e-4)
+    assert torch.isfinite(got).all()
+    assert err <= max(1e-4, err_tf32 / 8), f"{what}: {err:.3e} against TF32 {err_tf32:.3e}"
+    if (n + 127) // 128 * 128 % 256 == 0:
+        assert not torch.equal(got, exact), "the three-part form did not run"
+    else:
+        assert torch.equal(got, exact), "Np not a multiple of 256 takes true fp32 products"
