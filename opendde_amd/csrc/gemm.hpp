@@ -170,35 +170,62 @@ __device__ __forceinline__ void gemm_nt_mainloop(
 // of stage st within a row of A (is_b false) or B (a uniform value), so the k
 // walk may revisit or skip parts of a row (the three-part fp32 contraction
 // walks [hi | hi | lo] of A against [hi | lo | hi] of B).
-template <int TX, int TY, int WX, bool kPairCols, typename ARow, typename BRow, typename KOff>
+//
+// With kBuf the direct loads go through buffer resources based at bufs.a /
+// bufs.b (uniform pointers; every A row pointer arow(r) lies within
+// bufs.a_bytes of bufs.a, likewise for B): each lane keeps one 32-bit byte
+// offset per load, the k advance is the uniform offset and the LDS
+// destinations are uniform, so a stage's loads issue no vector instructions
+// (the 64-bit form spends a 64-bit add, a v_readfirstlane for M0 and an
+// offset add per load).
+struct GemmBufs {
+  const bf16* a = nullptr;
+  uint32_t a_bytes = 0;
+  const bf16* b = nullptr;
+  uint32_t b_bytes = 0;
+};
+template <int TX, int TY, int WX, bool kPairCols, bool kBuf = false, typename ARow, typename BRow,
+          typename KOff>
 __device__ __forceinline__ void gemm_nt_mainloop_pipe64_k(
     ARow arow, BRow brow, int nst, KOff koff, bf16* sm,
-    f32x4 (&acc)[GemmShape<TX, TY, WX, 64>::MX][GemmShape<TX, TY, WX, 64>::MY]) {
+    f32x4 (&acc)[GemmShape<TX, TY, WX, 64>::MX][GemmShape<TX, TY, WX, 64>::MY],
+    GemmBufs bufs = GemmBufs{}) {
   constexpr int KC = 64, NS = 2;
   using S = GemmShape<TX, TY, WX, KC>;
   constexpr int MX = S::MX, MY = S::MY, OPS_A = S::OPS_A, OPS = S::OPS;
   constexpr int CPR = S::CPR, RPO = S::RPO;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int wx = w % WX, wy = w / WX;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
 
-  const bf16* src0[OPS];
+  const bf16* src0[kBuf ? 1 : OPS];
+  uint32_t voff[kBuf ? OPS : 1];
 #pragma unroll
   for (int op = 0; op < OPS; ++op) {
     const bool isb = op >= OPS_A;
     const int blk = isb ? w * S::OPS_B + (op - OPS_A) : w * OPS_A + op;
     const int row = blk * RPO + l / CPR;
-    src0[op] = (isb ? brow(row) : arow(row)) + gemm_swz<KC>(row, l % CPR) * 8;
+    const bf16* src = (isb ? brow(row) : arow(row)) + gemm_swz<KC>(row, l % CPR) * 8;
+    if constexpr (kBuf)
+      voff[op] = (uint32_t)((src - (isb ? bufs.b : bufs.a)) * (int64_t)sizeof(bf16));
+    else
+      src0[op] = src;
   }
   auto issue = [&](int st) {
     bf16* base = sm + (st % NS) * S::STAGE_ELEMS;
 #pragma unroll
     for (int op = 0; op < OPS; ++op) {
       const bool isb = op >= OPS_A;
-      const int blk = isb ? w * S::OPS_B + (op - OPS_A) : w * OPS_A + op;
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(src0[op] + koff(isb, st)),
-          (__attribute__((address_space(3))) void*)(base + (isb ? TX * KC : 0) + blk * 512),
-          16, 0, 0);
+      const int blk = isb ? wu * S::OPS_B + (op - OPS_A) : wu * OPS_A + op;
+      bf16* dst = base + (isb ? TX * KC : 0) + blk * 512;
+      if constexpr (kBuf) {
+        buffer_load_lds16(isb ? bufs.b : bufs.a, isb ? bufs.b_bytes : bufs.a_bytes, dst, voff[op],
+                          (uint32_t)koff(isb, st) * (uint32_t)sizeof(bf16));
+      } else {
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src0[op] + koff(isb, st)),
+            (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      }
     }
   };
 
@@ -255,6 +282,9 @@ __device__ __forceinline__ void gemm_nt_mainloop_pipe64_k(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // half 0 of stage st in registers
     read_half(I1{}, st, fsw1);
     mult(I0{});
+    // the wait below is ordered only against memory operations: keep the
+    // half's last MFMAs ahead of it, so they run while its reads land
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // all of stage st in registers
     if (st + 1 < nst) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage st+1

@@ -253,9 +253,16 @@ __global__ __launch_bounds__(512) void trimul_contract_big_kernel(ContractArgs<b
     const int m = r & 15;
     return Bb + (size_t)((r & ~31) + 8 * (m >> 2) + 4 * ((r >> 4) & 1) + (m & 3)) * a.np;
   };
-  if constexpr (kPipe)
-    gemm_nt_mainloop_pipe64<TX, TY, WX, true>(arow, brow, a.np, sm, acc);
-  else
+  if constexpr (kPipe) {
+    // buffer-resource loads based at the tile's first A and B rows
+    GemmBufs bufs;
+    bufs.a = Ab;
+    bufs.a_bytes = (uint32_t)((size_t)TX * a.np * sizeof(bf16));
+    bufs.b = Bb;
+    bufs.b_bytes = (uint32_t)((size_t)TY * a.np * sizeof(bf16));
+    gemm_nt_mainloop_pipe64_k<TX, TY, WX, true, true>(
+        arow, brow, a.np / 64, [](bool, int st) { return st * 64; }, sm, acc, bufs);
+  } else
     gemm_nt_mainloop<TX, TY, WX, NS, true, KC>(arow, brow, a.np, sm, acc);
   // acc[i][j]: column = row x (x0 + wx*TX/WX + 16i + r16); rows = columns
   // y0 + wy*TY/WY + 16 (j & ~1) + 8g + 4 (j & 1) + r
@@ -356,7 +363,12 @@ __global__ __launch_bounds__(512) void trimul_contract_x3_kernel(ContractArgs<bf
     const int seg = st / nst0, k = st - seg * nst0;
     return (k + ((isb ? seg == 1 : seg == 2) ? nst0 : 0)) * 64;
   };
-  gemm_nt_mainloop_pipe64_k<TX, TY, WX, true>(arow, brow, 3 * nst0, koff, sm, acc);
+  GemmBufs bufs;
+  bufs.a = Ab;
+  bufs.a_bytes = (uint32_t)((size_t)TX * ld * sizeof(bf16));
+  bufs.b = Bb;
+  bufs.b_bytes = (uint32_t)((size_t)TY * ld * sizeof(bf16));
+  gemm_nt_mainloop_pipe64_k<TX, TY, WX, true, true>(arow, brow, 3 * nst0, koff, sm, acc, bufs);
   // lane: row xx, columns y + 8g .. + 7 (row blocks j, j + 1) and
   // y + 32 + 8g .. + 7 (row blocks j + 2, j + 3)
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
