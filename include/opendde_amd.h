@@ -30,12 +30,15 @@ extern "C" {
 #define ODDE_F32 0
 #define ODDE_BF16 1
 #define ODDE_F16 2 /* LayerNorm entry points only */
-/* compute_dtype of odde_triatt_fwd and odde_trimul_fwd: f32 data and
- * weights, the attention core's and the triangle contraction's products on
- * the bf16 MFMA in three parts (each operand as a bf16 pair hi + lo;
- * hi*hi + hi*lo + lo*hi, f32 accumulation; about 2^-16 of relative error
- * per product; the contraction where Np is a multiple of 256).  The f32 mode for callers that allow reduced-
- * precision products: the reference's kernel slot takes TF32 (2^-11) from
+/* compute_dtype of odde_triatt_fwd, odde_trimul_fwd and odde_transition_fwd:
+ * f32 data and weights, the products on the bf16 MFMA in three parts (each
+ * operand as a bf16 pair hi + lo; hi*hi + hi*lo + lo*hi, f32 accumulation;
+ * about 2^-16 of relative error per product): every projection, the
+ * attention core, the outputs and the transition's GEMMs, and the triangle
+ * contraction where Np is a multiple of 256 (true fp32 products otherwise;
+ * the transition's pair-bias projection stays true fp32).  The f32 mode for
+ * callers that allow reduced-precision products: the reference's kernel
+ * slot and its linear layers take TF32 (2^-11) from
  * torch.backends.cuda.matmul.allow_tf32 (opendde/model/triangular/
  * triangular.py:55-56), which its inference default enables
  * (opendde/config/model_base.py:35, opendde/model/opendde.py:106). */
@@ -208,7 +211,7 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  * x, out: [rows][c] contiguous (out may alias x); W_a, W_b: [n*c][c],
  * W_o: [c][n*c] in compute_dtype; LN params f32.  c in {64, 128, 256, 384},
  * n = 4.  compute_dtype ODDE_BF16 takes f32 or bf16 rows; ODDE_F32 (true
- * fp32 products) takes f32 rows.
+ * fp32 products) and ODDE_F32X3 (three-part products) take f32 rows.
  * Optional (pb_heads = 16; 0 = off): the pair-bias projection that the single
  * track's AttentionPairBias takes from the updated pair tensor
  * (linear_nobias_z(layernorm_z(z)), opendde/model/modules/transformer.py:

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace odde {
 
 typedef __bf16 bf16;
@@ -100,6 +102,53 @@ __device__ __forceinline__ void mma(f32x4& acc, const Frag<float>& a, const Frag
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[2], b.hi[2], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[3], b.hi[3], acc, 0, 0, 0);
 }
+
+// An f32 fragment as a pair of bf16 fragments, x = hi + lo + O(2^-18 |x|):
+// hi = bf16(x) to nearest, lo = bf16(x - hi).  Products of two such pairs as
+// hi*hi + hi*lo + lo*hi on the bf16 MFMA (fp32 accumulation) carry ~2^-16 of
+// relative error: the three-part fp32 form (ODDE_F32X3), for callers that
+// allow reduced-precision fp32 products.  Same lane layout as Frag<float>
+// (lane l: row l % 16, k = 8 (l / 16) + e), so the accumulators of the two
+// forms match element for element.
+__device__ __forceinline__ void split_x3(const Frag<float>& f, Frag<bf16>& hi, Frag<bf16>& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = f.get(e);
+    const bf16 h = (bf16)x;
+    hi.v[e] = h;
+    lo.v[e] = (bf16)(x - (float)h);
+  }
+}
+__device__ __forceinline__ void mma_x3(f32x4& acc, const Frag<bf16>& ah, const Frag<bf16>& al,
+                                       const Frag<bf16>& bh, const Frag<bf16>& bl) {
+  mma(acc, al, bh);
+  mma(acc, ah, bl);
+  mma(acc, ah, bh);
+}
+struct FragX3 {
+  Frag<bf16> hi, lo;
+  __device__ __forceinline__ void zero() {
+    hi.zero();
+    lo.zero();
+  }
+  __device__ __forceinline__ void load(const float* p) {
+    Frag<float> f;
+    f.load(p);
+    split_x3(f, hi, lo);
+  }
+  __device__ __forceinline__ void from(const Frag<float>& f) { split_x3(f, hi, lo); }
+};
+__device__ __forceinline__ void mma(f32x4& acc, const FragX3& a, const FragX3& b) {
+  mma_x3(acc, a.hi, a.lo, b.hi, b.lo);
+}
+// The fragment type a kernel multiplies with: CT's own, or the three-part
+// pair for f32 data (kX3).
+template <typename CT, bool kX3>
+using MulFrag = typename std::conditional<kX3, FragX3, Frag<CT>>::type;
+// x as a multiplication fragment (a split for the three-part form)
+__device__ __forceinline__ void to_mul(const Frag<float>& f, FragX3& m) { m.from(f); }
+template <typename CT>
+__device__ __forceinline__ void to_mul(const Frag<CT>& f, Frag<CT>& m) { m = f; }
 
 // ----------------------------------------------------------------------------
 // small vector stores of 4 consecutive elements
@@ -350,6 +399,12 @@ __device__ __forceinline__ void load_w_frag(const CT* __restrict__ w, int ld, in
   const int g = lane_id() >> 4;
   if (o < n_out) f.load(w + (size_t)o * ld + 32 * t + 8 * g);
   else f.zero();
+}
+__device__ __forceinline__ void load_w_frag(const float* __restrict__ w, int ld, int o0, int n_out,
+                                            int t, FragX3& f) {
+  Frag<float> x;
+  load_w_frag(w, ld, o0, n_out, t, x);
+  f.from(x);
 }
 // bf16 weights as fp16 fragments (exact: fp16 holds every bf16 value of the
 // weights' range, |w| >= 2^-14, to more mantissa bits than bf16 has)

@@ -662,19 +662,27 @@ __global__ __launch_bounds__(256, 2) void transition_pipe_kernel(TransitionArgs<
 // workgroups (a.part set): each writes its partial 16 x C output to
 // a.part[blockIdx.y], and transition_f32_reduce_kernel adds the partials in
 // split order and the residual.
-template <typename ZT, int kC>
+// kX3 (ODDE_F32X3): the products in three bf16 parts (rows and hidden
+// activations split once, weight fragments as they are read).
+template <typename ZT, int kC, bool kX3 = false>
 __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, float> a,
                                                              int64_t nblk) {
   constexpr int C = kC * 32, HID = 4 * C, NCB = C / 16, NCHUNK = HID / kTrHid;
   static_assert(NCHUNK % 4 == 0, "hidden chunks split evenly over the 4 waves");
+  using MF = MulFrag<float, kX3>;
   __shared__ f32x4 part[3][NCB][64];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
     const int64_t row = b * 16 + r16;
     const bool valid = row < a.rows;
-    Frag<float> xf[kC];
-    ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
-                                   xf);
+    MF xf[kC];
+    {
+      Frag<float> xt[kC];
+      ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
+                                     xt);
+#pragma unroll
+      for (int t = 0; t < kC; ++t) to_mul(xt[t], xf[t]);
+    }
     f32x4 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -689,7 +697,7 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-          Frag<float> fa, fb;
+          MF fa, fb;
           load_w_frag(a.wa, C, h0 + 16 * hb, HID, t, fa);
           load_w_frag(a.wb, C, h0 + 16 * hb, HID, t, fb);
           mma(sa, fa, xf[t]);
@@ -698,6 +706,8 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
 #pragma unroll
         for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
       }
+      MF hm;
+      to_mul(hf, hm);
       // GEMM2: W_o[c][h0 + slot] with the same slot -> hidden map
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
@@ -705,7 +715,9 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
         Frag<float> fo;
         fo.lo = *reinterpret_cast<const f32x4*>(wrow + 4 * g);
         fo.hi = *reinterpret_cast<const f32x4*>(wrow + 16 + 4 * g);
-        mma(acc[cb], fo, hf);
+        MF fm;
+        to_mul(fo, fm);
+        mma(acc[cb], fm, hm);
       }
     }
     if (w) {
@@ -778,10 +790,13 @@ struct TfStage {
   f32x4 wo[C * 8];           // [C][8 chunks of 4 hidden]
 };
 
-template <typename ZT, int kC, int kW>
+// kX3 (ODDE_F32X3): the products in three bf16 parts (rows and hidden
+// activations split once, weight fragments as they are read from LDS).
+template <typename ZT, int kC, int kW, bool kX3 = false>
 __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(TransitionArgs<ZT, float> a,
                                                                       int64_t ntiles) {
   constexpr int C = kC * 32, HID = 4 * C, NCB = C / 16, NCHUNK = HID / kTrHid;
+  using MF = MulFrag<float, kX3>;
   constexpr int CPR = C / 4;                 // 16-byte chunks per W_a / W_b row
   constexpr int NAB = kTrHid * CPR / 64;     // direct loads per W_a (W_b) chunk
   constexpr int NO = C * 8 / 64;             // direct loads per W_o chunk
@@ -830,9 +845,14 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t row = tile * (16 * kW) + 16 * w + r16;
     const bool valid = row < a.rows;
-    Frag<float> xf[kC];
-    ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
-                                   xf);
+    MF xf[kC];
+    {
+      Frag<float> xt[kC];
+      ln_rows_to_frags<ZT, float, C>(a.x + (valid ? row : 0) * C, valid, a.ln_w, a.ln_b, a.eps,
+                                     xt);
+#pragma unroll
+      for (int t = 0; t < kC; ++t) to_mul(xt[t], xf[t]);
+    }
     f32x4 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -856,12 +876,17 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
           fa.hi = S.wa[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
           fb.lo = S.wb[rr * CPR + ((8 * t + 2 * g) ^ key)];
           fb.hi = S.wb[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
-          mma(sa, fa, xf[t]);
-          mma(sb, fb, xf[t]);
+          MF ma, mb;
+          to_mul(fa, ma);
+          to_mul(fb, mb);
+          mma(sa, ma, xf[t]);
+          mma(sb, mb, xf[t]);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) hf.set(4 * hb + e, siluf_(sa[e]) * sb[e]);
       }
+      MF hm;
+      to_mul(hf, hm);
       // GEMM2: W_o[c][h0 + 4g .. + 3] and [h0 + 16 + 4g .. + 3] (chunks g, 4 + g)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
@@ -869,7 +894,9 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
         Frag<float> fo;
         fo.lo = S.wo[c * 8 + (g ^ key)];
         fo.hi = S.wo[c * 8 + ((4 + g) ^ key)];
-        mma(acc[cb], fo, hf);
+        MF mo;
+        to_mul(fo, mo);
+        mma(acc[cb], mo, hm);
       }
     }
     // epilogue: lane holds row r16 of the wave, channels 16 cb + 4g + e
@@ -1109,7 +1136,9 @@ int64_t transition_wide_rows(int64_t rows) {
 // the chunks per wave (4C / 32 / 4) that keeps the grid within 1024
 // workgroups.  1: no split.  Not with the pair-bias epilogue.
 int transition_f32_splits(const odde_transition_args* a) {
-  if (a->compute_dtype != ODDE_F32 || a->n_factor != 4 || a->pb_heads) return 1;
+  if ((a->compute_dtype != ODDE_F32 && a->compute_dtype != ODDE_F32X3) || a->n_factor != 4 ||
+      a->pb_heads)
+    return 1;
   if (a->c != 64 && a->c != 128 && a->c != 256 && a->c != 384) return 1;
   const int64_t nblk = (a->rows + 15) / 16;
   if (nblk >= 512 || nblk == 0) return 1;
@@ -1194,6 +1223,8 @@ int run_transition_wide(const odde_transition_args* a, hipStream_t st) {
   return check_launch("transition (wide)");
 }
 
+// kX3: the products in three bf16 parts (ODDE_F32X3)
+template <bool kX3>
 int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
   TransitionArgs<float, float> p;
   p.x = static_cast<const float*>(a->x);
@@ -1220,16 +1251,16 @@ int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
       const int64_t ntiles = (p.rows + 127) / 128;
       const int g2 = (int)std::min<int64_t>(ntiles, a->c == 64 ? 2 * 256 : 256);
       if (a->c == 64)
-        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 8>), dim3(g2), dim3(512), 0, st, p, ntiles);
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 8, kX3>), dim3(g2), dim3(512), 0, st, p, ntiles);
       else
-        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 8>), dim3(g2), dim3(512), 0, st, p, ntiles);
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 8, kX3>), dim3(g2), dim3(512), 0, st, p, ntiles);
     } else {  // 4 waves (64 rows) per workgroup: more workgroups for fewer rows
       const int64_t ntiles = (p.rows + 63) / 64;
       const int g2 = (int)std::min<int64_t>(ntiles, a->c == 64 ? 3 * 256 : 256);
       if (a->c == 64)
-        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 4>), dim3(g2), dim3(256), 0, st, p, ntiles);
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 2, 4, kX3>), dim3(g2), dim3(256), 0, st, p, ntiles);
       else
-        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 4>), dim3(g2), dim3(256), 0, st, p, ntiles);
+        hipLaunchKernelGGL((transition_f32_pipe_kernel<float, 4, 4, kX3>), dim3(g2), dim3(256), 0, st, p, ntiles);
     }
     return check_launch("transition (fp32)");
   }
@@ -1241,10 +1272,10 @@ int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
     p.part = static_cast<float*>(a->workspace);
     const dim3 g3((unsigned)nblk, (unsigned)splits);
     switch (a->c) {
-      case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2>), g3, dim3(256), 0, st, p, nblk); break;
-      case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4>), g3, dim3(256), 0, st, p, nblk); break;
-      case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8>), g3, dim3(256), 0, st, p, nblk); break;
-      default: hipLaunchKernelGGL((transition_f32_kernel<float, 12>), g3, dim3(256), 0, st, p, nblk); break;
+      case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2, kX3>), g3, dim3(256), 0, st, p, nblk); break;
+      case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4, kX3>), g3, dim3(256), 0, st, p, nblk); break;
+      case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8, kX3>), g3, dim3(256), 0, st, p, nblk); break;
+      default: hipLaunchKernelGGL((transition_f32_kernel<float, 12, kX3>), g3, dim3(256), 0, st, p, nblk); break;
     }
     const int64_t n4 = p.rows * a->c / 4;
     const int rg = (int)std::min<int64_t>((n4 + 255) / 256, 1024);
@@ -1253,10 +1284,10 @@ int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
     return check_launch("transition (fp32, split hidden)");
   }
   switch (a->c) {
-    case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2>), dim3(grid), dim3(256), 0, st, p, nblk); break;
-    case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4>), dim3(grid), dim3(256), 0, st, p, nblk); break;
-    case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8>), dim3(grid), dim3(256), 0, st, p, nblk); break;
-    case 384: hipLaunchKernelGGL((transition_f32_kernel<float, 12>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 64: hipLaunchKernelGGL((transition_f32_kernel<float, 2, kX3>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 128: hipLaunchKernelGGL((transition_f32_kernel<float, 4, kX3>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 256: hipLaunchKernelGGL((transition_f32_kernel<float, 8, kX3>), dim3(grid), dim3(256), 0, st, p, nblk); break;
+    case 384: hipLaunchKernelGGL((transition_f32_kernel<float, 12, kX3>), dim3(grid), dim3(256), 0, st, p, nblk); break;
     default: return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256, 384} with n = 4");
   }
   return check_launch("transition (fp32)");
@@ -1323,9 +1354,10 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
     return set_error(ODDE_EINVAL, "transition: bad sizes");
   if (a->rows >= (int64_t(1) << 31))
     return set_error(ODDE_EUNSUPPORTED, "transition: at most 2^31 - 1 rows per call");
-  if (!valid_dtype(a->x_dtype) || !valid_dtype(a->compute_dtype))
+  if (!valid_dtype(a->x_dtype) ||
+      !(valid_dtype(a->compute_dtype) || a->compute_dtype == ODDE_F32X3))
     return set_error(ODDE_EINVAL, "transition: bad dtype");
-  if (a->compute_dtype == ODDE_F32 && a->x_dtype != ODDE_F32)
+  if ((a->compute_dtype == ODDE_F32 || a->compute_dtype == ODDE_F32X3) && a->x_dtype != ODDE_F32)
     return set_error(ODDE_EUNSUPPORTED, "transition: fp32 arithmetic needs float32 rows");
   if (a->n_factor != 4 || (a->c != 64 && a->c != 128 && a->c != 256 && a->c != 384))
     return set_error(ODDE_EUNSUPPORTED, "transition: c in {64, 128, 256, 384} with n = 4");
@@ -1349,7 +1381,8 @@ int odde_transition_fwd(const odde_transition_args* a, void* stream) {
   }
   if (a->rows == 0) return ODDE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (a->compute_dtype == ODDE_F32) return run_transition_f32(a, st);
+  if (a->compute_dtype == ODDE_F32) return run_transition_f32<false>(a, st);
+  if (a->compute_dtype == ODDE_F32X3) return run_transition_f32<true>(a, st);
   if (a->x_dtype == ODDE_F32) return run_transition<float, bf16>(a, st);
   return run_transition<bf16, bf16>(a, st);
 }

@@ -162,15 +162,17 @@ struct TriattProjArgs {
 // consecutive rows i: every weight fragment it reads from L2 serves kRB row
 // blocks (the fp32 form, whose weights are too large to hold, is bound by
 // those reads).  Rows i at or past n are skipped (workgroup-uniform).
-template <typename ZT, typename CT, int kC, int kRB = 1>
+// kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
+template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
+  using MF = MulFrag<CT, kX3Mul>;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int j0 = blockIdx.x * 64 + w * 16;
   const int jl = j0 + r16;
   const int i0 = blockIdx.y * kRB;
   const int H = a.heads, HD = H * 32, jp = a.jp;
-  Frag<CT> x[kRB][kC];
+  MF x[kRB][kC];
 
   // mask rows: additive form for the exact core, keep flags for the fast one
   __shared__ float keep_s[kRB][64];
@@ -181,7 +183,12 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     const bool live = i < a.n;
     const bool valid = live && jl < a.n;
     const ZT* rowp = a.z + (int64_t)(live ? i : 0) * a.z_s0 + (int64_t)(valid ? jl : 0) * a.z_s1;
-    ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, x[rb]);
+    {
+      Frag<CT> xt[kC];
+      ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xt);
+#pragma unroll
+      for (int t = 0; t < kC; ++t) to_mul(xt[t], x[rb][t]);
+    }
     float mv = -INFINITY, kp = 0.f;
     if (valid) {
       const float m = a.mask ? a.mask[(int64_t)i * a.m_s0 + (int64_t)jl * a.m_s1] : 1.0f;
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     for (int rb = 0; rb < kRB; ++rb) aq[rb] = ak[rb] = ag[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wq, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(aq[rb], f, x[rb][t]);
@@ -270,7 +277,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     for (int rb = 0; rb < kRB; ++rb) av[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wv, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(av[rb], x[rb][t], f);
@@ -292,7 +299,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     for (int rb = 0; rb < kRB; ++rb) ab[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wb, C, 0, H, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ab[rb], x[rb][t], f);
@@ -723,25 +730,6 @@ __device__ __forceinline__ float psum8(const Frag<float>& p, const Frag<float>& 
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc = fmaf(p.get(e), wgt.get(e), acc);
   return acc;
-}
-// An f32 fragment as a pair of bf16 fragments, x = hi + lo + O(2^-18 |x|):
-// hi = bf16(x) to nearest, lo = bf16(x - hi).  Products of two such pairs as
-// hi*hi + hi*lo + lo*hi on the bf16 MFMA (fp32 accumulation) carry ~2^-16 of
-// relative error: the three-part fp32 form.
-__device__ __forceinline__ void split_x3(const Frag<float>& f, Frag<bf16>& hi, Frag<bf16>& lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float x = f.get(e);
-    const bf16 h = (bf16)x;
-    hi.v[e] = h;
-    lo.v[e] = (bf16)(x - (float)h);
-  }
-}
-__device__ __forceinline__ void mma_x3(f32x4& acc, const Frag<bf16>& ah, const Frag<bf16>& al,
-                                       const Frag<bf16>& bh, const Frag<bf16>& bl) {
-  mma(acc, al, bh);
-  mma(acc, ah, bl);
-  mma(acc, ah, bh);
 }
 __device__ __forceinline__ Frag<bf16> ones_frag(bf16) {
   Frag<bf16> f;
@@ -1328,14 +1316,15 @@ struct TriattOutArgs {
   float eps;
 };
 
-template <typename ZT, typename CT, int kHD>
+template <typename ZT, typename CT, int kHD, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a) {
   constexpr int HD = kHD * 32;
+  using MF = MulFrag<CT, kX3Mul>;
   const int i = blockIdx.y;
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
   const int jl = blockIdx.x * 64 + w * 16 + r16;
   const bool valid = jl < a.n;
-  Frag<CT> x[kHD];
+  MF x[kHD];
   const CT* orow = a.o + ((size_t)i * a.jp + jl) * HD;
 #pragma unroll
   for (int t = 0; t < kHD; ++t) {
@@ -1346,7 +1335,7 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kHD; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wo, HD, cb * 16, a.c, t, f);
       mma(acc, f, x[t]);
     }
@@ -1906,7 +1895,7 @@ int check_triatt(const odde_triatt_args* a) {
   return ODDE_OK;
 }
 
-template <typename ZT, typename CT, int kC>
+template <typename ZT, typename CT, int kC, bool kX3Mul = false>
 void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   // fp32 weights are read from L2 per fragment: more rows i per wave as
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
@@ -1914,11 +1903,22 @@ void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 8 ? 2 : 1;
   if (kRB > 1 && n >= 256) {
     dim3 grid(jp / 64, (n + kRB - 1) / kRB);
-    hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, kRB>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, kRB, kX3Mul>), grid, dim3(256), 0, st, p);
     return;
   }
   dim3 grid(jp / 64, n);
-  hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, 1, kX3Mul>), grid, dim3(256), 0, st, p);
+}
+// f32 compute: true fp32 products, or three bf16 parts (x3)
+template <typename ZT, typename CT, int kC>
+void launch_proj_ct(const TriattProjArgs<ZT, CT>& p, int n, int jp, bool x3, hipStream_t st) {
+  if constexpr (sizeof(CT) == 4) {
+    if (x3) {
+      launch_proj<ZT, CT, kC, true>(p, n, jp, st);
+      return;
+    }
+  }
+  launch_proj<ZT, CT, kC>(p, n, jp, st);
 }
 
 // Persistent weight-stationary projection where the per-wave weight slice
@@ -1977,8 +1977,14 @@ bool launch_out_ws(const TriattOutArgs<ZT, CT>& p, int HD, int C, int n, int jp,
 }
 
 template <typename ZT, typename CT, int kHD>
-void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
+void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStream_t st) {
   dim3 grid(jp / 64, n);
+  if constexpr (sizeof(CT) == 4) {
+    if (x3) {
+      hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true>), grid, dim3(256), 0, st, p);
+      return;
+    }
+  }
   hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD>), grid, dim3(256), 0, st, p);
 }
 
@@ -2114,6 +2120,9 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   bool wide = false;
   if constexpr (sizeof(CT) == 2) wide = triatt_wide(C, H, a->compute_dtype);
   const bool ws_path = triatt_ws(C, H, a->compute_dtype);
+  // f32 data with reduced-precision products allowed: every product of the
+  // module in three bf16 parts
+  const bool x3 = sizeof(CT) == 4 && a->compute_dtype == ODDE_F32X3;
 
   TriattProjArgs<ZT, CT> p;
   p.z = static_cast<const ZT*>(a->z);
@@ -2149,10 +2158,10 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
         return set_error(ODDE_EUNSUPPORTED, "triatt: no weight-stationary projection for this shape");
     } else if (!wide) {
       switch (C) {
-        case 64: launch_proj<ZT, CT, 2>(p, n, jp, st); break;
-        case 128: launch_proj<ZT, CT, 4>(p, n, jp, st); break;
-        case 256: launch_proj<ZT, CT, 8>(p, n, jp, st); break;
-        case 384: launch_proj<ZT, CT, 12>(p, n, jp, st); break;
+        case 64: launch_proj_ct<ZT, CT, 2>(p, n, jp, x3, st); break;
+        case 128: launch_proj_ct<ZT, CT, 4>(p, n, jp, x3, st); break;
+        case 256: launch_proj_ct<ZT, CT, 8>(p, n, jp, x3, st); break;
+        case 384: launch_proj_ct<ZT, CT, 12>(p, n, jp, x3, st); break;
         default: return set_error(ODDE_EUNSUPPORTED, "triatt: c must be 64, 128, 256 or 384");
       }
     }
@@ -2162,7 +2171,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
 
   TriattCoreArgs<CT> c;
   fill_core_args(c, ws.c);
-  c.x3 = a->compute_dtype == ODDE_F32X3;
+  c.x3 = x3;
   c.gate = ws_path ? nullptr : static_cast<const CT*>(ws.gate);  // else gated in triatt_out_ws
   c.out = static_cast<CT*>(ws.o);
   c.o_row = (int64_t)jp * HD; c.o_h = 32; c.o_j = HD;
@@ -2193,10 +2202,10 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
       return check_launch("triatt_out");
     }
     switch (HD) {
-      case 64: launch_out<ZT, CT, 2>(o, n, jp, st); break;
-      case 128: launch_out<ZT, CT, 4>(o, n, jp, st); break;
-      case 256: launch_out<ZT, CT, 8>(o, n, jp, st); break;
-      case 384: launch_out<ZT, CT, 12>(o, n, jp, st); break;
+      case 64: launch_out<ZT, CT, 2>(o, n, jp, x3, st); break;
+      case 128: launch_out<ZT, CT, 4>(o, n, jp, x3, st); break;
+      case 256: launch_out<ZT, CT, 8>(o, n, jp, x3, st); break;
+      case 384: launch_out<ZT, CT, 12>(o, n, jp, x3, st); break;
       default: return set_error(ODDE_EUNSUPPORTED, "triatt: heads*32 must be 64, 128, 256 or 384");
     }
     return check_launch("triatt_out");

@@ -52,16 +52,19 @@ struct TrimulProjArgs {
 // kRB row blocks (the fp32 form, whose weights are too large to hold, is
 // bound by those reads).  kX3 (f32 compute, ODDE_F32X3): A and B are written
 // as bf16 rows of 2 Np, [hi | lo] with hi = bf16(a) and lo = bf16(a - hi),
-// for the three-part contraction.
-template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false>
+// for the three-part contraction.  kX3Mul (f32 compute, ODDE_F32X3): the
+// projections' products in three bf16 parts (rows split once after the
+// LayerNorm, weight fragments as they are read).
+template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
+  using MF = MulFrag<CT, kX3Mul>;
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int y0 = blockIdx.x * 64 + w * 16;
   const int yl = y0 + r16;
   // mask for the four rows y0+4g .. +3 this lane writes
   const int yb = y0 + 4 * g;
-  Frag<CT> xf[kRB][kC];
+  MF xf[kRB][kC];
   float mk[kRB][4];
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
@@ -69,7 +72,12 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
     const bool valid = x_ < a.n && yl < a.n;
     const ZT* rowp =
         a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
-    ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xf[rb]);
+    {
+      Frag<CT> xt[kC];
+      ln_rows_to_frags<ZT, CT, C>(rowp, valid, a.ln_w, a.ln_b, a.eps, xt);
+#pragma unroll
+      for (int t = 0; t < kC; ++t) to_mul(xt[t], xf[rb][t]);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int y = yb + r;
@@ -85,7 +93,7 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
     for (int rb = 0; rb < kRB; ++rb) ap[rb] = ag[rb] = bp[rb] = bg[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ap[rb], xf[rb][t], f);
@@ -452,9 +460,11 @@ __global__ __launch_bounds__(256) void trimul_fold_ln_out_kernel(const float* __
   }
 }
 
-template <typename ZT, typename CT, int kC, int kCh>
+// kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
+template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a) {
   constexpr int C = kC * 32, CH = kCh * 32;
+  using MF = MulFrag<CT, kX3Mul>;
   constexpr int LD = CH + 16 / sizeof(CT);   // row stride of the transposed tile
   __shared__ __attribute__((aligned(16))) CT pt[64 * LD];
 
@@ -479,22 +489,30 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int yl = y0 + w * 16 + r16;
   const bool valid = x_ < a.n && yl < a.n;
-  Frag<CT> xp[kCh], xz[kC];
-  ln_rows_to_frags<CT, CT, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b, a.eps, xp);
+  MF xp[kCh], xz[kC];
   const ZT* zrow = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
-  ln_rows_to_frags<ZT, CT, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, xz);
+  {
+    Frag<CT> tp[kCh], tz[kC];
+    ln_rows_to_frags<CT, CT, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b, a.eps,
+                                 tp);
+    ln_rows_to_frags<ZT, CT, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, tz);
+#pragma unroll
+    for (int t = 0; t < kCh; ++t) to_mul(tp[t], xp[t]);
+#pragma unroll
+    for (int t = 0; t < kC; ++t) to_mul(tz[t], xz[t]);
+  }
 
   for (int cb = 0; cb < C / 16; ++cb) {
     f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
 #pragma unroll
     for (int t = 0; t < kCh; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wz, CH, cb * 16, C, t, f);
       mma(ay, f, xp[t]);
     }
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<CT> f;
+      MF f;
       load_w_frag(a.wg, C, cb * 16, C, t, f);
       mma(agt, f, xz[t]);
     }
@@ -1109,27 +1127,28 @@ int check_trimul(const odde_trimul_args* a) {
   return ODDE_OK;
 }
 
-// the three-part form's projection (f32 compute, A and B as [hi | lo] rows)
-template <typename ZT, int kC>
-void launch_tp_x3(const TrimulProjArgs<ZT, float>& p, hipStream_t st) {
-  constexpr int kRB = kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
-  dim3 grid(p.np / 64, p.np / kRB);
-  hipLaunchKernelGGL((trimul_proj_kernel<ZT, float, kC, kRB, true>), grid, dim3(256), 0, st, p);
-}
-
-template <typename ZT, typename CT, int kC>
+// kX3Out: A and B as [hi | lo] bf16 rows (the three-part contraction);
+// kX3Mul: the projections' products in three bf16 parts (f32 compute)
+template <typename ZT, typename CT, int kC, bool kX3Out = false, bool kX3Mul = false>
 void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   // fp32 weights are read from L2 per fragment: more row blocks per wave as
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
   // large enough (np >= 256: np^2 / 256 workgroups and more)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
-  if (kRB > 1 && p.np >= 256) {
+  if (kX3Out || (kRB > 1 && p.np >= 256)) {
     dim3 grid(p.np / 64, p.np / kRB);
-    hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kRB>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kRB, kX3Out, kX3Mul>), grid, dim3(256), 0,
+                       st, p);
     return;
   }
   dim3 grid(p.np / 64, p.np);
-  hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, 1, false, kX3Mul>), grid, dim3(256), 0, st, p);
+}
+template <typename ZT, int kC>
+void launch_tp_f32(const TrimulProjArgs<ZT, float>& p, bool x3out, bool x3mul, hipStream_t st) {
+  if (x3out) launch_tp<ZT, float, kC, true, true>(p, st);
+  else if (x3mul) launch_tp<ZT, float, kC, false, true>(p, st);
+  else launch_tp<ZT, float, kC>(p, st);
 }
 
 // Weight-stationary launches where the per-wave weight slices fit in
@@ -1174,18 +1193,24 @@ bool launch_to_ws(const TrimulOutArgs<ZT, CT>& p, int C, int ch, hipStream_t st)
 }
 
 template <typename ZT, typename CT, int kC, int kCh>
-void launch_to(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
+void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
   dim3 grid(p.np / 64, p.n);
+  if constexpr (sizeof(CT) == 4) {
+    if (x3) {
+      hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh, true>), grid, dim3(256), 0, st, p);
+      return;
+    }
+  }
   hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh>), grid, dim3(256), 0, st, p);
 }
 
 template <typename ZT, typename CT, int kC>
-bool dispatch_to(const TrimulOutArgs<ZT, CT>& p, int ch, hipStream_t st) {
+bool dispatch_to(const TrimulOutArgs<ZT, CT>& p, int ch, bool x3, hipStream_t st) {
   switch (ch) {
-    case 64: launch_to<ZT, CT, kC, 2>(p, st); return true;
-    case 128: launch_to<ZT, CT, kC, 4>(p, st); return true;
-    case 256: launch_to<ZT, CT, kC, 8>(p, st); return true;
-    case 384: launch_to<ZT, CT, kC, 12>(p, st); return true;
+    case 64: launch_to<ZT, CT, kC, 2>(p, x3, st); return true;
+    case 128: launch_to<ZT, CT, kC, 4>(p, x3, st); return true;
+    case 256: launch_to<ZT, CT, kC, 8>(p, x3, st); return true;
+    case 384: launch_to<ZT, CT, kC, 12>(p, x3, st); return true;
     default: return false;
   }
 }
@@ -1213,22 +1238,20 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   p.wg = static_cast<const CT*>(a->g_in_weight);
   p.A = static_cast<CT*>(ws.A); p.B = static_cast<CT*>(ws.B);
   p.n = n; p.np = np; p.ch = ch; p.eps = a->eps;
-  // the three-part fp32 form where its contraction tiles fit (Np a multiple
-  // of 256); otherwise true fp32 products
-  const bool x3 = sizeof(CT) == 4 && a->compute_dtype == ODDE_F32X3 && np % 256 == 0;
+  // the three-part fp32 form: the projections' and the output's products
+  // always, the contraction where its tiles fit (Np a multiple of 256;
+  // otherwise true fp32 products)
+  const bool x3mul = sizeof(CT) == 4 && a->compute_dtype == ODDE_F32X3;
+  const bool x3 = x3mul && np % 256 == 0;
   {
     LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
     if constexpr (sizeof(CT) == 4) {
-      if (x3) {
-        switch (C) {
-          case 64: launch_tp_x3<ZT, 2>(p, st); break;
-          case 128: launch_tp_x3<ZT, 4>(p, st); break;
-          case 256: launch_tp_x3<ZT, 8>(p, st); break;
-          case 384: launch_tp_x3<ZT, 12>(p, st); break;
-        }
+      switch (C) {
+        case 64: launch_tp_f32<ZT, 2>(p, x3, x3mul, st); break;
+        case 128: launch_tp_f32<ZT, 4>(p, x3, x3mul, st); break;
+        case 256: launch_tp_f32<ZT, 8>(p, x3, x3mul, st); break;
+        case 384: launch_tp_f32<ZT, 12>(p, x3, x3mul, st); break;
       }
-    }
-    if (x3) {
     } else if (!launch_tp_ws<ZT, CT>(p, C, ch, st)) {
       switch (C) {
         case 64: launch_tp<ZT, CT, 2>(p, st); break;
@@ -1292,10 +1315,10 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
     }
     bool ok = launch_to_ws<ZT, CT>(o, C, ch, st);
     if (!ok) switch (C) {
-      case 64: ok = dispatch_to<ZT, CT, 2>(o, ch, st); break;
-      case 128: ok = dispatch_to<ZT, CT, 4>(o, ch, st); break;
-      case 256: ok = dispatch_to<ZT, CT, 8>(o, ch, st); break;
-      case 384: ok = dispatch_to<ZT, CT, 12>(o, ch, st); break;
+      case 64: ok = dispatch_to<ZT, CT, 2>(o, ch, x3mul, st); break;
+      case 128: ok = dispatch_to<ZT, CT, 4>(o, ch, x3mul, st); break;
+      case 256: ok = dispatch_to<ZT, CT, 8>(o, ch, x3mul, st); break;
+      case 384: ok = dispatch_to<ZT, CT, 12>(o, ch, x3mul, st); break;
     }
     if (!ok) return set_error(ODDE_EUNSUPPORTED, "trimul: unsupported c/c_hidden");
     return check_launch("trimul_out");

@@ -251,10 +251,11 @@ def triangle_attention(z: torch.Tensor, mask: Optional[torch.Tensor], *, ln_w, l
     update.  Returns ``out``.
 
     fp32 arithmetic with ``torch.backends.cuda.matmul.allow_tf32`` set (the
-    reference's inference default, ``enable_tf32``) runs the attention
-    core's products on the bf16 MFMA in three parts (each operand as a bf16
-    pair; about 2^-16 of relative error per product, against TF32's 2^-11),
-    the way the reference's kernel slot takes its TF32 mode from that flag
+    reference's inference default, ``enable_tf32``) runs every product of
+    the module (projections, attention core, output) on the bf16 MFMA in
+    three parts (each operand as a bf16 pair; about 2^-16 of relative error
+    per product, against TF32's 2^-11), the way the reference's kernel slot
+    and its linear layers take their TF32 mode from that flag
     (opendde/model/triangular/triangular.py:55-56).  Otherwise the products
     are true fp32.
     """
@@ -321,9 +322,9 @@ def triangle_multiplication(z: torch.Tensor, mask: Optional[torch.Tensor], *, ou
     ``f32_out_weight``: with bf16 compute, also hand the library linear_z in
     f32 (it folds LN_out into that weight with a single bf16 rounding).
     fp32 arithmetic with ``torch.backends.cuda.matmul.allow_tf32`` set runs
-    the contraction's products in three bf16 parts, as
-    :func:`triangle_attention` does its core's (where Np is a multiple of
-    256; true fp32 products otherwise)."""
+    the products in three bf16 parts, as :func:`triangle_attention` does:
+    the projections and the output always, the contraction where Np is a
+    multiple of 256 (true fp32 products otherwise)."""
     _require_gpu(z, mask)
     zb, nbatch, z_sb = _batch_view(z, "z")
     n, c = z.shape[-3], z.shape[-1]
@@ -452,7 +453,11 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     ``pair_bias = (ln_w, ln_b, w, eps, dest)`` also writes
     ``dest[h, r] = (LN(out[r]) @ w.T)[h]`` (w: [16, c], dest: float32
     [16, rows]) from the rows as written, i.e. AttentionPairBias's
-    ``linear_nobias_z(layernorm_z(z))`` over the updated pair tensor."""
+    ``linear_nobias_z(layernorm_z(z))`` over the updated pair tensor.
+
+    fp32 arithmetic with ``torch.backends.cuda.matmul.allow_tf32`` set runs
+    the products in three bf16 parts, as :func:`triangle_attention` does
+    (the pair-bias projection stays true fp32)."""
     _require_gpu(x)
     c = x.shape[-1]
     nf = w_a.shape[0] // c
@@ -474,6 +479,8 @@ def transition(x: torch.Tensor, *, ln_w, ln_b, w_a, w_b, w_o, out: Optional[torc
     a.struct_size = ctypes.sizeof(_lib.TransitionArgs)
     a.c, a.n_factor = c, nf
     a.x_dtype, a.compute_dtype = dtype_code(x.dtype), dtype_code(ct)
+    if a.compute_dtype == _lib.F32 and torch.backends.cuda.matmul.allow_tf32:
+        a.compute_dtype = _lib.F32X3
     a.add_residual = 1 if add_residual else 0
     a.rows = x.numel() // c
     a.x, a.out = _ptr(x), _ptr(out)

@@ -1,16 +1,19 @@
-"""fp32 triangle attention with reduced-precision products allowed.
+"""fp32 pair-stack modules with reduced-precision products allowed.
 
 With ``torch.backends.cuda.matmul.allow_tf32`` set (the reference's inference
 default: ``enable_tf32``, opendde/config/model_base.py:35, applied at
-opendde/model/opendde.py:106), fp32 triangle attention runs its core's
-products on the bf16 MFMA in three parts: each operand as a bf16 pair
-hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation (about 2^-16 of
-relative error per product, against TF32's 2^-11).  The projections, the
-softmax, the exact fallback rows and the output stay fp32.
+opendde/model/opendde.py:106), the fp32 triangle modules and the transition
+run their products on the bf16 MFMA in three parts: each operand as a bf16
+pair hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation (about 2^-16 of
+relative error per product, against TF32's 2^-11).  That covers every
+projection, the attention core, the outputs, the transition's GEMMs and the
+triangle contraction where Np is a multiple of 256.  The softmax, the
+LayerNorms, the gates, the exact fallback rows and the residuals stay fp32.
 
-Checks: the fp32 tier's bar (max-abs <= 1e-4) against the fp32 oracle, and
-output bits that differ from the true-fp32 products' (so the three-part form
-did run).
+Checks: the fp32 tier's bar (max-abs <= 1e-4) against the fp32 oracle (or,
+where scaled-up weights make the reference's own TF32 mode miss that bar by
+far, at least 8x closer than it), and output bits that differ from the
+true-fp32 products' (so the three-part form did run).
 """
 
 import pytest
@@ -151,11 +154,12 @@ _orig_combine = ref.combine_projections
 @pytest.mark.parametrize("n,c,ch", [(256, 128, 128), (250, 64, 128), (512, 128, 128),
                                     (300, 128, 128)])
 def test_three_part_contraction_matches_fp32_oracle(outgoing, n, c, ch, monkeypatch):
-    """fp32 triangle multiplication with TF32 allowed: the contraction's
-    products in three bf16 parts where Np (n rounded up to 128) is a multiple
-    of 256 (n 250, 256, 512), true fp32 products otherwise (n 300: Np 384,
-    bit-identical to TF32 off).  Within the fp32 tier's bar of the fp32
-    oracle, or at least 8x closer to it than the reference's TF32 mode."""
+    """fp32 triangle multiplication with TF32 allowed: the projections' and
+    the output's products in three bf16 parts, the contraction's too where Np
+    (n rounded up to 128) is a multiple of 256 (n 250, 256, 512), true fp32
+    contraction products otherwise (n 300: Np 384).  Within the fp32 tier's
+    bar of the fp32 oracle, or at least 8x closer to it than the reference's
+    TF32 mode (the oracle with the contraction's operands rounded to TF32)."""
     from opendde_amd.triangular import (TriangleMultiplicationIncoming,
                                         TriangleMultiplicationOutgoing)
     cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
@@ -184,7 +188,65 @@ def test_three_part_contraction_matches_fp32_oracle(outgoing, n, c, ch, monkeypa
     margin(f"{what} (reference TF32 mode: {err_tf32:.3e})", max_abs=err, bar=1e-4)
     assert torch.isfinite(got).all()
     assert err <= max(1e-4, err_tf32 / 8), f"{what}: {err:.3e} against TF32 {err_tf32:.3e}"
-    if (n + 127) // 128 * 128 % 256 == 0:
-        assert not torch.equal(got, exact), "the three-part form did not run"
-    else:
-        assert torch.equal(got, exact), "Np not a multiple of 256 takes true fp32 products"
+    assert not torch.equal(got, exact), "the three-part form did not run"
+
+
+# pair rows (from 16384: LDS-staged weights, 4- and 8-wave tiles, ragged last
+# tiles) and single-track rows (hidden chunks split over workgroups), every
+# width of the fp32 row kernel
+@pytest.mark.parametrize("c,rows", [(128, 16384), (128, 40000), (64, 16400), (64, 33000),
+                                    (128, 1000), (256, 130), (384, 130), (384, 17), (64, 257)])
+def test_three_part_transition_matches_fp32_oracle(c, rows):
+    from opendde_amd.pairformer import Transition
+    mod = seeded(Transition(c, 4), 760 + c, 0.7 * STD * (128 / c) ** 0.5)
+    x = torch.randn(rows, c, generator=torch.Generator().manual_seed(c + 3))
+    exp = ref.transition(x, params_of(mod))
+    mod = mod.to(DEV)
+    xg = x.to(DEV)
+    res = []
+    for tf32 in (True, False):
+        old = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+        try:
+            with torch.no_grad():
+                res.append(mod.hip_apply(xg))
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = old
+    got, exact = res
+    err = float((got.double().cpu() - exp.double()).abs().max())
+    what = f"transition three-part c={c} rows={rows}"
+    say(f"    {what}: max-abs {err:.3e}")
+    margin(what, max_abs=err, bar=1e-4)
+    assert torch.isfinite(got).all()
+    assert err <= 1e-4, f"{what}: {err:.3e}"
+    assert not torch.equal(got, exact), "the three-part form did not run"
+
+
+def test_three_part_transition_pair_bias_in_place():
+    # the fused pair-bias epilogue (true fp32) after three-part GEMMs, in place
+    from opendde_amd.pairformer import AttentionPairBias, Transition
+    n, c = 131, 128
+    tr = seeded(Transition(c, 4), 770, STD)
+    apb = seeded(AttentionPairBias(n_heads=16, c_a=384, c_z=c, create_offset_ln_z=True), 771, 0.1)
+    x = torch.randn(n, n, c, generator=torch.Generator().manual_seed(772))
+    z_new = x + ref.transition(x, params_of(tr))
+    pz = params_of(apb)
+    exp_bias = ref.linear(ref.layer_norm(z_new, pz["layernorm_z.weight"], pz.get("layernorm_z.bias")),
+                          pz["linear_nobias_z.weight"]).permute(2, 0, 1)
+    tr, apb = tr.to(DEV), apb.to(DEV)
+    xg = x.to(DEV)
+    dest = torch.full((16, n, n), float("nan"), device=DEV)
+    old = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = True
+    try:
+        with torch.no_grad():
+            out = tr.hip_apply(xg, out=xg, add_residual=True,
+                               pair_bias=apb.pair_bias_spec(dest.view(16, -1)))
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = old
+    assert out.data_ptr() == xg.data_ptr()
+    dz = float((out.double().cpu() - z_new.double()).abs().max())
+    db = float((dest.double().cpu() - exp_bias.double()).abs().max())
+    margin("transition three-part in place z", max_abs=dz, bar=1e-4)
+    margin("transition three-part pair bias", max_abs=db, bar=1e-4)
+    assert dz <= 1e-4 and db <= 1e-4
