@@ -1316,35 +1316,47 @@ struct TriattOutArgs {
   float eps;
 };
 
-template <typename ZT, typename CT, int kHD, bool kX3Mul = false>
+// kRB consecutive rows i per workgroup: every weight fragment a wave reads
+// from L2 serves kRB row blocks (the fp32 form reads W_o per fragment).
+template <typename ZT, typename CT, int kHD, bool kX3Mul = false, int kRB = 1>
 __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a) {
   constexpr int HD = kHD * 32;
   using MF = MulFrag<CT, kX3Mul>;
-  const int i = blockIdx.y;
+  const int i0 = blockIdx.y * kRB;
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
   const int jl = blockIdx.x * 64 + w * 16 + r16;
-  const bool valid = jl < a.n;
-  MF x[kHD];
-  const CT* orow = a.o + ((size_t)i * a.jp + jl) * HD;
+  MF x[kRB][kHD];
 #pragma unroll
-  for (int t = 0; t < kHD; ++t) {
-    if (valid) x[t].load(orow + 32 * t + 8 * g);
-    else x[t].zero();
+  for (int rb = 0; rb < kRB; ++rb) {
+    const bool valid = i0 + rb < a.n && jl < a.n;
+    const CT* orow = a.o + ((size_t)(valid ? i0 + rb : 0) * a.jp + jl) * HD;
+#pragma unroll
+    for (int t = 0; t < kHD; ++t) {
+      if (valid) x[rb][t].load(orow + 32 * t + 8 * g);
+      else x[rb][t].zero();
+    }
   }
   for (int cb = 0; cb < a.c / 16; ++cb) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kHD; ++t) {
       MF f;
       load_w_frag(a.wo, HD, cb * 16, a.c, t, f);
-      mma(acc, f, x[t]);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(acc[rb], f, x[rb][t]);
     }
-    if (!valid) continue;
     const int c0 = cb * 16 + 4 * g;
-    float base[4] = {0.f, 0.f, 0.f, 0.f};
-    if (a.add) load4(a.res + (int64_t)i * a.r_s0 + (int64_t)jl * a.r_s1 + c0, base);
-    store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jl * a.o_s1 + c0, base[0] + acc[0],
-           base[1] + acc[1], base[2] + acc[2], base[3] + acc[3]);
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int i = i0 + rb;
+      if (i >= a.n || jl >= a.n) continue;
+      float base[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.add) load4(a.res + (int64_t)i * a.r_s0 + (int64_t)jl * a.r_s1 + c0, base);
+      store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jl * a.o_s1 + c0, base[0] + acc[rb][0],
+             base[1] + acc[rb][1], base[2] + acc[rb][2], base[3] + acc[rb][3]);
+    }
   }
 }
 
@@ -1978,6 +1990,19 @@ bool launch_out_ws(const TriattOutArgs<ZT, CT>& p, int HD, int C, int n, int jp,
 
 template <typename ZT, typename CT, int kHD>
 void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStream_t st) {
+  // fp32: W_o is read from L2 per fragment, so 4 rows i per workgroup up to
+  // HD = 128 (2 up to 256) once the grid stays large (n >= 256)
+  constexpr int kRB = sizeof(CT) != 4 ? 1 : kHD <= 4 ? 4 : kHD <= 8 ? 2 : 1;
+  if constexpr (kRB > 1) {
+    if (n >= 256) {
+      dim3 grid(jp / 64, (n + kRB - 1) / kRB);
+      if (x3)
+        hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true, kRB>), grid, dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, false, kRB>), grid, dim3(256), 0, st, p);
+      return;
+    }
+  }
   dim3 grid(jp / 64, n);
   if constexpr (sizeof(CT) == 4) {
     if (x3) {
