@@ -125,6 +125,11 @@ __device__ __forceinline__ void mma_x3(f32x4& acc, const Frag<bf16>& ah, const F
   mma(acc, ah, bl);
   mma(acc, ah, bh);
 }
+__device__ __forceinline__ bf16x8 as_bf16x8(const f32x4& v) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &v, sizeof(r));
+  return r;
+}
 struct FragX3 {
   Frag<bf16> hi, lo;
   __device__ __forceinline__ void zero() {
@@ -400,11 +405,60 @@ __device__ __forceinline__ void load_w_frag(const CT* __restrict__ w, int ld, in
   if (o < n_out) f.load(w + (size_t)o * ld + 32 * t + 8 * g);
   else f.zero();
 }
-__device__ __forceinline__ void load_w_frag(const float* __restrict__ w, int ld, int o0, int n_out,
-                                            int t, FragX3& f) {
-  Frag<float> x;
-  load_w_frag(w, ld, o0, n_out, t, x);
-  f.from(x);
+// Three-part weight fragments from weights split once per call
+// (split_x3_rows_kernel): `w_split` holds the bytes of an [n_out][2 ld] bf16
+// array whose row o is hi = bf16(W[o][:]) followed by lo = bf16(W[o][:] - hi)
+// (the same 4 bytes per weight as the f32 array it replaces).
+__device__ __forceinline__ void load_w_frag(const float* __restrict__ w_split, int ld, int o0,
+                                            int n_out, int t, FragX3& f) {
+  const int o = o0 + (lane_id() & 15);
+  const int g = lane_id() >> 4;
+  if (o < n_out) {
+    const bf16* p = reinterpret_cast<const bf16*>(w_split) + (size_t)o * 2 * ld + 32 * t + 8 * g;
+    f.hi.load(p);
+    f.lo.load(p + ld);
+  } else {
+    f.zero();
+  }
+}
+
+// W [rows][cols] f32 -> [rows][2 cols] bf16: row r = hi = bf16(W[r][:]) to
+// nearest, then lo = bf16(W[r][:] - hi).  With kPerm32 the columns are
+// permuted within each block of 32, column 16 s + 4 q + e to 8 q + 4 s + e,
+// so that the 8 columns {4q .. 4q+3, 16+4q .. 16+4q+3} are contiguous (the
+// transition's W_o, whose GEMM2 fragment slots of lane group q are those
+// hidden units).
+template <bool kPerm32>
+__global__ __launch_bounds__(256) void split_x3_rows_kernel(const float* __restrict__ src,
+                                                            bf16* __restrict__ dst, int rows,
+                                                            int cols) {
+  const int64_t total = (int64_t)rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cols;
+    const int c = (int)(i - r * cols);
+    int cc = c;
+    if constexpr (kPerm32) {
+      const int m = c & 31;
+      cc = (c & ~31) + 8 * ((m >> 2) & 3) + 4 * (m >> 4) + (m & 3);
+    }
+    const float x = src[i];
+    const bf16 h = (bf16)x;
+    bf16* row = dst + r * 2 * cols;
+    row[cc] = h;
+    row[cols + cc] = (bf16)(x - (float)h);
+  }
+}
+inline void launch_split_x3(const void* src, int rows, int cols, void* dst, bool perm32,
+                            hipStream_t st) {
+  const int64_t total = (int64_t)rows * cols;
+  const int grid = (int)(total / 256 + 1 < 1024 ? total / 256 + 1 : 1024);
+  if (perm32)
+    hipLaunchKernelGGL((split_x3_rows_kernel<true>), dim3(grid), dim3(256), 0, st,
+                       static_cast<const float*>(src), static_cast<bf16*>(dst), rows, cols);
+  else
+    hipLaunchKernelGGL((split_x3_rows_kernel<false>), dim3(grid), dim3(256), 0, st,
+                       static_cast<const float*>(src), static_cast<bf16*>(dst), rows, cols);
 }
 // bf16 weights as fp16 fragments (exact: fp16 holds every bf16 value of the
 // weights' range, |w| >= 2^-14, to more mantissa bits than bf16 has)

@@ -708,15 +708,22 @@ __global__ __launch_bounds__(256) void transition_f32_kernel(TransitionArgs<ZT, 
       }
       MF hm;
       to_mul(hf, hm);
-      // GEMM2: W_o[c][h0 + slot] with the same slot -> hidden map
+      // GEMM2: W_o[c][h0 + slot] with the same slot -> hidden map (three-part:
+      // W_o split with its hidden units permuted within blocks of 32, so the
+      // slots of lane group g are 8 consecutive units of the hi and lo rows)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const float* wrow = a.wo + (size_t)(cb * 16 + r16) * HID + h0;
-        Frag<float> fo;
-        fo.lo = *reinterpret_cast<const f32x4*>(wrow + 4 * g);
-        fo.hi = *reinterpret_cast<const f32x4*>(wrow + 16 + 4 * g);
         MF fm;
-        to_mul(fo, fm);
+        if constexpr (kX3) {
+          const bf16* w16 = reinterpret_cast<const bf16*>(a.wo) +
+                            (size_t)(cb * 16 + r16) * 2 * HID + h0 + 8 * g;
+          fm.hi.load(w16);
+          fm.lo.load(w16 + HID);
+        } else {
+          const float* wrow = a.wo + (size_t)(cb * 16 + r16) * HID + h0;
+          fm.lo = *reinterpret_cast<const f32x4*>(wrow + 4 * g);
+          fm.hi = *reinterpret_cast<const f32x4*>(wrow + 16 + 4 * g);
+        }
         mma(acc[cb], fm, hm);
       }
     }
@@ -830,8 +837,14 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
         dst = (m ? S.wb : S.wa) + 64 * i;
       } else {
         const int i = op - 2 * NAB;
-        const int c = 8 * i + (l >> 3), pos = l & 7;
-        src = a.wo + (size_t)c * HID + h0 + (pos ^ (c & 7)) * 4;
+        const int c = 8 * i + (l >> 3), sp = (l & 7) ^ (c & 7);
+        // three-part: W_o rows of 2 HID bf16 (hi | lo, the same bytes per
+        // row as f32); a chunk's 32 hidden units are 4 chunks of hi (sp < 4)
+        // and 4 of lo
+        if constexpr (kX3)
+          src = a.wo + (size_t)c * HID + (sp < 4 ? h0 / 2 + sp * 4 : HID / 2 + h0 / 2 + (sp - 4) * 4);
+        else
+          src = a.wo + (size_t)c * HID + h0 + sp * 4;
         dst = S.wo + 64 * i;
       }
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -871,14 +884,19 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
         const int rr = 16 * hb + r16;
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-          Frag<float> fa, fb;
-          fa.lo = S.wa[rr * CPR + ((8 * t + 2 * g) ^ key)];
-          fa.hi = S.wa[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
-          fb.lo = S.wb[rr * CPR + ((8 * t + 2 * g) ^ key)];
-          fb.hi = S.wb[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
           MF ma, mb;
-          to_mul(fa, ma);
-          to_mul(fb, mb);
+          if constexpr (kX3) {
+            // rows of C / 8 hi chunks, then C / 8 lo chunks
+            ma.hi.v = as_bf16x8(S.wa[rr * CPR + ((4 * t + g) ^ key)]);
+            ma.lo.v = as_bf16x8(S.wa[rr * CPR + ((C / 8 + 4 * t + g) ^ key)]);
+            mb.hi.v = as_bf16x8(S.wb[rr * CPR + ((4 * t + g) ^ key)]);
+            mb.lo.v = as_bf16x8(S.wb[rr * CPR + ((C / 8 + 4 * t + g) ^ key)]);
+          } else {
+            ma.lo = S.wa[rr * CPR + ((8 * t + 2 * g) ^ key)];
+            ma.hi = S.wa[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
+            mb.lo = S.wb[rr * CPR + ((8 * t + 2 * g) ^ key)];
+            mb.hi = S.wb[rr * CPR + ((8 * t + 2 * g + 1) ^ key)];
+          }
           mma(sa, ma, xf[t]);
           mma(sb, mb, xf[t]);
         }
@@ -891,11 +909,15 @@ __global__ __launch_bounds__(64 * kW) void transition_f32_pipe_kernel(Transition
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         const int c = 16 * cb + r16;
-        Frag<float> fo;
-        fo.lo = S.wo[c * 8 + (g ^ key)];
-        fo.hi = S.wo[c * 8 + ((4 + g) ^ key)];
         MF mo;
-        to_mul(fo, mo);
+        if constexpr (kX3) {
+          // hi chunk g and lo chunk g: hidden units 4g .. 4g+3, 16+4g .. +3
+          mo.hi.v = as_bf16x8(S.wo[c * 8 + (g ^ key)]);
+          mo.lo.v = as_bf16x8(S.wo[c * 8 + ((4 + g) ^ key)]);
+        } else {
+          mo.lo = S.wo[c * 8 + (g ^ key)];
+          mo.hi = S.wo[c * 8 + ((4 + g) ^ key)];
+        }
         mma(acc[cb], mo, hm);
       }
     }
@@ -1149,9 +1171,19 @@ int transition_f32_splits(const odde_transition_args* a) {
   return best;
 }
 
-uint64_t transition_ws_bytes(const odde_transition_args* a) {
+// ODDE_F32X3: W_a, W_b and W_o split once per call into bf16 hi | lo rows
+uint64_t transition_split_bytes(const odde_transition_args* a) {
+  return a->compute_dtype == ODDE_F32X3 ? (uint64_t)3 * a->n_factor * a->c * a->c * 4 : 0;
+}
+// fp32 workspace: the split-hidden partial sums, then the split weights
+uint64_t transition_part_bytes(const odde_transition_args* a) {
   const int splits = transition_f32_splits(a);
-  if (splits > 1) return (uint64_t)splits * (uint64_t)a->rows * (uint64_t)a->c * 4 + 256;
+  if (splits <= 1) return 0;
+  return ((uint64_t)splits * (uint64_t)a->rows * (uint64_t)a->c * 4 + 255) & ~uint64_t(255);
+}
+uint64_t transition_ws_bytes(const odde_transition_args* a) {
+  const uint64_t f32 = transition_part_bytes(a) + transition_split_bytes(a);
+  if (f32) return f32 + 256;
   if (!transition_wide(a->c, a->n_factor, a->compute_dtype)) return 0;
   // normalised rows [Mp][C] and hidden activations [Mp][4C], bf16; with the
   // split output GEMM its fp32 partial sums [kTwSplit][Mp][C]
@@ -1241,6 +1273,20 @@ int run_transition_f32(const odde_transition_args* a, hipStream_t st) {
   p.pb_zero = nullptr;
   const int64_t nblk = (p.rows + 15) / 16;
   const int grid = (int)std::min<int64_t>(nblk, 8 * 256);
+  if constexpr (kX3) {
+    // the weights as bf16 hi | lo rows (W_o's hidden units permuted within
+    // blocks of 32), split once for this call
+    const int C = a->c, HID = a->n_factor * a->c;
+    char* d = static_cast<char*>(a->workspace) + transition_part_bytes(a);
+    launch_split_x3(a->w_a, HID, C, d, false, st);
+    p.wa = reinterpret_cast<const float*>(d);
+    d += (size_t)HID * C * 4;
+    launch_split_x3(a->w_b, HID, C, d, false, st);
+    p.wb = reinterpret_cast<const float*>(d);
+    d += (size_t)HID * C * 4;
+    launch_split_x3(a->w_o, C, HID, d, true, st);
+    p.wo = reinterpret_cast<const float*>(d);
+  }
   LaunchScope ls(ODDE_K_TRANSITION, st);
   // the staged form when its tiles fill the GPU and the weights can be
   // staged by 16-byte direct loads

@@ -1873,7 +1873,9 @@ bool triatt_ws(int c, int heads, int dt) {
 // 8 row tiles
 int64_t triatt_wide_rows(int n) { return (int64_t)round_up(n * round_up(n, 64), 2048); }
 
-struct TriattWs { CoreBufs c; void* gate; void* o; void* zn; uint64_t bytes; };
+// wsplit (ODDE_F32X3): W_q, W_k, W_v, W_g ([HD][C] each), W_b ([H][C]) and
+// W_o ([C][HD]) split once per call into bf16 hi | lo rows
+struct TriattWs { CoreBufs c; void* gate; void* o; void* zn; char* wsplit; uint64_t bytes; };
 
 TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int cz, int dt) {
   const int jp = round_up(n, 64);
@@ -1886,6 +1888,8 @@ TriattWs carve_triatt(void* base, uint64_t size, int n, int heads, int cz, int d
   // the wide path reads o as GEMM rows, whole 256-row tiles
   w.o = c.take<char>(wide ? (uint64_t)triatt_wide_rows(n) * heads * 32 * 2 : per);
   w.zn = wide ? c.take<char>((uint64_t)triatt_wide_rows(n) * cz * 2) : nullptr;
+  const uint64_t hd = (uint64_t)heads * 32;
+  w.wsplit = dt == ODDE_F32X3 ? c.take<char>((5 * hd + heads) * cz * 4) : nullptr;
   w.bytes = (c.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -2161,6 +2165,22 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
   p.wg = static_cast<const CT*>(a->w_g);
   p.q = static_cast<CT*>(ws.c.q); p.k = static_cast<CT*>(ws.c.k); p.v = static_cast<CT*>(ws.c.v);
   p.gate = static_cast<CT*>(ws.gate); p.keep = static_cast<CT*>(ws.c.keep);
+  const CT* w_o = static_cast<const CT*>(a->w_o);
+  if (x3) {
+    // the weights as bf16 hi | lo rows, split once for this call
+    const int HDw = H * 32;
+    char* d = ws.wsplit;
+    const void* src[5] = {a->w_q, a->w_k, a->w_v, a->w_g, a->w_bias};
+    const CT** dstp[5] = {&p.wq, &p.wk, &p.wv, &p.wg, &p.wb};
+    for (int m = 0; m < 5; ++m) {
+      const int rows = m < 4 ? HDw : H;
+      launch_split_x3(src[m], rows, C, d, false, st);
+      *dstp[m] = reinterpret_cast<const CT*>(d);
+      d += (size_t)rows * C * 4;
+    }
+    launch_split_x3(a->w_o, C, HDw, d, false, st);
+    w_o = reinterpret_cast<const CT*>(d);
+  }
   p.bias = ws.c.bias; p.mb = ws.c.mb; p.mflag = ws.c.mflag; p.kmax = ws.c.kmax;
   p.bmax = ws.c.bmax; p.anykeep = ws.c.anykeep;
   p.n = n; p.jp = jp; p.heads = H;
@@ -2206,7 +2226,7 @@ int run_triatt(const odde_triatt_args* a, hipStream_t st) {
 
   TriattOutArgs<ZT, CT> o;
   o.o = static_cast<const CT*>(ws.o);
-  o.wo = static_cast<const CT*>(a->w_o);
+  o.wo = w_o;
   o.res = static_cast<const ZT*>(a->z); o.r_s0 = a->z_s0; o.r_s1 = a->z_s1;
   o.out = static_cast<ZT*>(a->out); o.o_s0 = a->out_s0; o.o_s1 = a->out_s1;
   o.n = n; o.jp = jp; o.c = C; o.add = a->add_residual;

@@ -998,6 +998,9 @@ bool trimul_ws_shape(int c, int ch, int dt) {
 struct TrimulWs {
   void* A; void* B; void* P; void* zn;
   bf16* wfold; float* wsum; float* wbias;  // LN_out folded into W_z (ws shapes)
+  // ODDE_F32X3: W_p, W_g of the input ([2 Ch][C] each), W_z ([C][Ch]) and
+  // W_g of the output ([C][C]) split once per call into bf16 hi | lo rows
+  char* wsplit;
   uint64_t bytes;
 };
 
@@ -1016,6 +1019,9 @@ TrimulWs carve_trimul(void* base, uint64_t size, int n, int c, int ch, int dt) {
   w.wfold = fold ? cv.take<bf16>((uint64_t)c * ch) : nullptr;
   w.wsum = fold ? cv.take<float>(c) : nullptr;
   w.wbias = fold ? cv.take<float>(c) : nullptr;
+  w.wsplit =
+      dt == ODDE_F32X3 ? cv.take<char>(((uint64_t)4 * ch * c + (uint64_t)c * ch + (uint64_t)c * c) * 4)
+                       : nullptr;
   w.bytes = (cv.used + 255) & ~uint64_t(255);
   return w;
 }
@@ -1243,6 +1249,23 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   // otherwise true fp32 products)
   const bool x3mul = sizeof(CT) == 4 && a->compute_dtype == ODDE_F32X3;
   const bool x3 = x3mul && np % 256 == 0;
+  const CT* w_z = static_cast<const CT*>(a->p_out_weight);
+  const CT* w_go = static_cast<const CT*>(a->g_out_weight);
+  if (x3mul) {
+    // the weights as bf16 hi | lo rows, split once for this call
+    char* d = ws.wsplit;
+    launch_split_x3(a->p_in_weight, 2 * ch, C, d, false, st);
+    p.wp = reinterpret_cast<const CT*>(d);
+    d += (size_t)2 * ch * C * 4;
+    launch_split_x3(a->g_in_weight, 2 * ch, C, d, false, st);
+    p.wg = reinterpret_cast<const CT*>(d);
+    d += (size_t)2 * ch * C * 4;
+    launch_split_x3(a->p_out_weight, C, ch, d, false, st);
+    w_z = reinterpret_cast<const CT*>(d);
+    d += (size_t)C * ch * 4;
+    launch_split_x3(a->g_out_weight, C, C, d, false, st);
+    w_go = reinterpret_cast<const CT*>(d);
+  }
   {
     LaunchScope ls(ODDE_K_TRIMUL_PROJ, st);
     if constexpr (sizeof(CT) == 4) {
@@ -1296,8 +1319,8 @@ int run_trimul(const odde_trimul_args* a, hipStream_t st) {
   o.out = static_cast<ZT*>(a->out); o.o_s0 = a->out_s0; o.o_s1 = a->out_s1;
   o.ln_in_w = a->norm_in_weight; o.ln_in_b = a->norm_in_bias;
   o.ln_out_w = a->norm_out_weight; o.ln_out_b = a->norm_out_bias;
-  o.wz = static_cast<const CT*>(a->p_out_weight);
-  o.wg = static_cast<const CT*>(a->g_out_weight);
+  o.wz = w_z;
+  o.wg = w_go;
   o.wz_sum = o.wz_bias = nullptr;
   o.n = n; o.np = np; o.c = C; o.add = a->add_residual; o.eps = a->eps;
   {
