@@ -30,7 +30,9 @@ extern "C" {
 #define ODDE_F32 0
 #define ODDE_BF16 1
 #define ODDE_F16 2 /* LayerNorm entry points only */
-/* compute_dtype of odde_triatt_fwd, odde_trimul_fwd and odde_transition_fwd:
+/* compute_dtype of odde_triatt_fwd, odde_trimul_fwd and odde_transition_fwd
+ * (their workspaces then also hold the weights split into bf16 hi | lo rows,
+ * written once per call):
  * f32 data and weights, the products on the bf16 MFMA in three parts (each
  * operand as a bf16 pair hi + lo; hi*hi + hi*lo + lo*hi, f32 accumulation;
  * about 2^-16 of relative error per product): every projection, the
@@ -223,6 +225,8 @@ int odde_trimul_fwd(const odde_trimul_args* args, void* hip_stream);
  * GEMMs whose hidden activations live in the workspace
  * (odde_transition_workspace_bytes; 0 for the fused kernels, which need
  * none), and the pair-bias projection as a pass over the rows written.
+ * fp32 arithmetic with few rows keeps split-hidden partial sums there, and
+ * ODDE_F32X3 the weights split into bf16 hi | lo rows (3 n c^2 floats).
  */
 typedef struct odde_transition_args {
   uint32_t struct_size;
