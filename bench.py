@@ -183,9 +183,10 @@ def kernel_avg_ms(fn, kid, reps: int = 5):
 
 
 def probe_machine(dev):
-    """Sustained MFMA rates (bf16 16x16x32, f32 16x16x4; 2 workgroups of 4
-    waves per CU, 8 independent chains per wave), the attention core's
-    instruction mix as a ceiling (odde_probe_mix) and HBM bandwidth on this
+    """Sustained MFMA rates (bf16 16x16x32 on fixed and on pseudo-random
+    operands, f32 16x16x4; 2 workgroups of 4 waves per CU, 8 independent
+    chains per wave), the attention core's instruction mix as a ceiling
+    (odde_probe_mix, also split between the two waves of a SIMD) and HBM bandwidth on this
     GPU: the streaming probe over 2 GiB (read; copy and in-place rewrite,
     bytes read + written) and torch's device copy beside it.  The probes live
     in the measurement library (opendde_amd.probe), not the product library;
@@ -196,7 +197,8 @@ def probe_machine(dev):
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     out = {"cus": cus}
-    for name, code, iters in (("bf16", pr.BF16, 4000), ("f32", pr.F32, 1000)):
+    for name, code, iters in (("bf16", pr.BF16, 4000), ("bf16_random", pr.BF16_RANDOM, 4000),
+                              ("f32", pr.F32, 1000)):
         fl = ctypes.c_double(0.0)
         call = lambda it: pr.check(lib.odde_probe_mfma(code, it, 2 * cus,  # noqa: E731
                                                        ctypes.c_void_p(sink.data_ptr()),
@@ -209,9 +211,12 @@ def probe_machine(dev):
     # the attention core's per-key-block mix (40 MFMA, 64 exp, 32 bf16 packs)
     # with no memory traffic: its ceiling in attention TF/s on this GPU, and
     # the MFMA and exponential parts alone
-    for name, parts in (("mfma_only", 1), ("exp_only", 2), ("mix", 3)):
+    # (split: one wave of each SIMD issues the MFMAs and the other the
+    # exponentials and packs -- the most co-issue of the two kinds)
+    for name, parts in (("mfma_only", 1), ("exp_only", 2), ("mix", 3), ("split", 4)):
         fl = ctypes.c_double(0.0)
-        call = lambda it: pr.check(lib.odde_probe_mix(parts, it, 2 * cus,  # noqa: E731
+        grid = cus if parts == 4 else 2 * cus  # 8-wave workgroups for the split form
+        call = lambda it: pr.check(lib.odde_probe_mix(parts, it, grid,  # noqa: E731
                                                       ctypes.c_void_p(sink.data_ptr()),
                                                       ctypes.byref(fl), stream),
                                    "odde_probe_mix")
@@ -283,13 +288,23 @@ def fp32_block_leg(dev, tf32: bool = False):
             fl = {"triatt_core": fk["core"], "trimul_contract": fk["contract"]}.get(name)
             if fl:
                 kt = fl / (tot / cnt * 1e-3) / 1e12
-                ent.update(tflops=round(kt, 2), pct_f32_peak=round(100 * kt / PEAK_F32_TFLOPS, 2))
+                ent.update(tflops=round(kt, 2))
+                if tf32:
+                    # three bf16 MFMA products per fp32 product: the matrix
+                    # pipe executes 3x the algorithmic flops, in bf16
+                    ent.update(bf16_mfma_tflops=round(3 * kt, 2),
+                               pct_bf16_peak=round(100 * 3 * kt / PEAK_BF16_TFLOPS, 2))
+                else:
+                    ent.update(pct_f32_peak=round(100 * kt / PEAK_F32_TFLOPS, 2))
             per_kernel[name] = ent
     _lib.timing_reset()
+    rate = ({"bf16_mfma_tflops": round(3 * t, 2),
+             "pct_bf16_peak": round(100 * 3 * t / PEAK_BF16_TFLOPS, 2)} if tf32 else
+            {"pct_f32_peak": round(100 * t / PEAK_F32_TFLOPS, 2)})
     out = dict(
-        gpu_ms=round(ms, 3), gflop=round(f / 1e9, 1), tflops=round(t, 2),
-        pct_f32_peak=round(100 * t / PEAK_F32_TFLOPS, 2),
-        dtype="fp32, attention core products in three bf16 parts" if tf32 else "fp32",
+        gpu_ms=round(ms, 3), gflop=round(f / 1e9, 1), tflops=round(t, 2), **rate,
+        dtype=("fp32 data; the pair stack's products as three bf16 MFMA parts "
+               "(hi*hi + hi*lo + lo*hi, fp32 accumulation)") if tf32 else "fp32",
         residual_dtype="fp32", allow_tf32=tf32, pad_tokens=cfg.n_pad, kernels=per_kernel)
     log(f"bench: fp32 block n=1024{' (tf32 allowed)' if tf32 else ''} {ms:.2f} ms")
     del blk, z0, zw, sg, mg

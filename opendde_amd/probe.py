@@ -15,7 +15,7 @@ from typing import Optional
 HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE_LIB_PATH = os.environ.get("OPENDDE_AMD_PROBE_LIB",
                                 os.path.join(HERE, "lib", "libopendde_amd_probe.so"))
-F32, BF16 = 0, 1
+F32, BF16, BF16_RANDOM = 0, 1, 2
 
 _vp = ctypes.c_void_p
 _dp = ctypes.POINTER(ctypes.c_double)

@@ -28,7 +28,7 @@ def _timed_ms(fn):
     return e0.elapsed_time(e1)
 
 
-@pytest.mark.parametrize("parts", [1, 2, 3])
+@pytest.mark.parametrize("parts", [1, 2, 3, 4])
 def test_mix_probe_runs_and_counts_attention_flops(parts):
     say(f"[gpu] mix probe parts={parts}")
     lib = pr.load()
@@ -43,7 +43,7 @@ def test_mix_probe_runs_and_counts_attention_flops(parts):
     assert [_lib.launch_count(k) for k in _lib.KERNEL_NAMES] == before
 
 
-@pytest.mark.parametrize("code", [pr.BF16, pr.F32])
+@pytest.mark.parametrize("code", [pr.BF16, pr.BF16_RANDOM, pr.F32])
 def test_mfma_probe_counts_flops(code):
     say(f"[gpu] mfma probe dtype={code}")
     lib = pr.load()
@@ -52,13 +52,13 @@ def test_mfma_probe_counts_flops(code):
     ms = _timed_ms(lambda: pr.check(lib.odde_probe_mfma(code, 50, 4, ctypes.c_void_p(
         sink.data_ptr()), ctypes.byref(fl), _stream()), "odde_probe_mfma"))
     assert ms > 0
-    assert fl.value == 2.0 * 16 * 16 * (32 if code == pr.BF16 else 4) * 8 * 50 * 4 * 4
+    assert fl.value == 2.0 * 16 * 16 * (4 if code == pr.F32 else 32) * 8 * 50 * 4 * 4
 
 
 def test_probes_reject_bad_arguments():
     lib = pr.load()
     fl = ctypes.c_double(0.0)
-    assert lib.odde_probe_mix(4, 10, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
+    assert lib.odde_probe_mix(5, 10, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
     assert b"parts" in lib.odde_probe_last_error()
     assert lib.odde_probe_mix(1, 0, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
     assert lib.odde_probe_mfma(7, 10, 1, ctypes.c_void_p(0x1000), ctypes.byref(fl), None) == -1
