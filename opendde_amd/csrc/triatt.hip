@@ -928,28 +928,41 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
   };
 
   // ---- per-wave state ----
-  int rr[R];
-  bool skip = true;
+  // (every flag is loaded, without short-circuit branches, so that no load
+  // waits for another before the first key block is requested)
+  int rr[R], rf[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     rr[r] = min(row0 + r, a.rows - 1);
-    skip = skip && (row0 + r >= a.rows || a.rowflag[rr[r]] != 0);
+    rf[r] = a.rowflag[rr[r]];
   }
+  // q fragments, then the first key block's staging, so that the two
+  // latencies overlap; the overflow bound is checked while the stage lands
   Frag<CT> qf[R][QB];
-  bool over = false;
+  float bqv[QB], kmv[R];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qq = min(q0 + 16 * qb + r16, jp - 1);
-    const float bq = fkey_inv(a.bmax[((size_t)bb * a.heads + h) * jp + min(qq, n - 1)]);
+    bqv[qb] = fkey_inv(a.bmax[((size_t)bb * a.heads + h) * jp + min(qq, n - 1)]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      qf[r][qb].load(a.q + (((size_t)rr[r] * a.heads + h) * jp + qq) * 32 + 8 * g);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) kmv[r] = __uint_as_float(a.kmax[(size_t)rr[r] * a.heads + h]);
+  issue(0, 0);
+  bool skip = true;
+#pragma unroll
+  for (int r = 0; r < R; ++r) skip &= (row0 + r >= a.rows) | (rf[r] != 0);
+  bool over = false;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      qf[r][qb].load(a.q + (((size_t)rr[r] * a.heads + h) * jp + qq) * 32 + 8 * g);
       float q2 = 0.f;
       for (int e = 0; e < 8; ++e) q2 += qf[r][qb].get(e) * qf[r][qb].get(e);
-      const float km = __uint_as_float(a.kmax[(size_t)rr[r] * a.heads + h]);
-      over = over || (sqrtf(group_sum_fast(q2)) * km + bq > kFastBound);
+      over = over || (sqrtf(group_sum_fast(q2)) * kmv[r] + bqv[qb] > kFastBound);
     }
-  }
   if (__any(over) && !skip) {
     if (l < R && row0 + l < a.rows) a.rowflag[row0 + l] = 1;
     skip = true;
@@ -980,7 +993,6 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
       if constexpr (kMfmaSum) lacc[r][qb] = o[r][0][qb];
     }
 
-  issue(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   // Two key blocks per trip with the stage buffer a compile-time constant, so
@@ -1104,7 +1116,7 @@ __global__ __launch_bounds__(64 * RG * QS) void triatt_core_fast_kernel(TriattCo
       if constexpr (kMfmaSum) lt = lacc[r][qb][0];
       else lt = group_sum_fast(lsum[r][qb]);
       ur = ur || !(lt >= kUnderflowSum);
-      inv[r][qb] = 1.0f / lt;
+      inv[r][qb] = __builtin_amdgcn_rcpf(lt);  // lt >= kUnderflowSum here, else flagged
     }
     if (__any(ur)) under |= 1 << r;
   }
