@@ -743,11 +743,17 @@ __device__ __forceinline__ Frag<float> ones_frag(float) {
   return f;
 }
 
-// Epilogue shared by both cores: 1/l, sigmoid gate, store.
+// Epilogue shared by both cores: 1/l, sigmoid gate, store.  The lane's
+// output address is formed once; rows and query blocks step it by uniform
+// (scalar) offsets, so no per-store 64-bit multiplies run on the VALU.
 template <typename CT, int R, int QB>
 __device__ __forceinline__ void core_store(const TriattCoreArgs<CT>& a, int row0, int h, int q0,
                                            f32x4 (&o)[R][2][QB], const float (&inv)[R][QB]) {
   const int g = lane_id() >> 4, r16 = lane_id() & 15;
+  CT* const base = a.out + (int64_t)row0 * a.o_row + (int64_t)h * a.o_h +
+                   (int64_t)(q0 + r16) * a.o_j + 8 * g;
+  const CT* const gbase =
+      a.gate ? a.gate + (((size_t)row0 * a.heads + h) * a.jp + q0 + r16) * 32 + 8 * g : nullptr;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
@@ -763,14 +769,14 @@ __device__ __forceinline__ void core_store(const TriattCoreArgs<CT>& a, int row0
 #pragma unroll
         for (int e = 0; e < 4; ++e) ov[4 * db + e] = o[r][db][qb][e] * inv[r][qb];
       if (a.gate) {
-        const CT* gp = a.gate + (((size_t)row * a.heads + h) * a.jp + qq) * 32 + 8 * g;
+        const CT* gp = gbase + ((size_t)r * a.heads * a.jp + 16 * qb) * 32;
         float gv[8];
         load4(gp, gv);
         load4(gp + 4, gv + 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e) ov[e] *= gv[e];
       }
-      CT* dst = a.out + (int64_t)row * a.o_row + (int64_t)h * a.o_h + (int64_t)qq * a.o_j + 8 * g;
+      CT* dst = base + (int64_t)r * a.o_row + (int64_t)(16 * qb) * a.o_j;
       if constexpr (sizeof(CT) == 2) {
         if (a.out16) {
           bf16x8 v8;
