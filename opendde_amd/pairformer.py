@@ -234,6 +234,18 @@ def _hip_covers(mod: nn.Module, z: torch.Tensor, name: str) -> bool:
     return why is None
 
 
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device: torch.device) -> "torch.cuda.Stream":
+    """One extra stream per device (default priority) for the single track."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(idx)
+    if st is None:
+        st = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return st
+
+
 class PairformerBlock(nn.Module):
     """Algorithm 17 block (pairformer.py:59-273)."""
 
@@ -262,6 +274,17 @@ class PairformerBlock(nn.Module):
                 triangle_multiplicative: str = "torch", triangle_attention: str = "torch",
                 inplace_safe: bool = False, chunk_size: Optional[int] = None,
                 extra_attn_bias: Optional[torch.Tensor] = None):
+        z, z_bias, accel = self.pair_update(z, pair_mask, triangle_multiplicative,
+                                            triangle_attention, inplace_safe, chunk_size)
+        s = self.single_update(s, z, z_bias, accel, extra_attn_bias)
+        return s, z
+
+    def pair_update(self, z: torch.Tensor, pair_mask: torch.Tensor,
+                    triangle_multiplicative: str = "torch", triangle_attention: str = "torch",
+                    inplace_safe: bool = False, chunk_size: Optional[int] = None):
+        """The pair track of the block (pairformer.py:196-227): returns the
+        updated z, the single track's pair bias when the fused transition
+        formed it (else None), and whether the accelerated path runs."""
         hook.check_multiplicative_kernel(triangle_multiplicative)
         hook.check_attention_kernel(triangle_attention)
         hip_mul = hook.is_accelerated(triangle_multiplicative) and z.is_cuda
@@ -313,6 +336,13 @@ class PairformerBlock(nn.Module):
         else:
             upd = self.pair_transition(z)
             z = z.add_(upd) if inplace_safe else z + upd
+        return z, z_bias, accel
+
+    def single_update(self, s: Optional[torch.Tensor], z: torch.Tensor,
+                      z_bias: Optional[torch.Tensor], accel: bool,
+                      extra_attn_bias: Optional[torch.Tensor] = None):
+        """The single track of the block (pairformer.py:228-273).  With
+        ``z_bias`` given, z is not read."""
         if self.c_s > 0:
             s = s + self.attention_pair_bias(a=s, s=None, z=z, extra_attn_bias=extra_attn_bias,
                                              z_bias=z_bias, hip=accel)
@@ -320,7 +350,7 @@ class PairformerBlock(nn.Module):
                 s = self.single_transition.hip_apply(s.contiguous(), add_residual=True)
             else:
                 s = s + self.single_transition(s)
-        return s, z
+        return s
 
 
 class PairformerStack(nn.Module):
@@ -339,11 +369,57 @@ class PairformerStack(nn.Module):
                             num_intermediate_factor=num_intermediate_factor,
                             hidden_scale_up=hidden_scale_up) for _ in range(n_blocks))
 
+    # Run each block's single track on a second stream, beside the next
+    # block's pair track (see forward).
+    overlap_single_track = True
+
     def forward(self, s, z, pair_mask, triangle_multiplicative: str = "torch",
                 triangle_attention: str = "torch", inplace_safe: bool = False,
                 chunk_size: Optional[int] = None, extra_attn_bias=None):
+        if (self.overlap_single_track and s is not None and z.is_cuda and len(self.blocks) > 1
+                and (hook.is_accelerated(triangle_multiplicative)
+                     or hook.is_accelerated(triangle_attention))):
+            return self._forward_overlapped(s, z, pair_mask, triangle_multiplicative,
+                                            triangle_attention, inplace_safe, chunk_size,
+                                            extra_attn_bias)
         for b in self.blocks:
             s, z = b(s, z, pair_mask, triangle_multiplicative=triangle_multiplicative,
                      triangle_attention=triangle_attention, inplace_safe=inplace_safe,
                      chunk_size=chunk_size, extra_attn_bias=extra_attn_bias)
+        return s, z
+
+    def _forward_overlapped(self, s, z, pair_mask, triangle_multiplicative, triangle_attention,
+                            inplace_safe, chunk_size, extra_attn_bias):
+        """The z track of the stack never reads s (pairformer.py:196-227), and
+        a block's single track reads z only through the pair bias that the
+        fused pair transition writes into its own buffer.  So block b's
+        single track runs on a second stream while block b + 1's pair track
+        runs on the caller's: the second stream waits for an event recorded
+        after block b's pair transition, and the caller's stream waits for
+        the second stream before returning.  The kernels and their inputs
+        are those of the sequential order, so the results are bit-identical;
+        the single track's small kernels fill the pair kernels' tails.  A
+        block whose pair bias the transition could not form (its single
+        track would read z, which the next block overwrites in place) runs
+        its single track in order on the caller's stream."""
+        main = torch.cuda.current_stream(z.device)
+        side = _side_stream(z.device)
+        for b in self.blocks:
+            z, z_bias, accel = b.pair_update(z, pair_mask, triangle_multiplicative,
+                                             triangle_attention, inplace_safe, chunk_size)
+            if b.c_s <= 0:
+                continue
+            if z_bias is None:
+                main.wait_stream(side)
+                s = b.single_update(s, z, None, accel, extra_attn_bias)
+                continue
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                s = b.single_update(s, z, z_bias, accel, extra_attn_bias)
+            # z_bias was allocated on the caller's stream: keep its memory from
+            # being reused there before the second stream has read it
+            z_bias.record_stream(side)
+        main.wait_stream(side)
+        # s was allocated on the second stream and is used on the caller's
+        s.record_stream(main)
         return s, z

@@ -186,17 +186,37 @@ def test_opendde_v1_width_stack_48_blocks_drifts_less_than_reference_bf16():
             assert hr <= BF16_REL_L2 and hm <= BF16_MAX_ABS, f"block {i + 1}: {hr:.3e} / {hm:.3e}"
 
 
-def test_stack_equals_block_loop():
-    # the stack is the block loop: the trunk comparison above runs block by
-    # block, the benchmark runs the stack
-    cfg = wl.PairConfig("trunk_short", 96, n_blocks=3, n_pad=5, random_pad=True, seed=3)
+@pytest.mark.parametrize("n,bf16,inplace", [(96, True, True), (256, True, True),
+                                             (256, True, False), (130, False, True)])
+def test_stack_equals_block_loop(n, bf16, inplace):
+    """The stack is the block loop, bit for bit: the trunk comparison above
+    runs block by block, the benchmark runs the stack, whose single track
+    runs on a second stream beside the next block's pair track (and, with
+    that switched off, in order)."""
+    say(f"[gpu] stack vs block loop n={n} bf16={bf16} inplace={inplace}")
+    cfg = wl.PairConfig("trunk_short", n, n_blocks=4, n_pad=n // 20, random_pad=True, seed=3)
     z0, s0, mask, gen = wl.make_inputs(cfg)
     stack = _stack(cfg, gen)
     z0, s0, mask = z0.to(DEV), s0.to(DEV), mask.to(DEV)
-    zh, sh = z0.clone(), s0
-    for blk in stack.blocks:
-        sh, zh = _hip_block(blk, sh, zh, mask)
-    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
-        ss, zs = stack(s0, z0.clone(), mask, triangle_multiplicative="hip",
-                       triangle_attention="hip", inplace_safe=True)
-    assert torch.equal(zs, zh) and torch.equal(ss, sh)
+
+    def run(fn):
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=bf16):
+            return fn()
+
+    def loop():
+        zh, sh = z0.clone(), s0
+        for blk in stack.blocks:
+            sh, zh = blk(sh, zh, mask, triangle_multiplicative="hip", triangle_attention="hip",
+                         inplace_safe=inplace)
+        return sh, zh
+
+    sh, zh = run(loop)
+    results = {}
+    for overlap in (True, False):
+        stack.overlap_single_track = overlap
+        results[overlap] = run(lambda: stack(s0, z0.clone(), mask, triangle_multiplicative="hip",
+                                             triangle_attention="hip", inplace_safe=inplace))
+    stack.overlap_single_track = True
+    torch.cuda.synchronize()
+    for overlap, (ss, zs) in results.items():
+        assert torch.equal(zs, zh) and torch.equal(ss, sh), f"overlap={overlap}"
