@@ -106,11 +106,12 @@ def _gpu_params(mod):
     return {k: v.detach().float() for k, v in mod.named_parameters()}
 
 
-@pytest.mark.parametrize("n", [1024, 1200])
+@pytest.mark.parametrize("n", [740, 1024, 1200])
 @pytest.mark.parametrize("outgoing", [True, False])
 def test_triangle_multiplication_large_contraction_bf16(n, outgoing):
-    """Np = 1024 and 1280 (4 x 4 and 5 x 5 tiles of 256 x 256) take the large
-    contraction kernel; bf16 z against the fp32 oracle run on the GPU."""
+    """Np = 768, 1024 and 1280 (3 x 3, 4 x 4 and 5 x 5 tiles of 256 x 256)
+    take the large contraction kernel (N = 740 with a random pad mask); bf16 z
+    against the fp32 oracle run on the GPU."""
     gen = wl.generator(900 + n)
     cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
     mod = cls(128, 128)
