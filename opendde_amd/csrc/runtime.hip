@@ -58,6 +58,16 @@ int resident_grid(const void* kernel, int threads) {
   return (per > 0 ? per : 1) * (cus > 0 ? cus : 1);
 }
 
+int proj_split(int64_t wgs, int max_split) {
+  static const int forced = [] {
+    const char* e = getenv("ODDE_PROJ_SPLIT");
+    return e ? atoi(e) : 0;
+  }();
+  int s = 1;
+  while (max_split % (2 * s) == 0 && (forced > 0 ? 2 * s <= forced : wgs * s < 1024)) s *= 2;
+  return s;
+}
+
 LaunchScope::LaunchScope(int kernel_id, hipStream_t s, bool events)
     : id(kernel_id), stream(s), slot(-1) {
   g_launches[id].fetch_add(1, std::memory_order_relaxed);

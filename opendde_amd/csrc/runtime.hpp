@@ -45,6 +45,13 @@ struct Carver {
 };
 
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Output-channel split (gridDim.z) for the fp32 projections, whose
+// workgroups each walk all output channels: the smallest power of two s
+// dividing `max_split` with wgs * s >= 1024 (four workgroups per CU of an
+// MI355X), so small problems still keep two or more waves on every SIMD.
+// ODDE_PROJ_SPLIT fixes s (tuning; clamped to those divisors).
+int proj_split(int64_t wgs, int max_split);
 inline int dtype_size(int dt) { return dt == ODDE_BF16 ? 2 : 4; }
 inline bool valid_dtype(int dt) { return dt == ODDE_F32 || dt == ODDE_BF16; }
 

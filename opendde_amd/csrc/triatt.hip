@@ -162,6 +162,9 @@ struct TriattProjArgs {
 // consecutive rows i: every weight fragment it reads from L2 serves kRB row
 // blocks (the fp32 form, whose weights are too large to hold, is bound by
 // those reads).  Rows i at or past n are skipped (workgroup-uniform).
+// blockIdx.z of gridDim.z takes heads [z H / Z, (z + 1) H / Z) of q, k, v
+// and the gate (small grids); z = 0 also writes the mask outputs and the
+// triangle bias.
 // kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
 template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
@@ -172,6 +175,9 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
   const int jl = j0 + r16;
   const int i0 = blockIdx.y * kRB;
   const int H = a.heads, HD = H * 32, jp = a.jp;
+  const bool lead = blockIdx.z == 0;
+  const int ob_per = (HD / 16) / (int)gridDim.z;  // whole heads: two blocks each
+  const int ob_lo = (int)blockIdx.z * ob_per, ob_hi = ob_lo + ob_per;
   MF x[kRB][kC];
 
   // mask rows: additive form for the exact core, keep flags for the fast one
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
       kp = m == 1.0f ? 1.f : 0.f;
     }
     if (g == 0) {
-      if (live) a.mb[(size_t)i * jp + jl] = mv;
+      if (live && lead) a.mb[(size_t)i * jp + jl] = mv;
       keep_s[rb][w * 16 + r16] = kp;
     }
     const bool any_masked = __any(mv != 0.f);
@@ -209,11 +215,11 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     const int i = i0 + rb;
     zero_v[rb] = false;
     if (i >= a.n) continue;
-    if (threadIdx.x < 2) {
+    if (lead && threadIdx.x < 2) {
       const int b = threadIdx.x;  // 32-key block b of this 64-key tile = waves 2b, 2b+1
       a.mflag[(size_t)i * (jp >> 5) + blockIdx.x * 2 + b] = wmasked[rb][2 * b] | wmasked[rb][2 * b + 1];
     }
-    if (threadIdx.x < 64) {
+    if (lead && threadIdx.x < 64) {
       const int t = threadIdx.x, kb = t >> 5, s = t & 31;
       a.keep[((size_t)i * (jp >> 5) + blockIdx.x * 2 + kb) * 32 + s] =
           from_f32<CT>(keep_s[rb][kb * 32 + slot_key(s >> 3, s & 7)]);
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
   float ss[kRB];
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) ss[rb] = 0.f;
-  for (int ob = 0; ob < HD / 16; ++ob) {
+  for (int ob = ob_lo; ob < ob_hi; ++ob) {
     f32x4 aq[kRB], ak[kRB], ag[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) aq[rb] = ak[rb] = ag[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -271,7 +277,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
   for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
     for (int e = 0; e < 4; ++e) vk[rb][e] = zero_v[rb] ? keep_s[rb][w * 16 + 4 * g + e] : 1.f;
-  for (int ob = 0; ob < HD / 16; ++ob) {
+  for (int ob = ob_lo; ob < ob_hi; ++ob) {
     f32x4 av[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) av[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -293,7 +299,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
   }
 
   // triangle bias: channel h = r16 (< H), rows jb..jb+3 -> bias[h][i][jb..]
-  {
+  if (lead) {
     f32x4 ab[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) ab[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1936,11 +1942,12 @@ void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st)
   // large enough (n >= 256)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 8 ? 2 : 1;
   if (kRB > 1 && n >= 256) {
-    dim3 grid(jp / 64, (n + kRB - 1) / kRB);
+    const int rows = (n + kRB - 1) / kRB;
+    dim3 grid(jp / 64, rows, proj_split((int64_t)(jp / 64) * rows, p.heads));
     hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, kRB, kX3Mul>), grid, dim3(256), 0, st, p);
     return;
   }
-  dim3 grid(jp / 64, n);
+  dim3 grid(jp / 64, n, proj_split((int64_t)(jp / 64) * n, p.heads));
   hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, 1, kX3Mul>), grid, dim3(256), 0, st, p);
 }
 // f32 compute: true fp32 products, or three bf16 parts (x3)

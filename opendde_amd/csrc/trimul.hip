@@ -54,7 +54,8 @@ struct TrimulProjArgs {
 // as bf16 rows of 2 Np, [hi | lo] with hi = bf16(a) and lo = bf16(a - hi),
 // for the three-part contraction.  kX3Mul (f32 compute, ODDE_F32X3): the
 // projections' products in three bf16 parts (rows split once after the
-// LayerNorm, weight fragments as they are read).
+// LayerNorm, weight fragments as they are read).  blockIdx.z of gridDim.z
+// takes channels [z Ch / Z, (z + 1) Ch / Z) (small grids).
 template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
@@ -87,7 +88,8 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
     }
   }
   const int ch = a.ch, np = a.np;
-  for (int cb = 0; cb < ch / 16; ++cb) {
+  const int cb_per = (ch / 16) / (int)gridDim.z;
+  for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
     f32x4 ap[kRB], ag[kRB], bp[kRB], bg[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) ap[rb] = ag[rb] = bp[rb] = bg[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1142,12 +1144,12 @@ void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   // large enough (np >= 256: np^2 / 256 workgroups and more)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
   if (kX3Out || (kRB > 1 && p.np >= 256)) {
-    dim3 grid(p.np / 64, p.np / kRB);
+    dim3 grid(p.np / 64, p.np / kRB, proj_split((int64_t)(p.np / 64) * (p.np / kRB), p.ch / 16));
     hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kRB, kX3Out, kX3Mul>), grid, dim3(256), 0,
                        st, p);
     return;
   }
-  dim3 grid(p.np / 64, p.np);
+  dim3 grid(p.np / 64, p.np, proj_split((int64_t)(p.np / 64) * p.np, p.ch / 16));
   hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, 1, false, kX3Mul>), grid, dim3(256), 0, st, p);
 }
 template <typename ZT, int kC>

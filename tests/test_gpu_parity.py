@@ -9,7 +9,7 @@ rel-L2 <= 1e-2 and max-abs <= 5e-2 vs the fp32 oracle fed the same
 import pytest
 import torch
 
-from helpers import (assert_bf16, assert_fp32, params_of, rel_l2, say, seeded,
+from helpers import (assert_bf16, assert_fp32, margin, params_of, rel_l2, say, seeded,
                      token_pair_mask)
 from oracle import reference as ref
 from opendde_amd import _lib
@@ -264,13 +264,21 @@ def test_triangle_attention_large_logits_take_exact_path():
     z = _z(n, 128, 32)
     mask = token_pair_mask(n, pad)
     exp = ref.triangle_attention(z, mask, params_of(mod), 4)
+    exp64 = ref.triangle_attention(z.double(), mask.double(), params_of(mod, torch.float64), 4)
     got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
-    r = _rel(got[: n - pad], exp[: n - pad])
-    say(f"    large-logit rel max err {r:.2e}")
+    kept = slice(0, n - pad)
+    r = _rel(got[kept], exp[kept])
+    r_hip = _rel(got[kept], exp64[kept])
+    r_ref = _rel(exp[kept], exp64[kept])
+    say(f"    large-logit rel max err {r:.2e} vs the fp32 oracle; against float64: "
+        f"HIP {r_hip:.2e}, fp32 oracle {r_ref:.2e}")
+    margin("triatt large logits, kept rows, rel max err vs float64 [fp32]", hip=r_hip,
+           fp32_oracle=r_ref)
     # logits of hundreds of nats: a 1e-7 relative rounding difference in a
     # logit moves its weight by ~1e-5, so the bound reflects conditioning;
     # the overflowing fast path would be off by orders of magnitude
     assert torch.isfinite(got).all() and r < 1e-3
+    assert r_hip < 1e-3
 
 
 def test_triangle_attention_underflowing_rows_take_exact_path():
