@@ -1342,6 +1342,8 @@ struct TriattOutArgs {
 
 // kRB consecutive rows i per workgroup: every weight fragment a wave reads
 // from L2 serves kRB row blocks (the fp32 form reads W_o per fragment).
+// blockIdx.z of gridDim.z takes output channels [z C / Z, (z + 1) C / Z)
+// (small grids).
 template <typename ZT, typename CT, int kHD, bool kX3Mul = false, int kRB = 1>
 __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a) {
   constexpr int HD = kHD * 32;
@@ -1360,7 +1362,8 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
       else x[rb][t].zero();
     }
   }
-  for (int cb = 0; cb < a.c / 16; ++cb) {
+  const int cb_per = (a.c / 16) / (int)gridDim.z;
+  for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
     f32x4 acc[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2024,7 +2027,8 @@ void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStrea
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kHD <= 4 ? 4 : kHD <= 8 ? 2 : 1;
   if constexpr (kRB > 1) {
     if (n >= 256) {
-      dim3 grid(jp / 64, (n + kRB - 1) / kRB);
+      const int rows = (n + kRB - 1) / kRB;
+      dim3 grid(jp / 64, rows, proj_split((int64_t)(jp / 64) * rows, p.c / 16));
       if (x3)
         hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true, kRB>), grid, dim3(256), 0, st, p);
       else
@@ -2032,7 +2036,7 @@ void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStrea
       return;
     }
   }
-  dim3 grid(jp / 64, n);
+  dim3 grid(jp / 64, n, proj_split((int64_t)(jp / 64) * n, p.c / 16));
   if constexpr (sizeof(CT) == 4) {
     if (x3) {
       hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true>), grid, dim3(256), 0, st, p);

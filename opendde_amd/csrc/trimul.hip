@@ -463,6 +463,8 @@ __global__ __launch_bounds__(256) void trimul_fold_ln_out_kernel(const float* __
 }
 
 // kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
+// blockIdx.z of gridDim.z takes output channels [z C / Z, (z + 1) C / Z)
+// (small grids).
 template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a) {
   constexpr int C = kC * 32, CH = kCh * 32;
@@ -504,7 +506,8 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a
     for (int t = 0; t < kC; ++t) to_mul(tz[t], xz[t]);
   }
 
-  for (int cb = 0; cb < C / 16; ++cb) {
+  const int cb_per = (C / 16) / (int)gridDim.z;
+  for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
     f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
 #pragma unroll
     for (int t = 0; t < kCh; ++t) {
@@ -1202,7 +1205,14 @@ bool launch_to_ws(const TrimulOutArgs<ZT, CT>& p, int C, int ch, hipStream_t st)
 
 template <typename ZT, typename CT, int kC, int kCh>
 void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
-  dim3 grid(p.np / 64, p.n);
+  // every workgroup reads all channels of its z rows (LN_in for the gate):
+  // with out overlapping z, a channel split would let one split overwrite
+  // rows another still reads, so the in-place form keeps one workgroup per
+  // row block
+  const int64_t ext = (int64_t)(p.n - 1) * (p.z_s0 + p.z_s1) + kC * 32;
+  const int64_t oext = (int64_t)(p.n - 1) * (p.o_s0 + p.o_s1) + kC * 32;
+  const bool overlap = p.out < p.z + ext && p.z < p.out + oext;
+  dim3 grid(p.np / 64, p.n, overlap ? 1 : proj_split((int64_t)(p.np / 64) * p.n, kC * 2));
   if constexpr (sizeof(CT) == 4) {
     if (x3) {
       hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh, true>), grid, dim3(256), 0, st, p);

@@ -275,10 +275,12 @@ def test_triangle_attention_large_logits_take_exact_path():
     margin("triatt large logits, kept rows, rel max err vs float64 [fp32]", hip=r_hip,
            fp32_oracle=r_ref)
     # logits of hundreds of nats: a 1e-7 relative rounding difference in a
-    # logit moves its weight by ~1e-5, so the bound reflects conditioning;
-    # the overflowing fast path would be off by orders of magnitude
+    # logit moves its weight by ~1e-5, so the fp32 oracle itself is ~1.5e-5
+    # from the float64 result; the HIP path must be as close to it as the
+    # reference's own fp32 arithmetic (within 3x), where the overflowing fast
+    # path would be off by orders of magnitude
     assert torch.isfinite(got).all() and r < 1e-3
-    assert r_hip < 1e-3
+    assert r_hip <= 3 * r_ref
 
 
 def test_triangle_attention_underflowing_rows_take_exact_path():
