@@ -463,72 +463,88 @@ __global__ __launch_bounds__(256) void trimul_fold_ln_out_kernel(const float* __
 }
 
 // kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
-// blockIdx.z of gridDim.z takes output channels [z C / Z, (z + 1) C / Z)
-// (small grids).
-template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul = false>
+// kRB consecutive first indices x per workgroup: every W_z and W_g fragment
+// a wave reads from L2 serves kRB row blocks (the fp32 form reads its
+// weights per fragment).  blockIdx.z of gridDim.z takes output channels
+// [z C / Z, (z + 1) C / Z) (small grids).
+template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul = false, int kRB = 1>
 __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a) {
   constexpr int C = kC * 32, CH = kCh * 32;
   using MF = MulFrag<CT, kX3Mul>;
   constexpr int LD = CH + 16 / sizeof(CT);   // row stride of the transposed tile
-  __shared__ __attribute__((aligned(16))) CT pt[64 * LD];
+  __shared__ __attribute__((aligned(16))) CT pt[kRB][64 * LD];
 
-  const int x_ = blockIdx.y;
+  const int x0 = blockIdx.y * kRB;
   const int y0 = blockIdx.x * 64;
-  // stage P[:, x_, y0:y0+64] transposed to pt[y][c]
-  {
+  // stage P[:, x, y0:y0+64] transposed to pt[rb][y][c] (rows x past n read
+  // row n - 1, which exists, and are never stored)
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
     constexpr int VEC = 16 / sizeof(CT);
     constexpr int PER_C = 64 / VEC;              // 16-byte chunks per channel row
-    const CT* src = a.P + (size_t)x_ * a.np + y0;
+    const CT* src = a.P + (size_t)min(x0 + rb, a.n - 1) * a.np + y0;
     for (int ci = threadIdx.x; ci < CH * PER_C; ci += 256) {
       const int c = ci / PER_C, yy = (ci % PER_C) * VEC;
       CT v[VEC];
       *reinterpret_cast<f32x4*>(v) =
           *reinterpret_cast<const f32x4*>(src + (size_t)c * a.np * a.np + yy);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) pt[(yy + e) * LD + c] = v[e];
+      for (int e = 0; e < VEC; ++e) pt[rb][(yy + e) * LD + c] = v[e];
     }
   }
   __syncthreads();
 
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int yl = y0 + w * 16 + r16;
-  const bool valid = x_ < a.n && yl < a.n;
-  MF xp[kCh], xz[kC];
-  const ZT* zrow = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
-  {
+  MF xp[kRB][kCh], xz[kRB][kC];
+  bool valid[kRB];
+  const ZT* zrow[kRB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    const int x_ = x0 + rb;
+    valid[rb] = x_ < a.n && yl < a.n;
+    zrow[rb] = a.z + (int64_t)(valid[rb] ? x_ : 0) * a.z_s0 + (int64_t)(valid[rb] ? yl : 0) * a.z_s1;
     Frag<CT> tp[kCh], tz[kC];
-    ln_rows_to_frags<CT, CT, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b, a.eps,
+    ln_rows_to_frags<CT, CT, CH>(&pt[rb][(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b, a.eps,
                                  tp);
-    ln_rows_to_frags<ZT, CT, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, tz);
+    ln_rows_to_frags<ZT, CT, C>(zrow[rb], valid[rb], a.ln_in_w, a.ln_in_b, a.eps, tz);
 #pragma unroll
-    for (int t = 0; t < kCh; ++t) to_mul(tp[t], xp[t]);
+    for (int t = 0; t < kCh; ++t) to_mul(tp[t], xp[rb][t]);
 #pragma unroll
-    for (int t = 0; t < kC; ++t) to_mul(tz[t], xz[t]);
+    for (int t = 0; t < kC; ++t) to_mul(tz[t], xz[rb][t]);
   }
 
   const int cb_per = (C / 16) / (int)gridDim.z;
   for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
-    f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
+    f32x4 ay[kRB], agt[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) ay[rb] = agt[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < kCh; ++t) {
       MF f;
       load_w_frag(a.wz, CH, cb * 16, C, t, f);
-      mma(ay, f, xp[t]);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) mma(ay[rb], f, xp[rb][t]);
     }
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
       load_w_frag(a.wg, C, cb * 16, C, t, f);
-      mma(agt, f, xz[t]);
-    }
-    if (!valid) continue;
-    const int c0 = cb * 16 + 4 * g;
-    float base[4] = {0.f, 0.f, 0.f, 0.f};
-    if (a.add) load4(zrow + c0, base);
-    float r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[e] * sigmoidf_(agt[e]);
-    store4(a.out + (int64_t)x_ * a.o_s0 + (int64_t)yl * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+      for (int rb = 0; rb < kRB; ++rb) mma(agt[rb], f, xz[rb][t]);
+    }
+    const int c0 = cb * 16 + 4 * g;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      if (!valid[rb]) continue;
+      float base[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.add) load4(zrow[rb] + c0, base);
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[rb][e] * sigmoidf_(agt[rb][e]);
+      store4(a.out + (int64_t)(x0 + rb) * a.o_s0 + (int64_t)yl * a.o_s1 + c0, r[0], r[1], r[2],
+             r[3]);
+    }
   }
 }
 
@@ -1203,8 +1219,8 @@ bool launch_to_ws(const TrimulOutArgs<ZT, CT>& p, int C, int ch, hipStream_t st)
   }
 }
 
-template <typename ZT, typename CT, int kC, int kCh>
-void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
+template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul, int kRB>
+void launch_to_rb(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
   // every workgroup reads all channels of its z rows (LN_in for the gate):
   // with out overlapping z, a channel split would let one split overwrite
   // rows another still reads, so the in-place form keeps one workgroup per
@@ -1212,14 +1228,25 @@ void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
   const int64_t ext = (int64_t)(p.n - 1) * (p.z_s0 + p.z_s1) + kC * 32;
   const int64_t oext = (int64_t)(p.n - 1) * (p.o_s0 + p.o_s1) + kC * 32;
   const bool overlap = p.out < p.z + ext && p.z < p.out + oext;
-  dim3 grid(p.np / 64, p.n, overlap ? 1 : proj_split((int64_t)(p.np / 64) * p.n, kC * 2));
+  const int rows = (p.n + kRB - 1) / kRB;
+  dim3 grid(p.np / 64, rows, overlap ? 1 : proj_split((int64_t)(p.np / 64) * rows, kC * 2));
+  hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh, kX3Mul, kRB>), grid, dim3(256), 0, st, p);
+}
+template <typename ZT, typename CT, int kC, int kCh>
+void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
   if constexpr (sizeof(CT) == 4) {
     if (x3) {
-      hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh, true>), grid, dim3(256), 0, st, p);
+      // three-part products: two first indices per workgroup share each
+      // weight fragment read from L2 (C = Ch = 128 at N = 1024: 1.24 -> 1.17
+      // ms).  With true fp32 products the shared form needs 256 VGPRs, one
+      // wave per SIMD, and is slower (1.21 -> 1.57 ms), so it keeps one.
+      constexpr int kRB = kC <= 4 && kCh <= 4 ? 2 : 1;
+      if (kRB > 1 && p.n >= 256) launch_to_rb<ZT, CT, kC, kCh, true, kRB>(p, st);
+      else launch_to_rb<ZT, CT, kC, kCh, true, 1>(p, st);
       return;
     }
   }
-  hipLaunchKernelGGL((trimul_out_kernel<ZT, CT, kC, kCh>), grid, dim3(256), 0, st, p);
+  launch_to_rb<ZT, CT, kC, kCh, false, 1>(p, st);
 }
 
 template <typename ZT, typename CT, int kC>
