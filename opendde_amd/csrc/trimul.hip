@@ -55,11 +55,21 @@ struct TrimulProjArgs {
 // for the three-part contraction.  kX3Mul (f32 compute, ODDE_F32X3): the
 // projections' products in three bf16 parts (rows split once after the
 // LayerNorm, weight fragments as they are read).  blockIdx.z of gridDim.z
-// takes channels [z Ch / Z, (z + 1) Ch / Z) (small grids).
-template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false, bool kX3Mul = false>
+// takes channels [z Ch / Z, (z + 1) Ch / Z) (small grids).  kStage (true
+// fp32 products): the four weight rows blocks of each 16-channel block are
+// staged in LDS, double-buffered, and shared by the workgroup's 4 waves, so
+// a weight byte fetched from L2 serves 64 kRB rows instead of 16 kRB.
+template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false, bool kX3Mul = false,
+          bool kStage = false>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
   using MF = MulFrag<CT, kX3Mul>;
+  static_assert(!kStage || (sizeof(CT) == 4 && !kX3 && !kX3Mul), "staging: true fp32 products");
+  constexpr int WL = C + 4;                     // staged row stride (floats)
+  constexpr int CHUNK = 4 * 16 * WL;            // a_p, a_g, b_p, b_g rows of one block
+  constexpr int PT = 4 * 16 * C / 4;            // 16-byte pieces per chunk
+  constexpr int PPT = (PT + 255) / 256;
+  __shared__ __attribute__((aligned(16))) float wsm[kStage ? 2 * CHUNK : 4];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int y0 = blockIdx.x * 64 + w * 16;
   const int yl = y0 + r16;
@@ -89,23 +99,60 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
   }
   const int ch = a.ch, np = a.np;
   const int cb_per = (ch / 16) / (int)gridDim.z;
-  for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
+  const int cb_lo = (int)blockIdx.z * cb_per, cb_hi = cb_lo + cb_per;
+  // staging: piece q of block cb is matrix m = q / (4 C) (a_p, a_g, b_p,
+  // b_g), row r, 16-byte column piece c4
+  f32x4 wreg[kStage ? PPT : 1];
+  auto wload = [&](int cb) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      if (PT % 256 == 0 || q < PT) {
+        const int m = q / (4 * C), u = q % (4 * C), r = u / (C / 4), c4 = u % (C / 4);
+        const CT* src = (m & 1) ? a.wg : a.wp;
+        wreg[k] = *reinterpret_cast<const f32x4*>(src + (size_t)((m >> 1) * ch + cb * 16 + r) * C +
+                                                  4 * c4);
+      }
+    }
+  };
+  auto wstore = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      if (PT % 256 == 0 || q < PT) {
+        const int m = q / (4 * C), u = q % (4 * C), r = u / (C / 4), c4 = u % (C / 4);
+        *reinterpret_cast<f32x4*>(&wsm[buf * CHUNK + (m * 16 + r) * WL + 4 * c4]) = wreg[k];
+      }
+    }
+  };
+  if constexpr (kStage) {
+    wload(cb_lo);
+    wstore(0);
+    if (cb_lo + 1 < cb_hi) wload(cb_lo + 1);
+    __syncthreads();
+  }
+  for (int cb = cb_lo; cb < cb_hi; ++cb) {
     f32x4 ap[kRB], ag[kRB], bp[kRB], bg[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) ap[rb] = ag[rb] = bp[rb] = bg[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* wsb = wsm + ((cb - cb_lo) & 1) * CHUNK + r16 * WL + 8 * g;
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
+      if constexpr (kStage) f.load(wsb + 32 * t);
+      else load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ap[rb], xf[rb][t], f);
-      load_w_frag(a.wg, C, cb * 16, 2 * ch, t, f);
+      if constexpr (kStage) f.load(wsb + 16 * WL + 32 * t);
+      else load_w_frag(a.wg, C, cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], xf[rb][t], f);
-      load_w_frag(a.wp, C, ch + cb * 16, 2 * ch, t, f);
+      if constexpr (kStage) f.load(wsb + 32 * WL + 32 * t);
+      else load_w_frag(a.wp, C, ch + cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(bp[rb], xf[rb][t], f);
-      load_w_frag(a.wg, C, ch + cb * 16, 2 * ch, t, f);
+      if constexpr (kStage) f.load(wsb + 48 * WL + 32 * t);
+      else load_w_frag(a.wg, C, ch + cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(bg[rb], xf[rb][t], f);
     }
@@ -140,6 +187,15 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
         store4(a.A + off, va[0], va[1], va[2], va[3]);
         store4(a.B + off, vb[0], vb[1], vb[2], vb[3]);
       }
+    }
+    if constexpr (kStage) {
+      // buffer (cb + 1 - cb_lo) & 1 was last read in block cb - 1, before
+      // the barrier that ended it
+      if (cb + 1 < cb_hi) {
+        wstore((cb + 1 - cb_lo) & 1);
+        if (cb + 2 < cb_hi) wload(cb + 2);
+      }
+      __syncthreads();
     }
   }
 }
@@ -545,6 +601,112 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a
       store4(a.out + (int64_t)(x0 + rb) * a.o_s0 + (int64_t)yl * a.o_s1 + c0, r[0], r[1], r[2],
              r[3]);
     }
+  }
+}
+
+// True fp32 products with W_z and W_g staged in LDS, 16 output channels at
+// a time, shared by the workgroup's 4 waves: every weight byte fetched from
+// L2 serves the workgroup's 64 rows instead of one wave's 16.  Chunks are
+// double-buffered (the next one waits in registers while the current one is
+// multiplied), one barrier per chunk.  One first index x per workgroup, as
+// trimul_out_kernel; the arithmetic per output is the same.
+template <typename ZT, int kC, int kCh>
+__global__ __launch_bounds__(256) void trimul_out_f32s_kernel(TrimulOutArgs<ZT, float> a) {
+  constexpr int C = kC * 32, CH = kCh * 32, NCB = C / 16;
+  constexpr int LD = CH + 4;                    // row stride of the transposed P tile
+  constexpr int WLZ = CH + 4, WLG = C + 4;      // staged W_z / W_g row strides (floats)
+  constexpr int WCH = 16 * WLZ + 16 * WLG;      // floats per chunk buffer
+  constexpr int PZ = 16 * CH / 4, PT = PZ + 16 * C / 4;  // 16-byte pieces per chunk
+  constexpr int PPT = (PT + 255) / 256;         // pieces per thread
+  __shared__ __attribute__((aligned(16))) float pt[64 * LD];
+  __shared__ __attribute__((aligned(16))) float wsm[2][WCH];
+
+  const int x_ = blockIdx.y;
+  const int y0 = blockIdx.x * 64;
+  f32x4 wreg[PPT];
+  auto wload = [&](int cb) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      if (q < PZ) {
+        const int r = q / (CH / 4), c4 = q % (CH / 4);
+        wreg[k] = *reinterpret_cast<const f32x4*>(a.wz + (size_t)(cb * 16 + r) * CH + 4 * c4);
+      } else if (q < PT) {
+        const int u = q - PZ, r = u / (C / 4), c4 = u % (C / 4);
+        wreg[k] = *reinterpret_cast<const f32x4*>(a.wg + (size_t)(cb * 16 + r) * C + 4 * c4);
+      }
+    }
+  };
+  auto wstore = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      if (q < PZ) {
+        const int r = q / (CH / 4), c4 = q % (CH / 4);
+        *reinterpret_cast<f32x4*>(&wsm[buf][r * WLZ + 4 * c4]) = wreg[k];
+      } else if (q < PT) {
+        const int u = q - PZ, r = u / (C / 4), c4 = u % (C / 4);
+        *reinterpret_cast<f32x4*>(&wsm[buf][16 * WLZ + r * WLG + 4 * c4]) = wreg[k];
+      }
+    }
+  };
+  wload(0);
+  // stage P[:, x, y0:y0+64] transposed to pt[y][c]
+  {
+    constexpr int PER_C = 16;                   // 16-byte chunks per channel row
+    const float* src = a.P + (size_t)x_ * a.np + y0;
+    for (int ci = threadIdx.x; ci < CH * PER_C; ci += 256) {
+      const int c = ci / PER_C, yy = (ci % PER_C) * 4;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + (size_t)c * a.np * a.np + yy);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pt[(yy + e) * LD + c] = v[e];
+    }
+  }
+  wstore(0);
+  if (NCB > 1) wload(1);
+  __syncthreads();  // pt and chunk 0 staged
+
+  const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
+  const int yl = y0 + w * 16 + r16;
+  const bool valid = x_ < a.n && yl < a.n;
+  Frag<float> xp[kCh], xz[kC];
+  const ZT* zrow = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
+  ln_rows_to_frags<float, float, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b,
+                                     a.eps, xp);
+  ln_rows_to_frags<ZT, float, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, xz);
+
+  for (int cb = 0; cb < NCB; ++cb) {
+    const float* wz_s = wsm[cb & 1] + r16 * WLZ + 8 * g;
+    const float* wg_s = wsm[cb & 1] + 16 * WLZ + r16 * WLG + 8 * g;
+    f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
+#pragma unroll
+    for (int t = 0; t < kCh; ++t) {
+      Frag<float> f;
+      f.load(wz_s + 32 * t);
+      mma(ay, f, xp[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < kC; ++t) {
+      Frag<float> f;
+      f.load(wg_s + 32 * t);
+      mma(agt, f, xz[t]);
+    }
+    if (valid) {
+      const int c0 = cb * 16 + 4 * g;
+      float base[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.add) load4(zrow + c0, base);
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = base[e] + ay[e] * sigmoidf_(agt[e]);
+      store4(a.out + (int64_t)x_ * a.o_s0 + (int64_t)yl * a.o_s1 + c0, r[0], r[1], r[2], r[3]);
+    }
+    // buffer (cb + 1) & 1 was last read in chunk cb - 1, before the barrier
+    // that ended it
+    if (cb + 1 < NCB) {
+      wstore((cb + 1) & 1);
+      if (cb + 2 < NCB) wload(cb + 2);
+    }
+    __syncthreads();
   }
 }
 
@@ -1154,6 +1316,16 @@ int check_trimul(const odde_trimul_args* a) {
   return ODDE_OK;
 }
 
+// ODDE_TRIMUL_PROJ_F32_PLAIN=1: the fp32 projection without staged weights
+// (tuning).  ODDE_TRIMUL_PROJ_SRB: row blocks per wave of the staged form.
+inline bool trimul_proj_f32_plain() {
+  static const bool v = [] {
+    const char* e = getenv("ODDE_TRIMUL_PROJ_F32_PLAIN");
+    return e && atoi(e) != 0;
+  }();
+  return v;
+}
+constexpr int kSRB = 2;
 // kX3Out: A and B as [hi | lo] bf16 rows (the three-part contraction);
 // kX3Mul: the projections' products in three bf16 parts (f32 compute)
 template <typename ZT, typename CT, int kC, bool kX3Out = false, bool kX3Mul = false>
@@ -1162,6 +1334,16 @@ void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
   // large enough (np >= 256: np^2 / 256 workgroups and more)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
+  if constexpr (sizeof(CT) == 4 && !kX3Out && !kX3Mul && kC <= 4) {
+    // true fp32 products from Np = 256: the weights staged in LDS (kSRB row
+    // blocks per wave)
+    if (p.np >= 256 && !trimul_proj_f32_plain()) {
+      dim3 grid(p.np / 64, p.np / kSRB);
+      hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kSRB, false, false, true>), grid, dim3(256),
+                         0, st, p);
+      return;
+    }
+  }
   if (kX3Out || (kRB > 1 && p.np >= 256)) {
     dim3 grid(p.np / 64, p.np / kRB, proj_split((int64_t)(p.np / 64) * (p.np / kRB), p.ch / 16));
     hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kRB, kX3Out, kX3Mul>), grid, dim3(256), 0,
@@ -1219,6 +1401,15 @@ bool launch_to_ws(const TrimulOutArgs<ZT, CT>& p, int C, int ch, hipStream_t st)
   }
 }
 
+// ODDE_TRIMUL_OUT_F32_PLAIN=1: the fp32 output kernel without staged
+// weights (tuning).
+inline bool trimul_out_f32_plain() {
+  static const bool v = [] {
+    const char* e = getenv("ODDE_TRIMUL_OUT_F32_PLAIN");
+    return e && atoi(e) != 0;
+  }();
+  return v;
+}
 template <typename ZT, typename CT, int kC, int kCh, bool kX3Mul, int kRB>
 void launch_to_rb(const TrimulOutArgs<ZT, CT>& p, hipStream_t st) {
   // every workgroup reads all channels of its z rows (LN_in for the gate):
@@ -1243,6 +1434,15 @@ void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
       constexpr int kRB = kC <= 4 && kCh <= 4 ? 2 : 1;
       if (kRB > 1 && p.n >= 256) launch_to_rb<ZT, CT, kC, kCh, true, kRB>(p, st);
       else launch_to_rb<ZT, CT, kC, kCh, true, 1>(p, st);
+      return;
+    }
+  }
+  if constexpr (sizeof(CT) == 4 && kC <= 4 && kCh <= 4) {
+    // true fp32 products from N = 256: weights staged in LDS (the grid no
+    // longer needs an output-channel split)
+    if (p.n >= 256 && !trimul_out_f32_plain()) {
+      hipLaunchKernelGGL((trimul_out_f32s_kernel<ZT, kC, kCh>), dim3(p.np / 64, p.n), dim3(256), 0,
+                         st, p);
       return;
     }
   }

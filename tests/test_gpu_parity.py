@@ -152,9 +152,11 @@ def test_attention_core_slot_matches_oracle():
 # ---------------------------------------------------------- multiplication
 
 
-@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("n", [17, 64, 130, 300])
 @pytest.mark.parametrize("outgoing", [True, False])
 def test_triangle_multiplication_fp32(n, outgoing):
+    # from n = 256 the output kernel stages its weights in LDS (n = 300: a
+    # padded grid of 320)
     cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
     mod = seeded(cls(128, 128), 400 + n, STD)
     z = _z(n, 128, 3 * n)
@@ -213,8 +215,9 @@ def test_triangle_multiplication_wide_bf16(c, ch, outgoing, n):
     assert_bf16(z2 - z.to(DEV), exp32, f"trimul wide fp32-z c={c} ch={ch} n={n} out={outgoing}")
 
 
-def test_triangle_multiplication_in_place_add():
-    n = 70
+@pytest.mark.parametrize("n", [70, 300])
+def test_triangle_multiplication_in_place_add(n):
+    # n = 70: the output kernel unsplit in place; n = 300: staged weights
     mod = seeded(TriangleMultiplicationOutgoing(128, 128), 9, STD).to(DEV)
     z = _z(n, 128, 10).to(DEV)
     mask = token_pair_mask(n, 6).to(DEV)
@@ -222,7 +225,7 @@ def test_triangle_multiplication_in_place_add():
     z2 = z.clone()
     out = mod(z2, mask, inplace_safe=True, _add_with_inplace=True, triangle_multiplicative="hip")
     assert out.data_ptr() == z2.data_ptr()
-    assert_fp32(z2, exp, "trimul in-place add")
+    assert_fp32(z2, exp, f"trimul in-place add n={n}")
 
 
 # ------------------------------------------------------------------- block
