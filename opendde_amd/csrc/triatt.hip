@@ -166,10 +166,19 @@ struct TriattProjArgs {
 // and the gate (small grids); z = 0 also writes the mask outputs and the
 // triangle bias.
 // kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
-template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3Mul = false>
+// kStage (true fp32 products, one split): the weight rows of each 16-channel
+// block -- W_q, W_k, W_g, then W_v, then the H bias rows -- are staged in
+// LDS, double-buffered, and shared by the workgroup's 4 waves.
+template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3Mul = false, bool kStage = false>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
   using MF = MulFrag<CT, kX3Mul>;
+  static_assert(!kStage || (sizeof(CT) == 4 && !kX3Mul), "staging: true fp32 products");
+  constexpr int WL = C + 4;                     // staged row stride (floats)
+  constexpr int CHUNK = 3 * 16 * WL;            // three 16-row slots
+  constexpr int PT = 3 * 16 * C / 4;            // 16-byte pieces per chunk
+  constexpr int PPT = (PT + 255) / 256;
+  __shared__ __attribute__((aligned(16))) float wsm[kStage ? 2 * CHUNK : 4];
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int j0 = blockIdx.x * 64 + w * 16;
   const int jl = j0 + r16;
@@ -179,6 +188,47 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
   const int ob_per = (HD / 16) / (int)gridDim.z;  // whole heads: two blocks each
   const int ob_lo = (int)blockIdx.z * ob_per, ob_hi = ob_lo + ob_per;
   MF x[kRB][kC];
+  // staged chunks: ci < NOB: W_q, W_k, W_g rows 16 ci ..; NOB <= ci < 2 NOB:
+  // W_v rows 16 (ci - NOB) .. in slot 0; ci = 2 NOB: the bias rows (< H,
+  // zeros above) in slot 0.  Piece q of a chunk: slot q / (4 C), row r,
+  // 16-byte column piece c4.
+  const int NOB = HD / 16, NCHK = 2 * NOB + 1;
+  f32x4 wreg[kStage ? PPT : 1];
+  auto wload = [&](int ci) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      const int sl = q / (4 * C), u = q % (4 * C), r = u / (C / 4), c4 = u % (C / 4);
+      const CT* src = nullptr;
+      if (ci < NOB) src = (sl == 0 ? a.wq : sl == 1 ? a.wk : a.wg) + (size_t)(ci * 16 + r) * C;
+      else if (sl == 0 && ci < 2 * NOB) src = a.wv + (size_t)((ci - NOB) * 16 + r) * C;
+      else if (sl == 0 && r < H) src = a.wb + (size_t)r * C;
+      wreg[k] = (PT % 256 == 0 || q < PT) && src ? *reinterpret_cast<const f32x4*>(src + 4 * c4)
+                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto wstore = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k;
+      const int sl = q / (4 * C), u = q % (4 * C), r = u / (C / 4), c4 = u % (C / 4);
+      if (PT % 256 == 0 || q < PT)
+        *reinterpret_cast<f32x4*>(&wsm[buf * CHUNK + (sl * 16 + r) * WL + 4 * c4]) = wreg[k];
+    }
+  };
+  // after chunk `cur` is multiplied: stage chunk cur + 1 (its buffer was
+  // last read in chunk cur - 1, before the barrier that ended it), request
+  // chunk cur + 2, and make chunk cur + 1 visible
+  int cur = 0;
+  auto advance = [&]() {
+    if (cur + 1 < NCHK) {
+      wstore((cur + 1) & 1);
+      if (cur + 2 < NCHK) wload(cur + 2);
+    }
+    __syncthreads();
+    ++cur;
+  };
+  auto wslot = [&](int sl) { return wsm + (cur & 1) * CHUNK + (sl * 16 + r16) * WL + 8 * g; };
 
   // mask rows: additive form for the exact core, keep flags for the fast one
   __shared__ float keep_s[kRB][64];
@@ -227,6 +277,12 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     zero_v[rb] = a.anykeep[i] != 0;
   }
 
+  if constexpr (kStage) {
+    wload(0);
+    wstore(0);
+    wload(1);
+    __syncthreads();
+  }
   // q, k, gate: product W x^T -> lane holds pair row jl, channels o..o+3.
   float ss[kRB];
 #pragma unroll
@@ -238,13 +294,16 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      load_w_frag(a.wq, C, ob * 16, HD, t, f);
+      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      else load_w_frag(a.wq, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(aq[rb], f, x[rb][t]);
-      load_w_frag(a.wk, C, ob * 16, HD, t, f);
+      if constexpr (kStage) f.load(wslot(1) + 32 * t);
+      else load_w_frag(a.wk, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ak[rb], f, x[rb][t]);
-      load_w_frag(a.wg, C, ob * 16, HD, t, f);
+      if constexpr (kStage) f.load(wslot(2) + 32 * t);
+      else load_w_frag(a.wg, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], f, x[rb][t]);
     }
@@ -268,6 +327,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
         ss[rb] = 0.f;
       }
     }
+    if constexpr (kStage) advance();
   }
 
   // v: product x W^T -> lane holds channel o, pair rows j0+4g .. +3.
@@ -284,7 +344,8 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      load_w_frag(a.wv, C, ob * 16, HD, t, f);
+      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      else load_w_frag(a.wv, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(av[rb], x[rb][t], f);
     }
@@ -296,6 +357,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
       store4(a.v + vperm_offset(i, o >> 5, H, jp, jb, o & 31), av[rb][0] * vk[rb][0],
              av[rb][1] * vk[rb][1], av[rb][2] * vk[rb][2], av[rb][3] * vk[rb][3]);
     }
+    if constexpr (kStage) advance();
   }
 
   // triangle bias: channel h = r16 (< H), rows jb..jb+3 -> bias[h][i][jb..]
@@ -306,7 +368,8 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      load_w_frag(a.wb, C, 0, H, t, f);
+      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      else load_w_frag(a.wb, C, 0, H, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ab[rb], x[rb][t], f);
     }
@@ -1938,12 +2001,30 @@ int check_triatt(const odde_triatt_args* a) {
   return ODDE_OK;
 }
 
+// ODDE_TRIATT_PROJ_F32_PLAIN=1: the fp32 projection without staged weights
+// (tuning).
+inline bool triatt_proj_f32_plain() {
+  static const bool v = [] {
+    const char* e = getenv("ODDE_TRIATT_PROJ_F32_PLAIN");
+    return e && atoi(e) != 0;
+  }();
+  return v;
+}
 template <typename ZT, typename CT, int kC, bool kX3Mul = false>
 void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st) {
   // fp32 weights are read from L2 per fragment: more rows i per wave as
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
   // large enough (n >= 256)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 8 ? 2 : 1;
+  if constexpr (sizeof(CT) == 4 && !kX3Mul && kC <= 4) {
+    // true fp32 products from n = 256: the weights staged in LDS
+    if (n >= 256 && !triatt_proj_f32_plain()) {
+      dim3 grid(jp / 64, (n + 1) / 2);
+      hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, 2, false, true>), grid, dim3(256), 0, st,
+                         p);
+      return;
+    }
+  }
   if (kRB > 1 && n >= 256) {
     const int rows = (n + kRB - 1) / kRB;
     dim3 grid(jp / 64, rows, proj_split((int64_t)(jp / 64) * rows, p.heads));

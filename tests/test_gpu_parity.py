@@ -37,9 +37,11 @@ def _z(n, c, seed, dtype=torch.float32):
 # ---------------------------------------------------------------- attention
 
 
-@pytest.mark.parametrize("n", [17, 64, 130])
+@pytest.mark.parametrize("n", [17, 64, 130, 300])
 @pytest.mark.parametrize("starting", [True, False])
 def test_triangle_attention_fp32(n, starting):
+    # from n = 256 the projection stages its weights in LDS (n = 300: a
+    # padded grid of 320)
     mod = seeded(TriangleAttention(128, 32, 4, starting=starting), 100 + n, STD)
     z = _z(n, 128, n)
     mask = token_pair_mask(n, max(1, n // 10))
