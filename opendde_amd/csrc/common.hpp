@@ -422,6 +422,18 @@ __device__ __forceinline__ void load_w_frag(const float* __restrict__ w_split, i
   }
 }
 
+// A weight fragment from a weight row staged in LDS with the global row's
+// bytes: fp32 (8 floats at k = 32 t + 8 g) or three-part (the row's 2 ld
+// bf16, hi then lo, as load_w_frag reads them from the split weights).
+__device__ __forceinline__ void staged_w_frag(const float* row, int ld, int t, Frag<float>& f) {
+  (void)ld;
+  f.load(row + 32 * t + 8 * (lane_id() >> 4));
+}
+__device__ __forceinline__ void staged_w_frag(const float* row, int ld, int t, FragX3& f) {
+  const bf16* p = reinterpret_cast<const bf16*>(row) + 32 * t + 8 * (lane_id() >> 4);
+  f.hi.load(p);
+  f.lo.load(p + ld);
+}
 // W [rows][cols] f32 -> [rows][2 cols] bf16: row r = hi = bf16(W[r][:]) to
 // nearest, then lo = bf16(W[r][:] - hi).  With kPerm32 the columns are
 // permuted within each block of 32, column 16 s + 4 q + e to 8 q + 4 s + e,

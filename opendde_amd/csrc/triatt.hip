@@ -166,14 +166,15 @@ struct TriattProjArgs {
 // and the gate (small grids); z = 0 also writes the mask outputs and the
 // triangle bias.
 // kX3Mul (f32 compute, ODDE_F32X3): products in three bf16 parts.
-// kStage (true fp32 products, one split): the weight rows of each 16-channel
-// block -- W_q, W_k, W_g, then W_v, then the H bias rows -- are staged in
-// LDS, double-buffered, and shared by the workgroup's 4 waves.
+// kStage (f32 data, one split): the weight rows of each 16-channel block --
+// W_q, W_k, W_g, then W_v, then the H bias rows -- are staged in LDS
+// (fp32 rows, or the three-part split rows: the same bytes), double-
+// buffered, and shared by the workgroup's 4 waves.
 template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3Mul = false, bool kStage = false>
 __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
   using MF = MulFrag<CT, kX3Mul>;
-  static_assert(!kStage || (sizeof(CT) == 4 && !kX3Mul), "staging: true fp32 products");
+  static_assert(!kStage || sizeof(CT) == 4, "staging: f32 weights");
   constexpr int WL = C + 4;                     // staged row stride (floats)
   constexpr int CHUNK = 3 * 16 * WL;            // three 16-row slots
   constexpr int PT = 3 * 16 * C / 4;            // 16-byte pieces per chunk
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
     __syncthreads();
     ++cur;
   };
-  auto wslot = [&](int sl) { return wsm + (cur & 1) * CHUNK + (sl * 16 + r16) * WL + 8 * g; };
+  auto wslot = [&](int sl) { return wsm + (cur & 1) * CHUNK + (sl * 16 + r16) * WL; };
 
   // mask rows: additive form for the exact core, keep flags for the fast one
   __shared__ float keep_s[kRB][64];
@@ -294,15 +295,15 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      if constexpr (kStage) staged_w_frag(wslot(0), C, t, f);
       else load_w_frag(a.wq, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(aq[rb], f, x[rb][t]);
-      if constexpr (kStage) f.load(wslot(1) + 32 * t);
+      if constexpr (kStage) staged_w_frag(wslot(1), C, t, f);
       else load_w_frag(a.wk, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ak[rb], f, x[rb][t]);
-      if constexpr (kStage) f.load(wslot(2) + 32 * t);
+      if constexpr (kStage) staged_w_frag(wslot(2), C, t, f);
       else load_w_frag(a.wg, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], f, x[rb][t]);
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      if constexpr (kStage) staged_w_frag(wslot(0), C, t, f);
       else load_w_frag(a.wv, C, ob * 16, HD, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(av[rb], x[rb][t], f);
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(256) void triatt_proj_kernel(TriattProjArgs<ZT, CT>
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      if constexpr (kStage) f.load(wslot(0) + 32 * t);
+      if constexpr (kStage) staged_w_frag(wslot(0), C, t, f);
       else load_w_frag(a.wb, C, 0, H, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ab[rb], x[rb][t], f);
@@ -2016,11 +2017,11 @@ void launch_proj(const TriattProjArgs<ZT, CT>& p, int n, int jp, hipStream_t st)
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
   // large enough (n >= 256)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 8 ? 2 : 1;
-  if constexpr (sizeof(CT) == 4 && !kX3Mul && kC <= 4) {
-    // true fp32 products from n = 256: the weights staged in LDS
+  if constexpr (sizeof(CT) == 4 && kC <= 4) {
+    // f32 data from n = 256: the weights staged in LDS
     if (n >= 256 && !triatt_proj_f32_plain()) {
       dim3 grid(jp / 64, (n + 1) / 2);
-      hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, 2, false, true>), grid, dim3(256), 0, st,
+      hipLaunchKernelGGL((triatt_proj_kernel<ZT, CT, kC, 2, kX3Mul, true>), grid, dim3(256), 0, st,
                          p);
       return;
     }

@@ -55,16 +55,17 @@ struct TrimulProjArgs {
 // for the three-part contraction.  kX3Mul (f32 compute, ODDE_F32X3): the
 // projections' products in three bf16 parts (rows split once after the
 // LayerNorm, weight fragments as they are read).  blockIdx.z of gridDim.z
-// takes channels [z Ch / Z, (z + 1) Ch / Z) (small grids).  kStage (true
-// fp32 products): the four weight rows blocks of each 16-channel block are
-// staged in LDS, double-buffered, and shared by the workgroup's 4 waves, so
-// a weight byte fetched from L2 serves 64 kRB rows instead of 16 kRB.
+// takes channels [z Ch / Z, (z + 1) Ch / Z) (small grids).  kStage (f32
+// data): the four weight row blocks of each 16-channel block (fp32 rows, or
+// the three-part split rows: the same bytes) are staged in LDS, double-
+// buffered, and shared by the workgroup's 4 waves, so a weight byte fetched
+// from L2 serves 64 kRB rows instead of 16 kRB.
 template <typename ZT, typename CT, int kC, int kRB = 1, bool kX3 = false, bool kX3Mul = false,
           bool kStage = false>
 __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT> a) {
   constexpr int C = kC * 32;
   using MF = MulFrag<CT, kX3Mul>;
-  static_assert(!kStage || (sizeof(CT) == 4 && !kX3 && !kX3Mul), "staging: true fp32 products");
+  static_assert(!kStage || sizeof(CT) == 4, "staging: f32 weights");
   constexpr int WL = C + 4;                     // staged row stride (floats)
   constexpr int CHUNK = 4 * 16 * WL;            // a_p, a_g, b_p, b_g rows of one block
   constexpr int PT = 4 * 16 * C / 4;            // 16-byte pieces per chunk
@@ -135,23 +136,23 @@ __global__ __launch_bounds__(256) void trimul_proj_kernel(TrimulProjArgs<ZT, CT>
     f32x4 ap[kRB], ag[kRB], bp[kRB], bg[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) ap[rb] = ag[rb] = bp[rb] = bg[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const float* wsb = wsm + ((cb - cb_lo) & 1) * CHUNK + r16 * WL + 8 * g;
+    const float* wsb = wsm + ((cb - cb_lo) & 1) * CHUNK + r16 * WL;
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
       MF f;
-      if constexpr (kStage) f.load(wsb + 32 * t);
+      if constexpr (kStage) staged_w_frag(wsb, C, t, f);
       else load_w_frag(a.wp, C, cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ap[rb], xf[rb][t], f);
-      if constexpr (kStage) f.load(wsb + 16 * WL + 32 * t);
+      if constexpr (kStage) staged_w_frag(wsb + 16 * WL, C, t, f);
       else load_w_frag(a.wg, C, cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(ag[rb], xf[rb][t], f);
-      if constexpr (kStage) f.load(wsb + 32 * WL + 32 * t);
+      if constexpr (kStage) staged_w_frag(wsb + 32 * WL, C, t, f);
       else load_w_frag(a.wp, C, ch + cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(bp[rb], xf[rb][t], f);
-      if constexpr (kStage) f.load(wsb + 48 * WL + 32 * t);
+      if constexpr (kStage) staged_w_frag(wsb + 48 * WL, C, t, f);
       else load_w_frag(a.wg, C, ch + cb * 16, 2 * ch, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(bg[rb], xf[rb][t], f);
@@ -604,14 +605,16 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(TrimulOutArgs<ZT, CT> a
   }
 }
 
-// True fp32 products with W_z and W_g staged in LDS, 16 output channels at
-// a time, shared by the workgroup's 4 waves: every weight byte fetched from
-// L2 serves the workgroup's 64 rows instead of one wave's 16.  Chunks are
+// f32 data with W_z and W_g staged in LDS (fp32 rows, or with kX3Mul the
+// three-part split rows: the same bytes), 16 output channels at a time,
+// shared by the workgroup's 4 waves: every weight byte fetched from L2
+// serves the workgroup's 64 rows instead of one wave's 16.  Chunks are
 // double-buffered (the next one waits in registers while the current one is
 // multiplied), one barrier per chunk.  One first index x per workgroup, as
 // trimul_out_kernel; the arithmetic per output is the same.
-template <typename ZT, int kC, int kCh>
+template <typename ZT, int kC, int kCh, bool kX3Mul = false>
 __global__ __launch_bounds__(256) void trimul_out_f32s_kernel(TrimulOutArgs<ZT, float> a) {
+  using MF = MulFrag<float, kX3Mul>;
   constexpr int C = kC * 32, CH = kCh * 32, NCB = C / 16;
   constexpr int LD = CH + 4;                    // row stride of the transposed P tile
   constexpr int WLZ = CH + 4, WLG = C + 4;      // staged W_z / W_g row strides (floats)
@@ -669,26 +672,33 @@ __global__ __launch_bounds__(256) void trimul_out_f32s_kernel(TrimulOutArgs<ZT, 
   const int w = wave_id(), l = lane_id(), g = l >> 4, r16 = l & 15;
   const int yl = y0 + w * 16 + r16;
   const bool valid = x_ < a.n && yl < a.n;
-  Frag<float> xp[kCh], xz[kC];
+  MF xp[kCh], xz[kC];
   const ZT* zrow = a.z + (int64_t)(valid ? x_ : 0) * a.z_s0 + (int64_t)(valid ? yl : 0) * a.z_s1;
-  ln_rows_to_frags<float, float, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b,
-                                     a.eps, xp);
-  ln_rows_to_frags<ZT, float, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, xz);
+  {
+    Frag<float> tp[kCh], tz[kC];
+    ln_rows_to_frags<float, float, CH>(&pt[(w * 16 + r16) * LD], true, a.ln_out_w, a.ln_out_b,
+                                       a.eps, tp);
+    ln_rows_to_frags<ZT, float, C>(zrow, valid, a.ln_in_w, a.ln_in_b, a.eps, tz);
+#pragma unroll
+    for (int t = 0; t < kCh; ++t) to_mul(tp[t], xp[t]);
+#pragma unroll
+    for (int t = 0; t < kC; ++t) to_mul(tz[t], xz[t]);
+  }
 
   for (int cb = 0; cb < NCB; ++cb) {
-    const float* wz_s = wsm[cb & 1] + r16 * WLZ + 8 * g;
-    const float* wg_s = wsm[cb & 1] + 16 * WLZ + r16 * WLG + 8 * g;
+    const float* wz_s = wsm[cb & 1] + r16 * WLZ;
+    const float* wg_s = wsm[cb & 1] + 16 * WLZ + r16 * WLG;
     f32x4 ay = {0.f, 0.f, 0.f, 0.f}, agt = ay;
 #pragma unroll
     for (int t = 0; t < kCh; ++t) {
-      Frag<float> f;
-      f.load(wz_s + 32 * t);
+      MF f;
+      staged_w_frag(wz_s, CH, t, f);
       mma(ay, f, xp[t]);
     }
 #pragma unroll
     for (int t = 0; t < kC; ++t) {
-      Frag<float> f;
-      f.load(wg_s + 32 * t);
+      MF f;
+      staged_w_frag(wg_s, C, t, f);
       mma(agt, f, xz[t]);
     }
     if (valid) {
@@ -1334,13 +1344,13 @@ void launch_tp(const TrimulProjArgs<ZT, CT>& p, hipStream_t st) {
   // registers allow (4 up to C = 128, 2 at C = 256), once the grid stays
   // large enough (np >= 256: np^2 / 256 workgroups and more)
   constexpr int kRB = sizeof(CT) != 4 ? 1 : kC <= 4 ? 4 : kC <= 8 ? 2 : 1;
-  if constexpr (sizeof(CT) == 4 && !kX3Out && !kX3Mul && kC <= 4) {
-    // true fp32 products from Np = 256: the weights staged in LDS (kSRB row
-    // blocks per wave)
+  if constexpr (sizeof(CT) == 4 && kC <= 4) {
+    // f32 data from Np = 256: the weights staged in LDS (kSRB row blocks
+    // per wave)
     if (p.np >= 256 && !trimul_proj_f32_plain()) {
       dim3 grid(p.np / 64, p.np / kSRB);
-      hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kSRB, false, false, true>), grid, dim3(256),
-                         0, st, p);
+      hipLaunchKernelGGL((trimul_proj_kernel<ZT, CT, kC, kSRB, kX3Out, kX3Mul, true>), grid,
+                         dim3(256), 0, st, p);
       return;
     }
   }
@@ -1427,13 +1437,22 @@ template <typename ZT, typename CT, int kC, int kCh>
 void launch_to(const TrimulOutArgs<ZT, CT>& p, bool x3, hipStream_t st) {
   if constexpr (sizeof(CT) == 4) {
     if (x3) {
-      // three-part products: two first indices per workgroup share each
-      // weight fragment read from L2 (C = Ch = 128 at N = 1024: 1.24 -> 1.17
-      // ms).  With true fp32 products the shared form needs 256 VGPRs, one
-      // wave per SIMD, and is slower (1.21 -> 1.57 ms), so it keeps one.
-      constexpr int kRB = kC <= 4 && kCh <= 4 ? 2 : 1;
-      if (kRB > 1 && p.n >= 256) launch_to_rb<ZT, CT, kC, kCh, true, kRB>(p, st);
-      else launch_to_rb<ZT, CT, kC, kCh, true, 1>(p, st);
+      // three-part products: the weights staged in LDS from N = 256 (C =
+      // Ch = 128 at N = 1024: 1.24 -> 1.17 ms with two first indices per
+      // workgroup sharing each L2 fragment read, which the staged form
+      // replaces)
+      if constexpr (kC <= 4 && kCh <= 4) {
+        if (p.n >= 256 && !trimul_out_f32_plain()) {
+          hipLaunchKernelGGL((trimul_out_f32s_kernel<ZT, kC, kCh, true>), dim3(p.np / 64, p.n),
+                             dim3(256), 0, st, p);
+          return;
+        }
+        if (p.n >= 256) {
+          launch_to_rb<ZT, CT, kC, kCh, true, 2>(p, st);
+          return;
+        }
+      }
+      launch_to_rb<ZT, CT, kC, kCh, true, 1>(p, st);
       return;
     }
   }
