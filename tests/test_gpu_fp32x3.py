@@ -64,6 +64,18 @@ def test_three_part_core_matches_fp32_oracle(c, h, starting, n, monkeypatch):
     where the weights are scaled up so that logits reach tens of nats (c 384,
     12 heads), at least 8x closer to it than the reference's own TF32 mode
     (the oracle with its core's matmul operands rounded to TF32)."""
+    _check_three_part_attention(c, h, starting, n, monkeypatch)
+
+
+@pytest.mark.parametrize("c,h,starting", [(128, 4, True), (64, 2, True), (128, 2, False),
+                                          (64, 4, False)])
+def test_three_part_staged_projection_matches_fp32_oracle(c, h, starting, monkeypatch):
+    """n = 260: the projection reads its split weights through LDS staging
+    (from n = 256), for C of 64 and 128 and heads x 32 of 64 and 128."""
+    _check_three_part_attention(c, h, starting, 260, monkeypatch)
+
+
+def _check_three_part_attention(c, h, starting, n, monkeypatch):
     say(f"[gpu] three-part core c={c} h={h} n={n} start={starting}")
     mod = seeded(TriangleAttention(c, 32, h, starting=starting), 900 + c + h + n, STD)
     z = torch.randn(n, n, c, generator=torch.Generator().manual_seed(n + c))
@@ -152,12 +164,15 @@ _orig_combine = ref.combine_projections
 
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("n,c,ch", [(256, 128, 128), (250, 64, 128), (512, 128, 128),
-                                    (300, 128, 128)])
+                                    (300, 128, 128), (260, 64, 64), (260, 128, 64),
+                                    (260, 64, 128)])
 def test_three_part_contraction_matches_fp32_oracle(outgoing, n, c, ch, monkeypatch):
     """fp32 triangle multiplication with TF32 allowed: the projections' and
     the output's products in three bf16 parts, the contraction's too where Np
     (n rounded up to 128) is a multiple of 256 (n 250, 256, 512), true fp32
-    contraction products otherwise (n 300: Np 384).  Within the fp32 tier's
+    contraction products otherwise (n 260 and 300: Np 384).  From n = 256
+    the projection and the output stage their split weights in LDS (n 260:
+    C and Ch of 64 and 128).  Within the fp32 tier's
     bar of the fp32 oracle, or at least 8x closer to it than the reference's
     TF32 mode (the oracle with the contraction's operands rounded to TF32)."""
     from opendde_amd.triangular import (TriangleMultiplicationIncoming,

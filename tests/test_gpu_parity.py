@@ -192,6 +192,34 @@ def test_triangle_multiplication_channel_shapes(c, ch):
     assert_fp32(got, exp, f"trimul c={c} ch={ch}")
 
 
+@pytest.mark.parametrize("c,ch", [(64, 64), (64, 128), (128, 64)])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_staged_weights_fp32(c, ch, outgoing):
+    # n = 260 (from 256 the fp32 projection and output stage their weights
+    # in LDS): C and Ch of 64 and 128
+    n = 260
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = seeded(cls(c, ch), 650 + c + ch, STD)
+    z = _z(n, c, c + ch + 1)
+    mask = token_pair_mask(n, 13, seed=n, random=True)
+    exp = ref.triangle_multiplication(z, mask, params_of(mod), outgoing)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_multiplicative="hip")
+    assert_fp32(got, exp, f"trimul staged n={n} c={c} ch={ch} out={outgoing}")
+
+
+@pytest.mark.parametrize("c,h", [(64, 2), (128, 2), (64, 4)])
+def test_triangle_attention_staged_weights_fp32(c, h):
+    # n = 260: the fp32 projection stages its weights in LDS, for C of 64
+    # and 128 and heads x 32 of 64 and 128
+    n = 260
+    mod = seeded(TriangleAttention(c, 32, h), 310 + c + h, STD)
+    z = _z(n, c, c + h)
+    mask = token_pair_mask(n, 13, seed=n + 1, random=True)
+    exp = ref.triangle_attention(z, mask, params_of(mod), h)
+    got = mod.to(DEV)(z.to(DEV), mask.to(DEV), triangle_attention="hip")
+    assert_fp32(got, exp, f"triatt staged n={n} c={c} h={h}")
+
+
 @pytest.mark.parametrize("c,ch", [(384, 384), (256, 256), (128, 256), (384, 64)])
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("n", [40, 130])
