@@ -1407,11 +1407,19 @@ struct TriattOutArgs {
 // kRB consecutive rows i per workgroup: every weight fragment a wave reads
 // from L2 serves kRB row blocks (the fp32 form reads W_o per fragment).
 // blockIdx.z of gridDim.z takes output channels [z C / Z, (z + 1) C / Z)
-// (small grids).
-template <typename ZT, typename CT, int kHD, bool kX3Mul = false, int kRB = 1>
+// (small grids).  kStage (f32 data): W_o rows of each 16-channel block
+// (fp32 rows, or the three-part split rows: the same bytes) staged in LDS,
+// double-buffered, shared by the workgroup's 4 waves.
+template <typename ZT, typename CT, int kHD, bool kX3Mul = false, int kRB = 1, bool kStage = false>
 __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a) {
   constexpr int HD = kHD * 32;
   using MF = MulFrag<CT, kX3Mul>;
+  static_assert(!kStage || sizeof(CT) == 4, "staging: f32 weights");
+  constexpr int WL = HD + 4;                    // staged row stride (floats)
+  constexpr int CHUNK = 16 * WL;
+  constexpr int PT = 16 * HD / 4;               // 16-byte pieces per chunk
+  constexpr int PPT = (PT + 255) / 256;
+  __shared__ __attribute__((aligned(16))) float wsm[kStage ? 2 * CHUNK : 4];
   const int i0 = blockIdx.y * kRB;
   const int w = wave_id(), g = lane_id() >> 4, r16 = lane_id() & 15;
   const int jl = blockIdx.x * 64 + w * 16 + r16;
@@ -1427,14 +1435,40 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
     }
   }
   const int cb_per = (a.c / 16) / (int)gridDim.z;
-  for (int cb = (int)blockIdx.z * cb_per; cb < ((int)blockIdx.z + 1) * cb_per; ++cb) {
+  const int cb_lo = (int)blockIdx.z * cb_per, cb_hi = cb_lo + cb_per;
+  f32x4 wreg[kStage ? PPT : 1];
+  auto wload = [&](int cb) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k, r = q / (HD / 4), c4 = q % (HD / 4);
+      if (PT % 256 == 0 || q < PT)
+        wreg[k] = *reinterpret_cast<const f32x4*>(a.wo + (size_t)(cb * 16 + r) * HD + 4 * c4);
+    }
+  };
+  auto wstore = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int q = (int)threadIdx.x + 256 * k, r = q / (HD / 4), c4 = q % (HD / 4);
+      if (PT % 256 == 0 || q < PT)
+        *reinterpret_cast<f32x4*>(&wsm[buf * CHUNK + r * WL + 4 * c4]) = wreg[k];
+    }
+  };
+  if constexpr (kStage) {
+    wload(cb_lo);
+    wstore(0);
+    if (cb_lo + 1 < cb_hi) wload(cb_lo + 1);
+    __syncthreads();
+  }
+  for (int cb = cb_lo; cb < cb_hi; ++cb) {
     f32x4 acc[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* wrow = wsm + ((cb - cb_lo) & 1) * CHUNK + (lane_id() & 15) * WL;
 #pragma unroll
     for (int t = 0; t < kHD; ++t) {
       MF f;
-      load_w_frag(a.wo, HD, cb * 16, a.c, t, f);
+      if constexpr (kStage) staged_w_frag(wrow, HD, t, f);
+      else load_w_frag(a.wo, HD, cb * 16, a.c, t, f);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) mma(acc[rb], f, x[rb][t]);
     }
@@ -1447,6 +1481,15 @@ __global__ __launch_bounds__(256) void triatt_out_kernel(TriattOutArgs<ZT, CT> a
       if (a.add) load4(a.res + (int64_t)i * a.r_s0 + (int64_t)jl * a.r_s1 + c0, base);
       store4(a.out + (int64_t)i * a.o_s0 + (int64_t)jl * a.o_s1 + c0, base[0] + acc[rb][0],
              base[1] + acc[rb][1], base[2] + acc[rb][2], base[3] + acc[rb][3]);
+    }
+    if constexpr (kStage) {
+      // buffer (cb + 1 - cb_lo) & 1 was last read in block cb - 1, before
+      // the barrier that ended it
+      if (cb + 1 < cb_hi) {
+        wstore((cb + 1 - cb_lo) & 1);
+        if (cb + 2 < cb_hi) wload(cb + 2);
+      }
+      __syncthreads();
     }
   }
 }
@@ -2102,6 +2145,15 @@ bool launch_out_ws(const TriattOutArgs<ZT, CT>& p, int HD, int C, int n, int jp,
   }
 }
 
+// ODDE_TRIATT_OUT_F32_PLAIN=1: the fp32 output kernel without staged
+// weights (tuning).
+inline bool triatt_out_f32_plain() {
+  static const bool v = [] {
+    const char* e = getenv("ODDE_TRIATT_OUT_F32_PLAIN");
+    return e && atoi(e) != 0;
+  }();
+  return v;
+}
 template <typename ZT, typename CT, int kHD>
 void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStream_t st) {
   // fp32: W_o is read from L2 per fragment, so 4 rows i per workgroup up to
@@ -2110,6 +2162,17 @@ void launch_out(const TriattOutArgs<ZT, CT>& p, int n, int jp, bool x3, hipStrea
   if constexpr (kRB > 1) {
     if (n >= 256) {
       const int rows = (n + kRB - 1) / kRB;
+      if (kHD <= 4 && !triatt_out_f32_plain()) {
+        // f32 data: W_o staged in LDS (one split)
+        dim3 grid(jp / 64, rows);
+        if (x3)
+          hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true, kRB, true>), grid, dim3(256), 0,
+                             st, p);
+        else
+          hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, false, kRB, true>), grid, dim3(256), 0,
+                             st, p);
+        return;
+      }
       dim3 grid(jp / 64, rows, proj_split((int64_t)(jp / 64) * rows, p.c / 16));
       if (x3)
         hipLaunchKernelGGL((triatt_out_kernel<ZT, CT, kHD, true, kRB>), grid, dim3(256), 0, st, p);
